@@ -1,0 +1,205 @@
+"""Decode-attention throughput of the fused paged path on one MI355X.
+
+Workload (one "step" = one decode step of one layer over the whole batch): Qwen2.5-0.5B
+attention geometry (14 query heads, 2 KV heads, head_dim 64, fp16, 32-token blocks), batch 8,
+contexts drawn uniform in [1024, 32768] from a seed, each sequence keeping its 64 most recent
+blocks in HBM and the rest in pinned host RAM (recent_only placement). Every step appends one
+token per sequence, streams the host blocks, attends, and evicts the block that leaves the
+resident window. Synthetic N(0,1)*0.5 data. Prints one JSON line.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "rust-llm-pager_amd"))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
+LINK_PEAK_GBS = 64.0  # PCIe Gen5 x16 per direction
+MIB16 = 16 * 1024 * 1024
+
+CFG = dict(batch=8, hq=14, hkv=2, d=64, tpb=32, ctx_lo=1024, ctx_hi=32768, resident_blocks=64, seed=2)
+
+
+def draw_contexts(seed, batch, lo, hi):
+    import torch
+
+    g = torch.Generator().manual_seed(seed)
+    return torch.randint(lo, hi + 1, (batch,), generator=g).tolist()
+
+
+def build(steps_total):
+    import torch
+
+    from pager_hf import PagedDecoder
+
+    c = CFG
+    ctx = draw_contexts(c["seed"], c["batch"], c["ctx_lo"], c["ctx_hi"])
+    dec = PagedDecoder(
+        num_layers=1, num_query_heads=c["hq"], num_kv_heads=c["hkv"], head_dim=c["d"], tokens_per_block=c["tpb"],
+        dtype=torch.float16, device="cuda", pool_blocks=c["batch"] * (c["resident_blocks"] + 4),
+        host_blocks=sum(n // c["tpb"] + steps_total // c["tpb"] + 8 for n in ctx), staging_blocks=2048,
+    )
+    gen = torch.Generator(device="cuda").manual_seed(c["seed"])
+    sids = []
+    for n in ctx:
+        sid = dec.add_session(capacity_tokens=n + steps_total + 64, vram_budget=c["resident_blocks"] * MIB16,
+                              ram_budget=1 << 40, recent_window=c["resident_blocks"] - 1, policy="recent_only")
+        k = (torch.randn(1, c["hkv"], n, c["d"], device="cuda", generator=gen) * 0.5).half()
+        v = (torch.randn(1, c["hkv"], n, c["d"], device="cuda", generator=gen) * 0.5).half()
+        dec.prefill(sid, [k], [v], n)
+        del k, v
+        sids.append(sid)
+    S = c["batch"]
+    q = (torch.randn(steps_total, S, c["hq"], c["d"], device="cuda", generator=gen) * 0.5).half()
+    kn = (torch.randn(steps_total, S, c["hkv"], c["d"], device="cuda", generator=gen) * 0.5).half()
+    vn = (torch.randn(steps_total, S, c["hkv"], c["d"], device="cuda", generator=gen) * 0.5).half()
+    out = torch.empty(S, c["hq"], c["d"], dtype=torch.float16, device="cuda")
+    torch.cuda.synchronize()
+    return dec, sids, ctx, q, kn, vn, out
+
+
+def run_steps(dec, sids, q, kn, vn, out, first, count, stats):
+    for i in range(first, first + count):
+        dec.begin_step(sids)
+        st = dec.pool.step_stats()
+        stats["resident_tokens"] += st["resident_tokens"]
+        stats["host_tokens"] += st["host_tokens"]
+        stats["copies"] += st["copies"]
+        stats["launches"] += st["launches"]
+        dec.decode_layer(0, q[i], kn[i], vn[i], out)
+        dec.end_step()
+
+
+def cpu_baseline(ctx, budget_s=15.0):
+    """Times the oracle's fp32 dense attention on the host over a bounded sample of the same
+    workload (whole steps of the batch, upcast included); returns KV GB/s and tokens/s."""
+    import numpy as np
+
+    from oracle.attention import dense_reference
+
+    c = CFG
+    rng = np.random.default_rng(0)
+    kv = [((rng.standard_normal((1, c["hkv"], n + 1, c["d"])) * 0.5).astype(np.float16),
+           (rng.standard_normal((1, c["hkv"], n + 1, c["d"])) * 0.5).astype(np.float16)) for n in ctx]
+    q = (rng.standard_normal((1, c["hq"], c["d"])) * 0.5).astype(np.float16)
+    bytes_per_step = sum((n + 1) * 2 * c["hkv"] * c["d"] * 2 for n in ctx)
+    steps = 0
+    t0 = time.perf_counter()
+    while True:
+        for k, v in kv:
+            dense_reference(q.astype(np.float32), k.astype(np.float32), v.astype(np.float32),
+                            n_rep=c["hq"] // c["hkv"], tokens_per_block=c["tpb"])
+        steps += 1
+        if time.perf_counter() - t0 > budget_s or steps >= 50:
+            break
+    dt = time.perf_counter() - t0
+    return {
+        "value": round(bytes_per_step * steps / dt / 1e9, 3),
+        "unit": "GB/s",
+        "tokens_per_s": round(c["batch"] * steps / dt, 2),
+        "cores": 1,
+        "kind": "port",
+        "sample": f"{steps} full decode steps of the batch-8 workload (dense fp32 numpy oracle, fp16->fp32 upcast "
+                  f"included), {dt:.1f} s",
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=128)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1).", file=sys.stderr)
+        return 2
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        return 2
+    c = CFG
+    total = args.warmup + args.steps
+    dec, sids, ctx, q, kn, vn, out = build(total)
+    warm = {"resident_tokens": 0, "host_tokens": 0, "copies": 0, "launches": 0}
+    run_steps(dec, sids, q, kn, vn, out, 0, args.warmup, warm)
+    torch.cuda.synchronize()
+    dec.pool.sync()
+    dec.pool.kernel_time()  # discard warmup timings
+    dec.pool.set_timing(True)
+    stats = {"resident_tokens": 0, "host_tokens": 0, "copies": 0, "launches": 0}
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    run_steps(dec, sids, q, kn, vn, out, args.warmup, args.steps, stats)
+    torch.cuda.synchronize()
+    dec.pool.sync()
+    dt = time.perf_counter() - t0
+    k_ms, k_launches, k_bytes = dec.pool.kernel_time()
+
+    tok_bytes = 2 * c["hkv"] * c["d"] * 2  # K + V per token per layer
+    io_bytes = args.steps * c["batch"] * c["hq"] * c["d"] * 2 * 2  # q in + out
+    hbm_bytes = stats["resident_tokens"] * tok_bytes + io_bytes
+    host_bytes = stats["host_tokens"] * tok_bytes
+    value = (hbm_bytes + host_bytes) / dt / 1e9
+    kernel_gbs = k_bytes / (k_ms / 1e3) / 1e9 if k_ms > 0 else 0.0
+    link_gbs = host_bytes / dt / 1e9
+    line = {
+        "metric": "decode-attn KV GB/s (HBM + host link, % peak) & tokens/s, 32k ctx",
+        "value": round(value, 3),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dt / args.steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic N(0,1)*0.5, seeded",
+        "config": {
+            "workload": "single-layer streaming decode attention, Qwen2.5-0.5B geometry (14q/2kv, d64, fp16), "
+                        "batch 8, contexts U[1024,32768] seed 2, 32-token blocks, 64 recent blocks per sequence in "
+                        "HBM and the rest in pinned host RAM, 1 token appended per sequence per step",
+            "contexts": ctx,
+            "batch": c["batch"],
+        },
+        "tokens_per_s": round(c["batch"] * args.steps / dt, 2),
+        "host_link": {
+            "achieved": round(link_gbs, 3),
+            "peak": LINK_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(link_gbs / LINK_PEAK_GBS, 4),
+            "bytes_per_step": host_bytes // args.steps,
+            "copies_per_step": stats["copies"] / args.steps,
+        },
+        "hbm_resident": {"bytes_per_step": hbm_bytes // args.steps},
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "paged_attn_kernel",
+            "achieved": round(kernel_gbs, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(kernel_gbs / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "launches": k_launches,
+            "avg_launch_us": round(k_ms * 1e3 / max(k_launches, 1), 3),
+            "bytes_per_launch": k_bytes // max(k_launches, 1),
+        },
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(ctx, args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,233 @@
+/*
+ * pgr.h -- C ABI of the MI355X decode-attention library (libpgr.so).
+ *
+ * Plain pointers, sizes and status codes only. Device pointers are HIP device addresses,
+ * host pointers of the KV store are pinned memory owned by the store, `stream` is a
+ * hipStream_t passed as void* (NULL = the default stream). Every call is asynchronous on
+ * `stream` unless stated otherwise. Functions returning int return PGR_OK (0) or a negative
+ * PGR_ERR_* code; pgr_last_error() then describes the failure (thread-local).
+ *
+ * Citations name the reference interface each entry point replaces (paths are relative to
+ * the reference repository 3xecut0r/rust-llm-pager).
+ */
+#ifndef PGR_H_
+#define PGR_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PGR_OK 0
+#define PGR_ERR_INVALID (-1)
+#define PGR_ERR_UNSUPPORTED (-2)
+#define PGR_ERR_HIP (-3)
+#define PGR_ERR_CAPACITY (-4)
+#define PGR_ERR_STATE (-5)
+#define PGR_ERR_KEY (-6)
+#define PGR_ERR_BUDGET (-7)
+
+#define PGR_DTYPE_F16 0
+#define PGR_DTYPE_BF16 1
+#define PGR_DTYPE_F32 2 /* pgr_attn_finalize output only */
+
+/* ---- library ------------------------------------------------------------------------- */
+
+/* ABI version of this header (increments on incompatible change). */
+int pgr_abi_version(void);
+/* Message of the last failing call on this thread ("" if none). */
+const char* pgr_last_error(void);
+
+/* ---- decode attention operator API --------------------------------------------------
+ * Shapes follow pager_hf/streaming_attention.py: q [B, Hq, D]; k, v [B, Hkv, Tc, D]
+ * contiguous; valid [B, Tc] int32 0/1 or NULL (all valid); active [B] int32 or NULL (all
+ * active); online-softmax state m, l [B, Hq] and acc [B, Hq, D] fp32, updated in place.
+ * D in {32, 64, 128}; Hq / Hkv <= 16; scale > 0; softcap <= 0 disables softcapping.
+ * `workspace` must hold pgr_attn_workspace_bytes(...) bytes of device memory.
+ */
+#define PGR_MODE_FOLD 0
+#define PGR_MODE_STATS 1
+#define PGR_MODE_ACCUMULATE 2
+#define PGR_MODE_FOLD_FIXED 3
+
+size_t pgr_attn_workspace_bytes(int64_t batch, int64_t num_query_heads, int64_t num_kv_heads, int64_t tokens,
+                                int64_t head_dim, int mode, int64_t tokens_per_block);
+
+/* Fold one KV chunk into (m, l, acc).
+ * Replaces streaming_attention_step, pager_hf/streaming_attention.py:452-513
+ * (kernel :77-185). */
+int pgr_attn_step(const void* q, const void* k, const void* v, const int32_t* valid, const int32_t* active, float* m,
+                  float* l, float* acc, int64_t batch, int64_t num_query_heads, int64_t num_kv_heads, int64_t tokens,
+                  int64_t head_dim, int dtype, float scale, float softcap, void* workspace, size_t workspace_bytes,
+                  void* stream);
+
+/* Fold one chunk's K into (m, l) only.
+ * Replaces streaming_attention_stats_step, pager_hf/streaming_attention.py:516-560
+ * (kernel :188-261). */
+int pgr_attn_stats_step(const void* q, const void* k, const int32_t* valid, const int32_t* active, float* m, float* l,
+                        int64_t batch, int64_t num_query_heads, int64_t num_kv_heads, int64_t tokens, int64_t head_dim,
+                        int dtype, float scale, float softcap, void* workspace, size_t workspace_bytes, void* stream);
+
+/* With final (m, l): acc += P.V and block_mass[b, h, block_id_offset + j] = sum(p)/l per
+ * tokens_per_block tile j (tokens_per_block a multiple of 16; block_mass [B, Hq, max_blocks]).
+ * Replaces streaming_attention_accumulate_step, pager_hf/streaming_attention.py:563-621
+ * (kernel :264-352). */
+int pgr_attn_accumulate_step(const void* q, const void* k, const void* v, const int32_t* valid, const int32_t* active,
+                             const float* m, const float* l, float* acc, float* block_mass, int64_t max_blocks,
+                             int64_t block_id_offset, int64_t tokens_per_block, int64_t batch,
+                             int64_t num_query_heads, int64_t num_kv_heads, int64_t tokens, int64_t head_dim,
+                             int dtype, float scale, float softcap, void* workspace, size_t workspace_bytes,
+                             void* stream);
+
+/* With final (m, l): acc += P.V for a non-block chunk (the tail); no mass, no active.
+ * Replaces streaming_attention_fold_fixed_step, pager_hf/streaming_attention.py:624-665
+ * (kernel :355-430). */
+int pgr_attn_fold_fixed_step(const void* q, const void* k, const void* v, const int32_t* valid, const float* m,
+                             const float* l, float* acc, int64_t batch, int64_t num_query_heads, int64_t num_kv_heads,
+                             int64_t tokens, int64_t head_dim, int dtype, float scale, float softcap, void* workspace,
+                             size_t workspace_bytes, void* stream);
+
+/* out[r, :] = (acc[r, :] / l[r]) rounded to dtype, for rows = B * Hq.
+ * Replaces streaming_attention_finalize, pager_hf/streaming_attention.py:668-670. */
+int pgr_attn_finalize(const float* acc, const float* l, void* out, int64_t rows, int64_t head_dim, int dtype,
+                      void* stream);
+
+/* ---- placement policy ----------------------------------------------------------------
+ * Restatement of the Rust pager. Handles are opaque; not thread-safe per handle. */
+typedef struct pgr_pager_metrics_s {
+  uint64_t tokens;
+  uint64_t vram_peak;
+  uint64_t ram_peak;
+  uint64_t swap_vram_ram;
+  uint64_t swap_ram_ssd;
+  double attention_mass_total;
+  double attention_mass_vram;
+} pgr_pager_metrics_t;
+
+/* Replaces PyPager::new, pager/src/lib.rs:16-46 (core.rs:63-85). */
+void* pgr_pager_new(uint64_t vram, uint64_t ram, uint64_t recent, uint64_t rebalance_interval, float promote_margin,
+                    float ram_promote_margin, const char* policy);
+/* Frees a pager handle (PyO3 object drop). */
+void pgr_pager_free(void* pager);
+/* Replaces PyPager::on_step, lib.rs:48-50 (core.rs:87-98). PGR_ERR_STATE when a rebalance
+ * check divides by a zero rebalance_interval (the Rust code panics there). */
+int pgr_pager_on_step(void* pager, uint64_t token_idx, uint32_t layer, const float* attention, size_t n);
+/* Replaces PyPager::force_rebalance, lib.rs:52-54 (core.rs:100-107). */
+int pgr_pager_force_rebalance(void* pager, uint64_t token_idx);
+/* Number of blocks the pager tracks (length of tiers()). */
+size_t pgr_pager_num_blocks(void* pager);
+/* Replaces PyPager::tiers, lib.rs:60-62 (core.rs:113-122): writes min(cap, n) tiers, returns n. */
+size_t pgr_pager_tiers(void* pager, uint8_t* out, size_t cap);
+/* Replaces PyPager::vram_block_ids, lib.rs:64-66 (core.rs:124-130): writes min(cap, n), returns n. */
+size_t pgr_pager_vram_block_ids(void* pager, uint64_t* out, size_t cap);
+/* Replaces PyPager::metrics, lib.rs:56-58 (metrics.rs:4-27). */
+int pgr_pager_metrics(void* pager, pgr_pager_metrics_t* out);
+
+/* ---- paged KV store and fused decode -------------------------------------------------
+ * One store holds the KV cache of many sessions (a session = rows sharing one placement)
+ * for num_layers layers: an HBM slot pool per layer, a pinned host mirror per layer, and
+ * an HBM staging ring for host-to-device streaming. */
+typedef struct pgr_kv_config_s {
+  int32_t num_layers;
+  int32_t kv_heads;
+  int32_t query_heads;
+  int32_t head_dim;
+  int32_t tokens_per_block; /* multiple of 16 */
+  int32_t dtype;
+  int64_t pool_slots;       /* HBM records (block x row) per layer */
+  int64_t host_records;     /* pinned host records per layer */
+  int64_t staging_slots;    /* records per staging buffer */
+  int32_t staging_buffers;  /* ring depth, >= 1 (2 = double buffering) */
+  int32_t blocks_per_workgroup;
+} pgr_kv_config_t;
+
+typedef struct pgr_kv_stats_s {
+  uint64_t gpu_to_cpu_bytes, cpu_to_gpu_bytes, gpu_to_cpu_copies, cpu_to_gpu_copies;
+  double gpu_to_cpu_sec, cpu_to_gpu_sec;
+  uint64_t evict_bytes_copied, load_bytes_copied, stream_bytes, stream_copies;
+} pgr_kv_stats_t;
+
+typedef struct pgr_kv_step_stats_s {
+  int64_t resident_tokens, host_tokens, host_blocks, copies, chunks, launches, work_items;
+} pgr_kv_step_stats_t;
+
+/* Creates a store (allocates HBM pools, pinned host mirror, staging). NULL on failure.
+ * Replaces KVBlockStore.__init__, pager_hf/kv_block_store.py:41-56. */
+void* pgr_kv_create(const pgr_kv_config_t* cfg);
+void pgr_kv_destroy(void* kv);
+/* New session with `rows` sequences and room for capacity_tokens tokens; lo_per_row = first
+ * valid token per row (left padding), NULL = 0. Returns the session id (>= 0). */
+int pgr_kv_add_session(void* kv, int32_t rows, int64_t capacity_tokens, const int32_t* lo_per_row);
+int pgr_kv_remove_session(void* kv, int32_t sid);
+/* Sliding window / padding: first valid token per row. Replaces the padding and window mask
+ * fold of paged_model.py:964-982 (valid iff col > pos - window). */
+int pgr_kv_set_lo(void* kv, int32_t sid, const int32_t* lo_per_row);
+/* Declares the length of an empty session (prefill); full blocks start host-side. */
+int pgr_kv_set_length(void* kv, int32_t sid, int64_t n_tokens);
+/* Writes tokens [0, n_tokens) of (sid, row, layer) from k, v [Hkv, n_src, D] (device).
+ * Replaces _build_initial_store + real_past_to_blocks, paged_model.py:1183-1192 and
+ * kv_utils.py:38-61. Synchronous. */
+int pgr_kv_import(void* kv, int32_t sid, int32_t row, int32_t layer, const void* k, const void* v, int64_t n_src,
+                  int64_t n_tokens, void* stream);
+/* Reads tokens [0, n_tokens) back into k, v [Hkv, n_tokens, D]. Synchronous.
+ * Replaces reconstruct_past_from_store, kv_utils.py:112-178. */
+int pgr_kv_export(void* kv, int32_t sid, int32_t row, int32_t layer, void* k, void* v, int64_t n_tokens, void* stream);
+/* Registers block `block_id` (== current length / T, length block-aligned) from the reference
+ * block layout key, value [L, B, T, Hkv, D] (device). Replaces KVBlockStore.put_gpu,
+ * kv_block_store.py:58-67. */
+int pgr_kv_put_block(void* kv, int32_t sid, int64_t block_id, const void* key, const void* value, void* stream);
+/* Copies block `block_id` out in the reference layout [L, B, T, Hkv, D] (device), wherever it
+ * lives, without moving it. Replaces KVBlockStore.get_any / get_gpu, kv_block_store.py:256-274.
+ * Synchronous. */
+int pgr_kv_get_block(void* kv, int32_t sid, int64_t block_id, void* key, void* value, void* stream);
+/* Moves full blocks to the tier the pager assigned (0 = HBM, else host; ids >= n_tiers ->
+ * host), ascending by id; writes moved ids. PGR_ERR_BUDGET with *fail_block when an
+ * offload would exceed the RAM budget (earlier moves stay done).
+ * Replaces KVBlockStore.apply_tiers, kv_block_store.py:206-227 (offload :75-131, load :133-163). */
+int pgr_kv_apply_tiers(void* kv, int32_t sid, const uint8_t* tiers, int64_t n_tiers, int64_t* to_gpu, int64_t* n_gpu,
+                       int64_t* to_cpu, int64_t* n_cpu, int64_t* fail_block, void* stream);
+/* RAM budget in bytes over all sessions (< 0: unlimited). kv_block_store.py:83-108. */
+int pgr_kv_set_ram_budget(void* kv, int64_t bytes);
+/* Opens a decode step over sessions sids[0..n): their rows, in order, are the sequences
+ * (rows of q / k_new / v_new / out) of every decode_layer call of this step. */
+int pgr_kv_begin_step(void* kv, const int32_t* sids, int32_t n, void* stream);
+/* One layer of the step: appends k_new/v_new [S, Hkv, D] at each sequence's next position,
+ * folds every in-scope block (HBM in place, host blocks streamed), writes out [S, Hq, D]
+ * and, if mass_accum != NULL, adds the per-block attention mass (mean over the session's
+ * rows and query heads) into mass_accum[session_in_step * accum_stride + block].
+ * Replaces the patched layer forward's gather + fold loop, paged_model.py:926-1086
+ * (gather :878-924, tail append :955, mass :1041-1048). */
+int pgr_kv_decode_layer(void* kv, int32_t layer, const void* q, const void* k_new, const void* v_new, void* out,
+                        float* mass_accum, int64_t accum_stride, float scale, float softcap, void* stream);
+/* Closes the step: every session grows by one token; sessions whose open block became full
+ * are written to completed[] (the new block id is then length / T - 1).
+ * Replaces _append_new_full_blocks_from_grown_tail, paged_model.py:1210-1233. */
+int pgr_kv_end_step(void* kv, int32_t* completed, int32_t* n_completed);
+/* info[4] = {n_tokens, n_full_blocks, gpu_blocks, cpu_blocks}. */
+int pgr_kv_session_info(void* kv, int32_t sid, int64_t* info);
+/* Ascending full-block ids on HBM (gpu != 0) or host. Returns the count.
+ * Replaces KVBlockStore.gpu_block_ids / cpu_block_ids, kv_block_store.py:185-189. */
+int pgr_kv_block_ids(void* kv, int32_t sid, int32_t gpu, int64_t* out, int64_t cap);
+/* Host-resident in-scope block ids streamed for sequence `seq` of the open step (ascending).
+ * The gather index list of paged_model.py:907-916. Returns the count. */
+int pgr_kv_step_host_blocks(void* kv, int32_t seq, int64_t* out, int64_t cap);
+int pgr_kv_step_stats(void* kv, pgr_kv_step_stats_t* out);
+/* Replaces KVBlockStore.stats / summary, kv_block_store.py:16-23, 191-204. */
+int pgr_kv_stats(void* kv, pgr_kv_stats_t* out);
+/* Replaces resident_gpu_bytes / resident_cpu_bytes, kv_block_store.py:179-183. */
+int pgr_kv_resident_bytes(void* kv, int64_t* gpu, int64_t* cpu);
+/* Bytes of one block of session sid over all layers and rows (kv_nbytes of a reference block). */
+int pgr_kv_block_bytes(void* kv, int32_t sid, int64_t* bytes);
+/* Event timing of the attention launches (for measurement). */
+int pgr_kv_set_timing(void* kv, int32_t on);
+int pgr_kv_kernel_time(void* kv, double* ms, int64_t* launches, int64_t* bytes);
+/* Waits for all work of the store (both streams). */
+int pgr_kv_sync(void* kv);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PGR_H_ */

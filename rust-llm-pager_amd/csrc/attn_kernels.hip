@@ -1,0 +1,769 @@
+// Single-token GQA decode attention for CDNA4 (gfx950).
+//
+// Every kernel here computes, for one batch row and one KV head, the attention of the
+// n_rep query heads that share that KV head (heads kv*n_rep .. kv*n_rep+n_rep-1, the
+// repeat-interleave grouping of pager_hf/streaming_attention.py:119-123) over a range of
+// KV tokens, with fp32 online-softmax state.
+//
+// MFMA mapping (v_mfma_f32_16x16x16 f16/bf16, fp32 accumulate). A 16-token tile is folded as
+//     S^T[16 tok x 16 heads] = K[16 tok x D] . Q^T[D x 16 heads]
+//     O^T[D x 16 heads]     += V^T[D x 16 tok] . P^T[16 tok x 16 heads]
+// Lane l = 16*g + n holds S^T rows 4g..4g+3 (four tokens) of column n (query head n).
+// That register block is exactly the P^T operand of the second product, and every O^T
+// value a lane holds belongs to head n as well, so the softmax state (m, l) and the
+// rescale factor are per-lane scalars: no cross-lane traffic inside the tile except the
+// max over the four lane groups g. Columns n >= n_rep are zero-query padding and are
+// never stored (the reference pads its M tile the same way, streaming_attention.py:55).
+//
+// Operand layouts (verified on gfx950 with a probe): A[i][k]: lane i + 16*(k/4), element
+// k%4; B[k][j]: lane j + 16*(k/4), element k%4; C[i][j]: lane j + 16*(i/4), element i%4.
+// The contraction index of S^T (head_dim) is permuted so that lane (g, n) reads one
+// contiguous run of D/4 elements of K row n: chunk c, k-slot 4g+i <-> dim (D/4)g + 4c + i.
+// V is read as four token rows of D/16 contiguous elements (dims (D/16)n .. +D/16) and
+// transposed in registers with v_perm_b32 into the A operand of each of the D/16 M-tiles;
+// M-tile j, row r <-> dim (D/16)r + j. All global loads are 16/8/4-byte per lane and cover
+// whole 128-byte rows per instruction.
+//
+// P is rounded to the K/V element type before the P.V product, as the reference does
+// (streaming_attention.py:178, :347, :428).
+#include <hip/hip_runtime.h>
+
+#include "pgr_common.h"
+#include "pgr_kernels.h"
+
+namespace pgr {
+namespace {
+
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr float kNegInf = -__builtin_inff();
+
+struct F16 {
+  static __device__ __forceinline__ f32x4 mma(u32x2 a, u32x2 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a), __builtin_bit_cast(f16x4, b), c, 0, 0,
+                                                 0);
+  }
+  static __device__ __forceinline__ uint32_t pack(float x, float y) {
+    f16x2 h = {(_Float16)x, (_Float16)y};
+    return __builtin_bit_cast(uint32_t, h);
+  }
+  static __device__ __forceinline__ uint16_t cvt(float x) { return __builtin_bit_cast(uint16_t, (_Float16)x); }
+};
+
+struct BF16 {
+  static __device__ __forceinline__ f32x4 mma(u32x2 a, u32x2 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, a), __builtin_bit_cast(i16x4, b), c, 0,
+                                                     0, 0);
+  }
+  static __device__ __forceinline__ uint32_t pack(float x, float y) {
+    bf16x2 h = {(__bf16)x, (__bf16)y};
+    return __builtin_bit_cast(uint32_t, h);
+  }
+  static __device__ __forceinline__ uint16_t cvt(float x) { return __builtin_bit_cast(uint16_t, (__bf16)x); }
+};
+
+__device__ __forceinline__ float wave_max_g(float x) {
+  x = fmaxf(x, __shfl_xor(x, 16));
+  return fmaxf(x, __shfl_xor(x, 32));
+}
+__device__ __forceinline__ float wave_sum_g(float x) {
+  x += __shfl_xor(x, 16);
+  return x + __shfl_xor(x, 32);
+}
+
+// Registers of one 16-token tile held by one lane.
+template <int D>
+struct Tile {
+  static_assert(D == 32 || D == 64 || D == 128, "head_dim must be 32, 64 or 128");
+  static constexpr int KV4 = D / 32;  // u32x4 of K per lane (D/4 elements)
+  static constexpr int VW = D / 32;   // dwords of V per token row per lane (D/16 elements)
+  u32x4 k[KV4];
+  uint32_t v[4][VW];
+};
+
+// K row `row` of the tile at `tile_k` (row stride D elements): elements (D/4)g .. +D/4.
+template <int D>
+__device__ __forceinline__ void load_k(Tile<D>& t, const uint16_t* tile_k, int row, int g) {
+  const u32x4* p = reinterpret_cast<const u32x4*>(tile_k + (size_t)row * D + (D / 4) * g);
+#pragma unroll
+  for (int i = 0; i < Tile<D>::KV4; ++i) t.k[i] = p[i];
+}
+
+// V rows rows[0..3] at `tile_v`: elements (D/16)n .. +D/16 of each.
+template <int D>
+__device__ __forceinline__ void load_v(Tile<D>& t, const uint16_t* tile_v, const int (&rows)[4], int n) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint16_t* p = tile_v + (size_t)rows[i] * D + (D / 16) * n;
+    if constexpr (D == 32) {
+      t.v[i][0] = *reinterpret_cast<const uint32_t*>(p);
+    } else if constexpr (D == 64) {
+      u32x2 x = *reinterpret_cast<const u32x2*>(p);
+      t.v[i][0] = x.x;
+      t.v[i][1] = x.y;
+    } else {
+      u32x4 x = *reinterpret_cast<const u32x4*>(p);
+      t.v[i][0] = x.x;
+      t.v[i][1] = x.y;
+      t.v[i][2] = x.z;
+      t.v[i][3] = x.w;
+    }
+  }
+}
+
+template <int D>
+__device__ __forceinline__ void zero_v_row(Tile<D>& t, int i) {
+#pragma unroll
+  for (int w = 0; w < Tile<D>::VW; ++w) t.v[i][w] = 0u;
+}
+
+// K operand (A of S^T) for contraction chunk c: dwords 2c, 2c+1 of the lane's K run.
+template <int D>
+__device__ __forceinline__ u32x2 k_chunk(const u32x4 (&k)[D / 32], int c) {
+  const u32x4 q = k[c >> 1];
+  return (c & 1) ? u32x2{q.z, q.w} : u32x2{q.x, q.y};
+}
+
+// V^T operand (A of O^T) for M-tile j: element j of each of the four token rows.
+template <int D>
+__device__ __forceinline__ u32x2 v_tile(const uint32_t (&v)[4][D / 32], int j) {
+  const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
+  const int w = j >> 1;
+  return u32x2{__builtin_amdgcn_perm(v[1][w], v[0][w], sel), __builtin_amdgcn_perm(v[3][w], v[2][w], sel)};
+}
+
+// S^T tile of 16 tokens x 16 heads.
+template <class Ty, int D>
+__device__ __forceinline__ f32x4 qk_tile(const Tile<D>& t, const u32x4 (&q)[D / 32]) {
+  f32x4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int c = 0; c < D / 16; ++c) s = Ty::mma(k_chunk<D>(t.k, c), k_chunk<D>(q, c), s);
+  return s;
+}
+
+template <class Ty, int D>
+__device__ __forceinline__ void pv_tile(f32x4 (&acc)[D / 16], const Tile<D>& t, const float (&p)[4]) {
+  const u32x2 pb = {Ty::pack(p[0], p[1]), Ty::pack(p[2], p[3])};
+#pragma unroll
+  for (int j = 0; j < D / 16; ++j) acc[j] = Ty::mma(v_tile<D>(t.v, j), pb, acc[j]);
+}
+
+// Scale + optional softcap of one raw score (streaming_attention.py:158-160).
+__device__ __forceinline__ float transform_score(float s, float scale, float softcap) {
+  s = s * scale;
+  if (softcap > 0.f) s = softcap * tanhf(s / softcap);
+  return s;
+}
+
+// Dims held by lane (g, n) for O^T M-tile j, element i: (D/4)g + (D/16)i + j.
+template <int D>
+__device__ __forceinline__ int acc_dim(int g, int i, int j) {
+  return (D / 4) * g + (D / 16) * i + j;
+}
+
+// Q^T operand for query head (row index `qrow` of a [rows, D] array); zero for padding heads.
+template <int D>
+__device__ __forceinline__ void load_q(u32x4 (&q)[D / 32], const uint16_t* qptr, bool real, int g) {
+#pragma unroll
+  for (int i = 0; i < D / 32; ++i) q[i] = u32x4{0u, 0u, 0u, 0u};
+  if (real) {
+    const u32x4* p = reinterpret_cast<const u32x4*>(qptr + (D / 4) * g);
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i) q[i] = p[i];
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// Workgroup merge of the four waves' (m, l, acc) and store of one partial slot.
+// FOLD: online-softmax partials; FIXED: plain acc sums (m is the caller's fixed max).
+template <int D>
+struct MergeSmem {
+  float m[kWaves][kMaxRep];
+  float l[kWaves][kMaxRep];
+  float acc[kWaves][kMaxRep][D + 1];
+};
+
+template <int D, bool kFold, bool kWithAcc>
+__device__ __forceinline__ void wg_merge_store(MergeSmem<D>& sm, int wave, int g, int n, float m_run, float l_lane,
+                                               const f32x4 (&acc)[D / 16], int n_rep, float* pm, float* pl,
+                                               float* pacc) {
+  const float l_wave = wave_sum_g(l_lane);
+  if (g == 0) {
+    sm.m[wave][n] = m_run;
+    sm.l[wave][n] = l_wave;
+  }
+  if constexpr (kWithAcc) {
+#pragma unroll
+    for (int j = 0; j < D / 16; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sm.acc[wave][n][acc_dim<D>(g, i, j)] = acc[j][i];
+  }
+  __syncthreads();
+  const int tid = threadIdx.x;
+  if (tid < n_rep) {
+    const int r = tid;
+    if constexpr (kFold) {
+      float mw = kNegInf;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) mw = fmaxf(mw, sm.m[w][r]);
+      float lw = 0.f;
+      if (mw != kNegInf) {
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) lw += sm.l[w][r] * __expf(sm.m[w][r] - mw);
+      }
+      pm[r] = mw;
+      pl[r] = lw;
+    }
+  }
+  if constexpr (kWithAcc) {
+    for (int idx = tid; idx < n_rep * D; idx += kWaves * kWaveSize) {
+      const int r = idx / D, d = idx - r * D;
+      float a = 0.f;
+      if constexpr (kFold) {
+        float mw = kNegInf;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) mw = fmaxf(mw, sm.m[w][r]);
+        if (mw != kNegInf) {
+#pragma unroll
+          for (int w = 0; w < kWaves; ++w) a += sm.acc[w][r][d] * __expf(sm.m[w][r] - mw);
+        }
+      } else {
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) a += sm.acc[w][r][d];
+      }
+      pacc[idx] = a;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// Dense chunk kernel: the operator API of pager_hf/streaming_attention.py:452-665.
+// k, v: [B, Hkv, Tc, D] contiguous. Grid (n_split, Hkv, B); each wave folds
+// `wave_tokens` consecutive tokens, the workgroup covers 4 * wave_tokens.
+enum DenseMode : int { kModeFold = 0, kModeStats = 1, kModeAccumulate = 2, kModeFoldFixed = 3 };
+
+struct DenseArgs {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  const int32_t* valid;   // [B, Tc] or null (all valid)
+  const int32_t* active;  // [B] or null (all active)
+  const float* m_in;      // FIXED modes: final m [B, Hq]
+  const float* l_in;      // FIXED modes: final l [B, Hq]
+  float* block_mass;      // accumulate: [B, Hq, max_blocks]
+  float* pm;              // partials [slot][n_rep]
+  float* pl;
+  float* pacc;            // [slot][n_rep][D]
+  int tc, hq, hkv, n_rep, n_split, wave_tokens;
+  int tokens_per_block, max_blocks, block_id_offset;
+  float scale, softcap;
+};
+
+template <class Ty, int D, int kMode>
+__global__ __launch_bounds__(256) void dense_attn_kernel(DenseArgs a) {
+  constexpr bool kFold = (kMode == kModeFold || kMode == kModeStats);
+  constexpr bool kWithV = (kMode != kModeStats);
+  constexpr bool kMass = (kMode == kModeAccumulate);
+  __shared__ MergeSmem<D> sm;
+
+  const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  if (a.active != nullptr && a.active[b] == 0) return;  // whole workgroup: uniform exit
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int g = lane >> 4, n = lane & 15;
+  const bool real = n < a.n_rep;
+  const int qh = h * a.n_rep + (real ? n : 0);
+
+  const size_t kv_base = ((size_t)b * a.hkv + h) * (size_t)a.tc * D;
+  const uint16_t* kp = a.k + kv_base;
+  const uint16_t* vp = a.v + kv_base;
+
+  u32x4 q[D / 32];
+  load_q<D>(q, a.q + ((size_t)b * a.hq + qh) * D, real, g);
+
+  float m_run = kNegInf, l_run = 0.f;
+  float m_fix = 0.f, l_fix = 1.f;
+  if constexpr (!kFold) {
+    if (real) {
+      m_fix = a.m_in[(size_t)b * a.hq + qh];
+      l_fix = a.l_in[(size_t)b * a.hq + qh];
+    }
+  }
+  f32x4 acc[D / 16];
+#pragma unroll
+  for (int j = 0; j < D / 16; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int t_begin = split * kWaves * a.wave_tokens + wave * a.wave_tokens;
+  const int t_end = min(t_begin + a.wave_tokens, a.tc);
+  const int tiles = t_begin < t_end ? (t_end - t_begin + 15) / 16 : 0;
+  const int tiles_per_block = kMass ? a.tokens_per_block / 16 : 1;
+  float blk = 0.f;
+
+  for (int ti = 0; ti < tiles; ++ti) {
+    const int t0 = t_begin + ti * 16;
+    Tile<D> t;
+    load_k<D>(t, kp, min(t0 + n, a.tc - 1), g);
+    int rows[4];
+    bool ok[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int tok = t0 + 4 * g + i;
+      ok[i] = tok < t_end;
+      if (ok[i] && a.valid != nullptr) ok[i] = a.valid[(size_t)b * a.tc + tok] != 0;
+      rows[i] = min(tok, a.tc - 1);
+    }
+    if constexpr (kWithV) {
+      load_v<D>(t, vp, rows, n);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (!ok[i]) zero_v_row<D>(t, i);
+    }
+    const f32x4 s4 = qk_tile<Ty, D>(t, q);
+    float s[4], p[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s[i] = ok[i] ? transform_score(s4[i], a.scale, a.softcap) : kNegInf;
+
+    if constexpr (kFold) {
+      const float tmax = wave_max_g(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])));
+      const float m_new = fmaxf(m_run, tmax);
+      const bool empty = (m_new == kNegInf);
+      const float alpha = empty ? 0.f : __expf(m_run - m_new);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) p[i] = empty ? 0.f : __expf(s[i] - m_new);
+      l_run = l_run * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
+      if constexpr (kWithV) {
+#pragma unroll
+        for (int j = 0; j < D / 16; ++j) acc[j] *= alpha;
+        pv_tile<Ty, D>(acc, t, p);
+      }
+      m_run = m_new;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) p[i] = ok[i] ? __expf(s[i] - m_fix) : 0.f;
+      pv_tile<Ty, D>(acc, t, p);
+      if constexpr (kMass) {
+        blk += (p[0] + p[1]) + (p[2] + p[3]);
+        if ((ti + 1) % tiles_per_block == 0 || ti + 1 == tiles) {
+          const float bs = wave_sum_g(blk);
+          if (g == 0 && real) {
+            const int j = (t0 - 0) / a.tokens_per_block;
+            a.block_mass[((size_t)b * a.hq + qh) * a.max_blocks + a.block_id_offset + j] = bs / l_fix;
+          }
+          blk = 0.f;
+        }
+      }
+    }
+  }
+
+  const size_t slot = ((size_t)b * a.hkv + h) * a.n_split + split;
+  wg_merge_store<D, kFold, kWithV>(sm, wave, g, n, m_run, l_run, acc, a.n_rep, a.pm + slot * a.n_rep,
+                                   a.pl + slot * a.n_rep, a.pacc + slot * a.n_rep * D);
+}
+
+// Combine the dense partials into the caller's running state, in place.
+template <int kMode>
+__global__ __launch_bounds__(64) void dense_merge_kernel(DenseArgs a, float* m, float* l, float* acc, int d) {
+  const int row = blockIdx.x;  // b * hq + qh
+  const int b = row / a.hq, qh = row - b * a.hq;
+  if (a.active != nullptr && a.active[b] == 0) return;
+  const int h = qh / a.n_rep, r = qh - h * a.n_rep;
+  const size_t slot0 = ((size_t)b * a.hkv + h) * a.n_split;
+  const int lane = threadIdx.x;
+  if constexpr (kMode == kModeFold || kMode == kModeStats) {
+    const float m0 = m[row];
+    float mf = m0;
+    for (int s = 0; s < a.n_split; ++s) mf = fmaxf(mf, a.pm[(slot0 + s) * a.n_rep + r]);
+    if (mf == kNegInf) return;  // nothing valid anywhere yet: the state stays as it is
+    const float w0 = __expf(m0 - mf);
+    float lf = l[row] * w0;
+    for (int s = 0; s < a.n_split; ++s) {
+      const float ms = a.pm[(slot0 + s) * a.n_rep + r];
+      lf += a.pl[(slot0 + s) * a.n_rep + r] * __expf(ms - mf);
+    }
+    if constexpr (kMode == kModeFold) {
+      for (int dd = lane; dd < d; dd += 64) {
+        float x = acc[(size_t)row * d + dd] * w0;
+        for (int s = 0; s < a.n_split; ++s) {
+          const float ms = a.pm[(slot0 + s) * a.n_rep + r];
+          x += a.pacc[((slot0 + s) * a.n_rep + r) * d + dd] * __expf(ms - mf);
+        }
+        acc[(size_t)row * d + dd] = x;
+      }
+    }
+    __syncthreads();
+    if (lane == 0) {
+      m[row] = mf;
+      l[row] = lf;
+    }
+  } else {
+    for (int dd = lane; dd < d; dd += 64) {
+      float x = acc[(size_t)row * d + dd];
+      for (int s = 0; s < a.n_split; ++s) x += a.pacc[((slot0 + s) * a.n_rep + r) * d + dd];
+      acc[(size_t)row * d + dd] = x;
+    }
+  }
+}
+
+template <class Ty>
+__global__ void finalize_kernel(const float* acc, const float* l, uint16_t* out, int rows, int d) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (size_t)rows * d) return;
+  out[i] = Ty::cvt(acc[i] / l[i / d]);
+}
+
+__global__ void finalize_f32_kernel(const float* acc, const float* l, float* out, int rows, int d) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (size_t)rows * d) return;
+  out[i] = acc[i] / l[i / d];
+}
+
+// ---------------------------------------------------------------------------------------
+// Paged kernel: the fused decode path. Blocks are read in place from the layer's HBM
+// pool or from a staging buffer filled by host-to-device copies; record layout per
+// (block, sequence): K [Hkv][T][D] then V [Hkv][T][D]. Grid (n_work, Hkv).
+struct PagedArgs {
+  const uint16_t* q;     // [S, Hq, D]
+  const uint16_t* pool;  // layer pool base
+  const uint16_t* stage; // staging base
+  const WorkItem* work;
+  const BlockEntry* entries;
+  const SeqInfo* seqs;
+  float* pm;             // [slot][Hq]
+  float* pl;
+  float* pacc;           // [slot][Hq][D]
+  float* mass_m;         // [S][Hq][mass_stride] (null: no mass)
+  float* mass_s;
+  int hq, hkv, n_rep, tokens_per_block, mass_stride;
+  float scale, softcap;
+};
+
+template <class Ty, int D, bool kMass>
+__global__ __launch_bounds__(256) void paged_attn_kernel(PagedArgs a) {
+  __shared__ MergeSmem<D> sm;
+  const WorkItem wi = a.work[blockIdx.x];
+  const int h = blockIdx.y;
+  const SeqInfo si = a.seqs[wi.seq];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int g = lane >> 4, n = lane & 15;
+  const bool real = n < a.n_rep;
+  const int qh = h * a.n_rep + (real ? n : 0);
+  const int T = a.tokens_per_block;
+  const int tiles_per_block = T >> 4;
+  const size_t rec = (size_t)2 * a.hkv * T * D;  // elements per record
+  const size_t head_off = (size_t)h * T * D;
+  const size_t v_off = (size_t)a.hkv * T * D;
+
+  u32x4 q[D / 32];
+  load_q<D>(q, a.q + ((size_t)wi.seq * a.hq + qh) * D, real, g);
+
+  float m_run = kNegInf, l_run = 0.f, blk = 0.f;
+  f32x4 acc[D / 16];
+#pragma unroll
+  for (int j = 0; j < D / 16; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int my_blocks = wi.entry_count > wave ? (wi.entry_count - wave + kWaves - 1) / kWaves : 0;
+  const int tiles = my_blocks * tiles_per_block;
+  for (int ti = 0; ti < tiles; ++ti) {
+    const int e = ti / tiles_per_block, tb = ti - e * tiles_per_block;
+    const BlockEntry be = a.entries[wi.entry_begin + wave + kWaves * e];
+    const uint16_t* base = be.slot >= 0 ? a.pool + (size_t)be.slot * rec : a.stage + (size_t)(-be.slot - 1) * rec;
+    const uint16_t* kt = base + head_off + (size_t)tb * 16 * D;
+    const uint16_t* vt = base + v_off + head_off + (size_t)tb * 16 * D;
+    const int t0 = be.block_id * T + tb * 16;
+    Tile<D> t;
+    load_k<D>(t, kt, n, g);
+    const int rows[4] = {4 * g, 4 * g + 1, 4 * g + 2, 4 * g + 3};
+    load_v<D>(t, vt, rows, n);
+    bool ok[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int tok = t0 + 4 * g + i;
+      ok[i] = tok >= si.lo && tok < si.hi;
+      if (!ok[i]) zero_v_row<D>(t, i);
+    }
+    const f32x4 s4 = qk_tile<Ty, D>(t, q);
+    float s[4], p[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s[i] = ok[i] ? transform_score(s4[i], a.scale, a.softcap) : kNegInf;
+    const float tmax = wave_max_g(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])));
+    const float m_new = fmaxf(m_run, tmax);
+    const bool empty = (m_new == kNegInf);
+    const float alpha = empty ? 0.f : __expf(m_run - m_new);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) p[i] = empty ? 0.f : __expf(s[i] - m_new);
+    const float psum = (p[0] + p[1]) + (p[2] + p[3]);
+    l_run = l_run * alpha + psum;
+#pragma unroll
+    for (int j = 0; j < D / 16; ++j) acc[j] *= alpha;
+    pv_tile<Ty, D>(acc, t, p);
+    m_run = m_new;
+    if constexpr (kMass) {
+      blk = blk * alpha + psum;
+      if (tb == tiles_per_block - 1) {
+        const float bs = wave_sum_g(blk);
+        if (g == 0 && real && be.block_id < si.n_mass) {
+          const size_t mi = ((size_t)wi.seq * a.hq + qh) * a.mass_stride + be.block_id;
+          a.mass_m[mi] = m_run;
+          a.mass_s[mi] = bs;
+        }
+        blk = 0.f;
+      }
+    }
+  }
+
+  const size_t slot = (size_t)wi.partial;
+  wg_merge_store<D, true, true>(sm, wave, g, n, m_run, l_run, acc, a.n_rep, a.pm + slot * a.hq + h * a.n_rep,
+                                a.pl + slot * a.hq + h * a.n_rep, a.pacc + (slot * a.hq + h * a.n_rep) * D);
+}
+
+// Per (sequence, query head): combine the partial slots, write the output in the element
+// type and the final (m, l) for the mass pass. One wave per row.
+template <class Ty>
+__global__ __launch_bounds__(64) void paged_merge_kernel(const SeqInfo* seqs, const float* pm, const float* pl,
+                                                         const float* pacc, uint16_t* out, float* mf_out,
+                                                         float* lf_out, float* acc_out, int hq, int d) {
+  const int row = blockIdx.x;
+  const int s = row / hq, qh = row - s * hq;
+  const SeqInfo si = seqs[s];
+  float mf = kNegInf;
+  for (int k = 0; k < si.partial_count; ++k) mf = fmaxf(mf, pm[(size_t)(si.partial_base + k) * hq + qh]);
+  float lf = 0.f;
+  if (mf != kNegInf)
+    for (int k = 0; k < si.partial_count; ++k) {
+      const size_t pi = (size_t)(si.partial_base + k) * hq + qh;
+      lf += pl[pi] * __expf(pm[pi] - mf);
+    }
+  for (int dd = threadIdx.x; dd < d; dd += 64) {
+    float x = 0.f;
+    if (mf != kNegInf)
+      for (int k = 0; k < si.partial_count; ++k) {
+        const size_t pi = (size_t)(si.partial_base + k) * hq + qh;
+        x += pacc[pi * d + dd] * __expf(pm[pi] - mf);
+      }
+    out[(size_t)row * d + dd] = Ty::cvt(x / lf);
+    if (acc_out != nullptr) acc_out[(size_t)row * d + dd] = x;
+  }
+  if (threadIdx.x == 0) {
+    mf_out[row] = mf;
+    lf_out[row] = lf;
+  }
+}
+
+// Per (session, block): mean over the session's rows and all query heads of
+// s_b * exp(m_b - m_final) / l_final, added into the session's mass accumulator
+// (paged_model.py:1041-1048 per layer).
+__global__ void mass_reduce_kernel(const SeqInfo* seqs, const int32_t* session_rows, const int32_t* session_first,
+                                   const float* mass_m, const float* mass_s, const float* mf, const float* lf,
+                                   float* mass_accum, int accum_stride, int hq, int mass_stride, int n_sessions,
+                                   int max_blocks) {
+  const int sess = blockIdx.y;
+  const int blk = blockIdx.x * blockDim.x + threadIdx.x;
+  if (sess >= n_sessions) return;
+  const int first = session_first[sess], rows = session_rows[sess];
+  const SeqInfo si0 = seqs[first];
+  if (blk >= si0.n_mass || blk >= max_blocks) return;
+  float total = 0.f;
+  for (int r = 0; r < rows; ++r) {
+    const SeqInfo si = seqs[first + r];
+    if (blk < si.mass_lo) continue;  // out of scope for this row: mass 0
+    for (int qh = 0; qh < hq; ++qh) {
+      const size_t row = (size_t)(first + r) * hq + qh;
+      const size_t mi = row * mass_stride + blk;
+      total += mass_s[mi] * __expf(mass_m[mi] - mf[row]) / lf[row];
+    }
+  }
+  mass_accum[(size_t)sess * accum_stride + blk] += total / (float)(rows * hq);
+}
+
+template <class Ty, int D>
+hipError_t launch_dense_t(const DenseArgs& a, int mode, int batch, float* m, float* l, float* acc,
+                          hipStream_t stream) {
+  dim3 grid(a.n_split, a.hkv, batch);
+  switch (mode) {
+    case kModeFold:
+      dense_attn_kernel<Ty, D, kModeFold><<<grid, 256, 0, stream>>>(a);
+      break;
+    case kModeStats:
+      dense_attn_kernel<Ty, D, kModeStats><<<grid, 256, 0, stream>>>(a);
+      break;
+    case kModeAccumulate:
+      dense_attn_kernel<Ty, D, kModeAccumulate><<<grid, 256, 0, stream>>>(a);
+      break;
+    default:
+      dense_attn_kernel<Ty, D, kModeFoldFixed><<<grid, 256, 0, stream>>>(a);
+      break;
+  }
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return err;
+  dim3 mgrid(batch * a.hq);
+  switch (mode) {
+    case kModeFold:
+      dense_merge_kernel<kModeFold><<<mgrid, 64, 0, stream>>>(a, m, l, acc, D);
+      break;
+    case kModeStats:
+      dense_merge_kernel<kModeStats><<<mgrid, 64, 0, stream>>>(a, m, l, acc, D);
+      break;
+    default:
+      dense_merge_kernel<kModeAccumulate><<<mgrid, 64, 0, stream>>>(a, m, l, acc, D);
+      break;
+  }
+  return hipGetLastError();
+}
+
+template <class Ty>
+hipError_t launch_dense_ty(const DenseArgs& a, int mode, int batch, int d, float* m, float* l, float* acc,
+                           hipStream_t stream) {
+  switch (d) {
+    case 32:
+      return launch_dense_t<Ty, 32>(a, mode, batch, m, l, acc, stream);
+    case 64:
+      return launch_dense_t<Ty, 64>(a, mode, batch, m, l, acc, stream);
+    default:
+      return launch_dense_t<Ty, 128>(a, mode, batch, m, l, acc, stream);
+  }
+}
+
+template <class Ty, int D>
+hipError_t launch_paged_t(const PagedArgs& a, int n_work, bool mass, hipStream_t stream) {
+  dim3 grid(n_work, a.hkv);
+  if (mass)
+    paged_attn_kernel<Ty, D, true><<<grid, 256, 0, stream>>>(a);
+  else
+    paged_attn_kernel<Ty, D, false><<<grid, 256, 0, stream>>>(a);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+bool head_dim_supported(int d) { return d == 32 || d == 64 || d == 128; }
+
+int dense_wave_tokens(int batch, int hkv, int tc, int tokens_per_block, bool mass) {
+  // Aim for about 2048 waves over the grid (8 per CU), each folding at least one tile.
+  const long tiles = (tc + 15) / 16;
+  const long rows = (long)batch * hkv;
+  long per_wave = (tiles * rows + 2047) / 2048;
+  if (per_wave < 1) per_wave = 1;
+  long tokens = per_wave * 16;
+  if (mass) {
+    const long tpb = tokens_per_block;
+    tokens = (tokens + tpb - 1) / tpb * tpb;
+  }
+  return (int)tokens;
+}
+
+hipError_t launch_dense(int dtype, int mode, int d, const DenseLaunch& p, hipStream_t stream) {
+  DenseArgs a;
+  a.q = static_cast<const uint16_t*>(p.q);
+  a.k = static_cast<const uint16_t*>(p.k);
+  a.v = static_cast<const uint16_t*>(p.v);
+  a.valid = p.valid;
+  a.active = p.active;
+  a.m_in = p.m;
+  a.l_in = p.l;
+  a.block_mass = p.block_mass;
+  a.pm = p.pm;
+  a.pl = p.pl;
+  a.pacc = p.pacc;
+  a.tc = p.tc;
+  a.hq = p.hq;
+  a.hkv = p.hkv;
+  a.n_rep = p.hq / p.hkv;
+  a.wave_tokens = p.wave_tokens;
+  a.n_split = p.n_split;
+  a.tokens_per_block = p.tokens_per_block;
+  a.max_blocks = p.max_blocks;
+  a.block_id_offset = p.block_id_offset;
+  a.scale = p.scale;
+  a.softcap = p.softcap;
+  if (dtype == kF16) return launch_dense_ty<F16>(a, mode, p.batch, d, p.m, p.l, p.acc, stream);
+  return launch_dense_ty<BF16>(a, mode, p.batch, d, p.m, p.l, p.acc, stream);
+}
+
+hipError_t launch_finalize(int dtype, const float* acc, const float* l, void* out, int rows, int d,
+                           hipStream_t stream) {
+  const size_t total = (size_t)rows * d;
+  if (total == 0) return hipSuccess;
+  const int threads = 256;
+  const unsigned blocks = (unsigned)((total + threads - 1) / threads);
+  if (dtype == kF16)
+    finalize_kernel<F16><<<blocks, threads, 0, stream>>>(acc, l, static_cast<uint16_t*>(out), rows, d);
+  else if (dtype == kBF16)
+    finalize_kernel<BF16><<<blocks, threads, 0, stream>>>(acc, l, static_cast<uint16_t*>(out), rows, d);
+  else
+    finalize_f32_kernel<<<blocks, threads, 0, stream>>>(acc, l, static_cast<float*>(out), rows, d);
+  return hipGetLastError();
+}
+
+hipError_t launch_paged(int dtype, int d, const PagedLaunch& p, hipStream_t stream) {
+  if (p.n_work == 0) return hipSuccess;
+  PagedArgs a;
+  a.q = static_cast<const uint16_t*>(p.q);
+  a.pool = static_cast<const uint16_t*>(p.pool);
+  a.stage = static_cast<const uint16_t*>(p.stage);
+  a.work = p.work;
+  a.entries = p.entries;
+  a.seqs = p.seqs;
+  a.pm = p.pm;
+  a.pl = p.pl;
+  a.pacc = p.pacc;
+  a.mass_m = p.mass_m;
+  a.mass_s = p.mass_s;
+  a.hq = p.hq;
+  a.hkv = p.hkv;
+  a.n_rep = p.hq / p.hkv;
+  a.tokens_per_block = p.tokens_per_block;
+  a.mass_stride = p.mass_stride;
+  a.scale = p.scale;
+  a.softcap = p.softcap;
+  const bool mass = p.mass_m != nullptr;
+  if (dtype == kF16) {
+    switch (d) {
+      case 32:
+        return launch_paged_t<F16, 32>(a, p.n_work, mass, stream);
+      case 64:
+        return launch_paged_t<F16, 64>(a, p.n_work, mass, stream);
+      default:
+        return launch_paged_t<F16, 128>(a, p.n_work, mass, stream);
+    }
+  }
+  switch (d) {
+    case 32:
+      return launch_paged_t<BF16, 32>(a, p.n_work, mass, stream);
+    case 64:
+      return launch_paged_t<BF16, 64>(a, p.n_work, mass, stream);
+    default:
+      return launch_paged_t<BF16, 128>(a, p.n_work, mass, stream);
+  }
+}
+
+hipError_t launch_paged_merge(int dtype, const SeqInfo* seqs, int n_seq, int hq, int d, const float* pm,
+                              const float* pl, const float* pacc, void* out, float* mf, float* lf, float* acc_out,
+                              hipStream_t stream) {
+  if (n_seq == 0) return hipSuccess;
+  dim3 grid(n_seq * hq);
+  if (dtype == kF16)
+    paged_merge_kernel<F16><<<grid, 64, 0, stream>>>(seqs, pm, pl, pacc, static_cast<uint16_t*>(out), mf, lf, acc_out,
+                                                     hq, d);
+  else
+    paged_merge_kernel<BF16><<<grid, 64, 0, stream>>>(seqs, pm, pl, pacc, static_cast<uint16_t*>(out), mf, lf,
+                                                      acc_out, hq, d);
+  return hipGetLastError();
+}
+
+hipError_t launch_mass_reduce(const SeqInfo* seqs, const int32_t* session_rows, const int32_t* session_first,
+                              const float* mass_m, const float* mass_s, const float* mf, const float* lf,
+                              float* mass_accum, int accum_stride, int hq, int mass_stride, int n_sessions,
+                              int max_blocks, hipStream_t stream) {
+  if (n_sessions == 0 || max_blocks == 0) return hipSuccess;
+  dim3 grid((max_blocks + 255) / 256, n_sessions);
+  mass_reduce_kernel<<<grid, 256, 0, stream>>>(seqs, session_rows, session_first, mass_m, mass_s, mf, lf, mass_accum,
+                                               accum_stride, hq, mass_stride, n_sessions, max_blocks);
+  return hipGetLastError();
+}
+
+}  // namespace pgr

@@ -1,0 +1,439 @@
+// extern "C" entry points declared in include/pgr.h.
+#include "../../include/pgr.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <new>
+#include <string>
+
+#include "paged_kv.h"
+#include "pager_core.h"
+#include "pgr_common.h"
+#include "pgr_kernels.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int set_err(int code, const std::string& msg) {
+  g_last_error = msg;
+  return code;
+}
+
+int hip_err(hipError_t e, const char* what) {
+  return set_err(pgr::kErrHip, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
+
+int check_dense(int64_t batch, int64_t hq, int64_t hkv, int64_t tokens, int64_t d, int dtype, float scale) {
+  if (batch < 0 || hq <= 0 || hkv <= 0 || tokens < 0 || d <= 0)
+    return set_err(pgr::kErrInvalid, "negative or zero dimension");
+  if (hq % hkv != 0) return set_err(pgr::kErrInvalid, "num_query_heads must be a multiple of num_kv_heads");
+  if (hq / hkv > pgr::kMaxRep)
+    return set_err(pgr::kErrUnsupported, "streaming attention's GQA query-head packing supports n_rep up to 16");
+  if (!pgr::head_dim_supported((int)d)) return set_err(pgr::kErrUnsupported, "head_dim must be 32, 64 or 128");
+  if (dtype != pgr::kF16 && dtype != pgr::kBF16) return set_err(pgr::kErrInvalid, "dtype must be fp16 or bf16");
+  if (!(scale > 0.f) || !std::isfinite(scale)) return set_err(pgr::kErrInvalid, "scale must be positive and finite");
+  if (batch > 65535 || hkv > 65535 || tokens > ((int64_t)1 << 30))
+    return set_err(pgr::kErrInvalid, "shape exceeds the launch limits");
+  return pgr::kOk;
+}
+
+struct DensePlan {
+  int wave_tokens = 0, n_split = 0;
+  size_t bytes = 0, o_pm = 0, o_pl = 0, o_pacc = 0;
+};
+
+DensePlan plan_dense(int64_t batch, int64_t hq, int64_t hkv, int64_t tokens, int64_t d, int mode, int64_t tpb) {
+  DensePlan p;
+  if (tokens <= 0 || batch <= 0) return p;
+  const bool mass = mode == PGR_MODE_ACCUMULATE;
+  p.wave_tokens = pgr::dense_wave_tokens((int)batch, (int)hkv, (int)tokens, (int)(mass ? tpb : 16), mass);
+  const int64_t per_wg = (int64_t)pgr::kWaves * p.wave_tokens;
+  p.n_split = (int)((tokens + per_wg - 1) / per_wg);
+  const size_t slots = (size_t)batch * hkv * p.n_split;
+  const size_t n_rep = (size_t)(hq / hkv);
+  size_t off = 0;
+  p.o_pm = off;
+  off = pgr::align_up(off + slots * n_rep * sizeof(float), 256);
+  p.o_pl = off;
+  off = pgr::align_up(off + slots * n_rep * sizeof(float), 256);
+  p.o_pacc = off;
+  if (mode != PGR_MODE_STATS) off = pgr::align_up(off + slots * n_rep * d * sizeof(float), 256);
+  p.bytes = off;
+  return p;
+}
+
+int run_dense(int mode, const void* q, const void* k, const void* v, const int32_t* valid, const int32_t* active,
+              float* m, float* l, float* acc, float* block_mass, int64_t max_blocks, int64_t block_id_offset,
+              int64_t tpb, int64_t batch, int64_t hq, int64_t hkv, int64_t tokens, int64_t d, int dtype, float scale,
+              float softcap, void* ws, size_t ws_bytes, void* stream) {
+  int rc = check_dense(batch, hq, hkv, tokens, d, dtype, scale);
+  if (rc != pgr::kOk) return rc;
+  if (mode == PGR_MODE_ACCUMULATE) {
+    if (tpb <= 0 || tpb % 16 != 0) return set_err(pgr::kErrUnsupported, "tokens_per_block must be a multiple of 16");
+    const int64_t nb = (tokens + tpb - 1) / tpb;
+    if (block_id_offset < 0 || block_id_offset + nb > max_blocks)
+      return set_err(pgr::kErrInvalid, "block_mass is too small for block_id_offset + this chunk's blocks");
+    if (block_mass == nullptr) return set_err(pgr::kErrInvalid, "block_mass is null");
+  }
+  if (tokens == 0 || batch == 0) return pgr::kOk;  // nothing to fold: the state is unchanged
+  if (!q || !k || !m || !l || (mode != PGR_MODE_STATS && (!v || !acc)))
+    return set_err(pgr::kErrInvalid, "null tensor pointer");
+  const DensePlan p = plan_dense(batch, hq, hkv, tokens, d, mode, tpb);
+  if (ws == nullptr || ws_bytes < p.bytes) return set_err(pgr::kErrCapacity, "workspace too small");
+  char* w = static_cast<char*>(ws);
+  pgr::DenseLaunch L{};
+  L.q = q;
+  L.k = k;
+  L.v = v;
+  L.valid = valid;
+  L.active = active;
+  L.m = m;
+  L.l = l;
+  L.acc = acc;
+  L.block_mass = block_mass;
+  L.pm = reinterpret_cast<float*>(w + p.o_pm);
+  L.pl = reinterpret_cast<float*>(w + p.o_pl);
+  L.pacc = reinterpret_cast<float*>(w + p.o_pacc);
+  L.batch = (int)batch;
+  L.hq = (int)hq;
+  L.hkv = (int)hkv;
+  L.tc = (int)tokens;
+  L.wave_tokens = p.wave_tokens;
+  L.n_split = p.n_split;
+  L.tokens_per_block = (int)tpb;
+  L.max_blocks = (int)max_blocks;
+  L.block_id_offset = (int)block_id_offset;
+  L.scale = scale;
+  L.softcap = softcap > 0.f ? softcap : 0.f;
+  hipError_t e = pgr::launch_dense(dtype, mode, (int)d, L, as_stream(stream));
+  if (e != hipSuccess) return hip_err(e, "dense attention launch");
+  return pgr::kOk;
+}
+
+pgr::PagedKV* kv_of(void* h) { return static_cast<pgr::PagedKV*>(h); }
+
+int kv_rc(pgr::PagedKV* kv, int rc) {
+  if (rc != pgr::kOk) g_last_error = kv->error();
+  return rc;
+}
+
+}  // namespace
+
+extern "C" {
+
+int pgr_abi_version(void) { return 1; }
+
+const char* pgr_last_error(void) { return g_last_error.c_str(); }
+
+size_t pgr_attn_workspace_bytes(int64_t batch, int64_t num_query_heads, int64_t num_kv_heads, int64_t tokens,
+                                int64_t head_dim, int mode, int64_t tokens_per_block) {
+  if (batch <= 0 || num_kv_heads <= 0 || num_query_heads <= 0 || tokens <= 0 || head_dim <= 0) return 0;
+  if (mode == PGR_MODE_ACCUMULATE && (tokens_per_block <= 0 || tokens_per_block % 16 != 0)) return 0;
+  return plan_dense(batch, num_query_heads, num_kv_heads, tokens, head_dim, mode, tokens_per_block).bytes;
+}
+
+int pgr_attn_step(const void* q, const void* k, const void* v, const int32_t* valid, const int32_t* active, float* m,
+                  float* l, float* acc, int64_t batch, int64_t num_query_heads, int64_t num_kv_heads, int64_t tokens,
+                  int64_t head_dim, int dtype, float scale, float softcap, void* workspace, size_t workspace_bytes,
+                  void* stream) {
+  return run_dense(PGR_MODE_FOLD, q, k, v, valid, active, m, l, acc, nullptr, 0, 0, 16, batch, num_query_heads,
+                   num_kv_heads, tokens, head_dim, dtype, scale, softcap, workspace, workspace_bytes, stream);
+}
+
+int pgr_attn_stats_step(const void* q, const void* k, const int32_t* valid, const int32_t* active, float* m, float* l,
+                        int64_t batch, int64_t num_query_heads, int64_t num_kv_heads, int64_t tokens, int64_t head_dim,
+                        int dtype, float scale, float softcap, void* workspace, size_t workspace_bytes, void* stream) {
+  return run_dense(PGR_MODE_STATS, q, k, nullptr, valid, active, m, l, nullptr, nullptr, 0, 0, 16, batch,
+                   num_query_heads, num_kv_heads, tokens, head_dim, dtype, scale, softcap, workspace, workspace_bytes,
+                   stream);
+}
+
+int pgr_attn_accumulate_step(const void* q, const void* k, const void* v, const int32_t* valid, const int32_t* active,
+                             const float* m, const float* l, float* acc, float* block_mass, int64_t max_blocks,
+                             int64_t block_id_offset, int64_t tokens_per_block, int64_t batch,
+                             int64_t num_query_heads, int64_t num_kv_heads, int64_t tokens, int64_t head_dim,
+                             int dtype, float scale, float softcap, void* workspace, size_t workspace_bytes,
+                             void* stream) {
+  return run_dense(PGR_MODE_ACCUMULATE, q, k, v, valid, active, const_cast<float*>(m), const_cast<float*>(l), acc,
+                   block_mass, max_blocks, block_id_offset, tokens_per_block, batch, num_query_heads, num_kv_heads,
+                   tokens, head_dim, dtype, scale, softcap, workspace, workspace_bytes, stream);
+}
+
+int pgr_attn_fold_fixed_step(const void* q, const void* k, const void* v, const int32_t* valid, const float* m,
+                             const float* l, float* acc, int64_t batch, int64_t num_query_heads, int64_t num_kv_heads,
+                             int64_t tokens, int64_t head_dim, int dtype, float scale, float softcap, void* workspace,
+                             size_t workspace_bytes, void* stream) {
+  return run_dense(PGR_MODE_FOLD_FIXED, q, k, v, valid, nullptr, const_cast<float*>(m), const_cast<float*>(l), acc,
+                   nullptr, 0, 0, 16, batch, num_query_heads, num_kv_heads, tokens, head_dim, dtype, scale, softcap,
+                   workspace, workspace_bytes, stream);
+}
+
+int pgr_attn_finalize(const float* acc, const float* l, void* out, int64_t rows, int64_t head_dim, int dtype,
+                      void* stream) {
+  if (rows < 0 || head_dim <= 0) return set_err(pgr::kErrInvalid, "negative or zero dimension");
+  if (dtype != pgr::kF16 && dtype != pgr::kBF16 && dtype != PGR_DTYPE_F32)
+    return set_err(pgr::kErrInvalid, "dtype must be fp16, bf16 or fp32");
+  if (rows == 0) return pgr::kOk;
+  if (!acc || !l || !out) return set_err(pgr::kErrInvalid, "null tensor pointer");
+  hipError_t e = pgr::launch_finalize(dtype, acc, l, out, (int)rows, (int)head_dim, as_stream(stream));
+  if (e != hipSuccess) return hip_err(e, "finalize launch");
+  return pgr::kOk;
+}
+
+// ---- placement -----------------------------------------------------------------------
+
+void* pgr_pager_new(uint64_t vram, uint64_t ram, uint64_t recent, uint64_t rebalance_interval, float promote_margin,
+                    float ram_promote_margin, const char* policy) {
+  const std::string name = policy ? policy : "heavy_hitter";
+  return new (std::nothrow) pgr::PlacementPager(vram, ram, recent, rebalance_interval, promote_margin,
+                                                ram_promote_margin, pgr::policy_from_name(name));
+}
+
+void pgr_pager_free(void* pager) { delete static_cast<pgr::PlacementPager*>(pager); }
+
+int pgr_pager_on_step(void* pager, uint64_t token_idx, uint32_t layer, const float* attention, size_t n) {
+  (void)layer;
+  if (!pager || (n && !attention)) return set_err(pgr::kErrInvalid, "null pointer");
+  if (n > ((size_t)1 << 31)) return set_err(pgr::kErrInvalid, "attention vector too long");
+  if (!static_cast<pgr::PlacementPager*>(pager)->on_step(token_idx, attention, n))
+    return set_err(pgr::kErrState, "attempt to calculate the remainder with a divisor of zero");
+  return pgr::kOk;
+}
+
+int pgr_pager_force_rebalance(void* pager, uint64_t token_idx) {
+  if (!pager) return set_err(pgr::kErrInvalid, "null pager");
+  if (token_idx >= ((uint64_t)1 << 31)) return set_err(pgr::kErrInvalid, "token_idx too large for the block table");
+  static_cast<pgr::PlacementPager*>(pager)->force_rebalance(token_idx);
+  return pgr::kOk;
+}
+
+size_t pgr_pager_num_blocks(void* pager) { return pager ? static_cast<pgr::PlacementPager*>(pager)->num_blocks() : 0; }
+
+size_t pgr_pager_tiers(void* pager, uint8_t* out, size_t cap) {
+  if (!pager) return 0;
+  auto* p = static_cast<pgr::PlacementPager*>(pager);
+  const size_t n = p->num_blocks();
+  if (out && cap >= n) p->tiers(out);
+  return n;
+}
+
+size_t pgr_pager_vram_block_ids(void* pager, uint64_t* out, size_t cap) {
+  if (!pager) return 0;
+  auto* p = static_cast<pgr::PlacementPager*>(pager);
+  const size_t n = p->vram_count();
+  if (out && cap >= n) p->vram_block_ids(out);
+  return n;
+}
+
+int pgr_pager_metrics(void* pager, pgr_pager_metrics_t* out) {
+  if (!pager || !out) return set_err(pgr::kErrInvalid, "null pointer");
+  const pgr::PagerMetrics& m = static_cast<pgr::PlacementPager*>(pager)->metrics();
+  out->tokens = m.tokens;
+  out->vram_peak = m.vram_peak;
+  out->ram_peak = m.ram_peak;
+  out->swap_vram_ram = m.swap_vram_ram;
+  out->swap_ram_ssd = m.swap_ram_ssd;
+  out->attention_mass_total = m.attention_mass_total;
+  out->attention_mass_vram = m.attention_mass_vram;
+  return pgr::kOk;
+}
+
+// ---- paged KV store -------------------------------------------------------------------
+
+void* pgr_kv_create(const pgr_kv_config_t* c) {
+  if (!c) {
+    set_err(pgr::kErrInvalid, "null config");
+    return nullptr;
+  }
+  pgr::PagedKVConfig cfg;
+  cfg.num_layers = c->num_layers;
+  cfg.kv_heads = c->kv_heads;
+  cfg.query_heads = c->query_heads;
+  cfg.head_dim = c->head_dim;
+  cfg.tokens_per_block = c->tokens_per_block;
+  cfg.dtype = c->dtype;
+  cfg.pool_slots = c->pool_slots;
+  cfg.host_records = c->host_records;
+  cfg.staging_slots = c->staging_slots;
+  cfg.staging_buffers = c->staging_buffers;
+  cfg.blocks_per_workgroup = c->blocks_per_workgroup > 0 ? c->blocks_per_workgroup : 16;
+  auto* kv = new (std::nothrow) pgr::PagedKV(cfg);
+  if (!kv) {
+    set_err(pgr::kErrCapacity, "out of host memory");
+    return nullptr;
+  }
+  const int rc = kv->init();
+  if (rc != pgr::kOk) {
+    g_last_error = kv->error();
+    delete kv;
+    return nullptr;
+  }
+  return kv;
+}
+
+void pgr_kv_destroy(void* kv) { delete kv_of(kv); }
+
+int pgr_kv_add_session(void* kv, int32_t rows, int64_t capacity_tokens, const int32_t* lo_per_row) {
+  if (!kv) return set_err(pgr::kErrInvalid, "null store");
+  return kv_rc(kv_of(kv), kv_of(kv)->add_session(rows, capacity_tokens, lo_per_row));
+}
+
+int pgr_kv_remove_session(void* kv, int32_t sid) {
+  if (!kv) return set_err(pgr::kErrInvalid, "null store");
+  return kv_rc(kv_of(kv), kv_of(kv)->remove_session(sid));
+}
+
+int pgr_kv_set_lo(void* kv, int32_t sid, const int32_t* lo_per_row) {
+  if (!kv || !lo_per_row) return set_err(pgr::kErrInvalid, "null pointer");
+  return kv_rc(kv_of(kv), kv_of(kv)->set_lo(sid, lo_per_row));
+}
+
+int pgr_kv_set_length(void* kv, int32_t sid, int64_t n_tokens) {
+  if (!kv) return set_err(pgr::kErrInvalid, "null store");
+  return kv_rc(kv_of(kv), kv_of(kv)->set_length(sid, n_tokens));
+}
+
+int pgr_kv_import(void* kv, int32_t sid, int32_t row, int32_t layer, const void* k, const void* v, int64_t n_src,
+                  int64_t n_tokens, void* stream) {
+  if (!kv || !k || !v) return set_err(pgr::kErrInvalid, "null pointer");
+  return kv_rc(kv_of(kv), kv_of(kv)->import_tokens(sid, row, layer, k, v, n_src, n_tokens, as_stream(stream)));
+}
+
+int pgr_kv_export(void* kv, int32_t sid, int32_t row, int32_t layer, void* k, void* v, int64_t n_tokens,
+                  void* stream) {
+  if (!kv || !k || !v) return set_err(pgr::kErrInvalid, "null pointer");
+  return kv_rc(kv_of(kv), kv_of(kv)->export_tokens(sid, row, layer, k, v, n_tokens, as_stream(stream)));
+}
+
+int pgr_kv_put_block(void* kv, int32_t sid, int64_t block_id, const void* key, const void* value, void* stream) {
+  if (!kv || !key || !value) return set_err(pgr::kErrInvalid, "null pointer");
+  return kv_rc(kv_of(kv), kv_of(kv)->put_block(sid, block_id, key, value, as_stream(stream)));
+}
+
+int pgr_kv_get_block(void* kv, int32_t sid, int64_t block_id, void* key, void* value, void* stream) {
+  if (!kv || !key || !value) return set_err(pgr::kErrInvalid, "null pointer");
+  return kv_rc(kv_of(kv), kv_of(kv)->get_block(sid, block_id, key, value, as_stream(stream)));
+}
+
+int pgr_kv_apply_tiers(void* kv, int32_t sid, const uint8_t* tiers, int64_t n_tiers, int64_t* to_gpu, int64_t* n_gpu,
+                       int64_t* to_cpu, int64_t* n_cpu, int64_t* fail_block, void* stream) {
+  if (!kv || (n_tiers && !tiers) || !to_gpu || !n_gpu || !to_cpu || !n_cpu || !fail_block)
+    return set_err(pgr::kErrInvalid, "null pointer");
+  return kv_rc(kv_of(kv), kv_of(kv)->apply_tiers(sid, tiers, n_tiers, to_gpu, n_gpu, to_cpu, n_cpu, fail_block,
+                                                 as_stream(stream)));
+}
+
+int pgr_kv_set_ram_budget(void* kv, int64_t bytes) {
+  if (!kv) return set_err(pgr::kErrInvalid, "null store");
+  kv_of(kv)->set_ram_budget(bytes);
+  return pgr::kOk;
+}
+
+int pgr_kv_begin_step(void* kv, const int32_t* sids, int32_t n, void* stream) {
+  if (!kv || (n && !sids) || n < 0) return set_err(pgr::kErrInvalid, "null pointer or negative count");
+  return kv_rc(kv_of(kv), kv_of(kv)->begin_step(sids, n, as_stream(stream)));
+}
+
+int pgr_kv_decode_layer(void* kv, int32_t layer, const void* q, const void* k_new, const void* v_new, void* out,
+                        float* mass_accum, int64_t accum_stride, float scale, float softcap, void* stream) {
+  if (!kv || !q || !k_new || !v_new || !out) return set_err(pgr::kErrInvalid, "null pointer");
+  if (!(scale > 0.f) || !std::isfinite(scale)) return set_err(pgr::kErrInvalid, "scale must be positive and finite");
+  return kv_rc(kv_of(kv), kv_of(kv)->decode_layer(layer, q, k_new, v_new, out, mass_accum, accum_stride, scale,
+                                                  softcap > 0.f ? softcap : 0.f, as_stream(stream)));
+}
+
+int pgr_kv_end_step(void* kv, int32_t* completed, int32_t* n_completed) {
+  if (!kv) return set_err(pgr::kErrInvalid, "null store");
+  int c = 0;
+  const int rc = kv_of(kv)->end_step(completed, &c);
+  if (n_completed) *n_completed = c;
+  return kv_rc(kv_of(kv), rc);
+}
+
+int pgr_kv_session_info(void* kv, int32_t sid, int64_t* info) {
+  if (!kv || !info) return set_err(pgr::kErrInvalid, "null pointer");
+  const int rc = kv_of(kv)->session_info(sid, &info[0], &info[1], &info[2], &info[3]);
+  if (rc != pgr::kOk) return set_err(rc, "unknown session");
+  return rc;
+}
+
+int pgr_kv_block_ids(void* kv, int32_t sid, int32_t gpu, int64_t* out, int64_t cap) {
+  if (!kv || (cap && !out)) return set_err(pgr::kErrInvalid, "null pointer");
+  const int rc = kv_of(kv)->block_ids(sid, gpu, out, cap);
+  if (rc < 0) return set_err(rc, "unknown session");
+  return rc;
+}
+
+int pgr_kv_step_host_blocks(void* kv, int32_t seq, int64_t* out, int64_t cap) {
+  if (!kv || (cap && !out)) return set_err(pgr::kErrInvalid, "null pointer");
+  const int rc = kv_of(kv)->step_host_blocks(seq, out, cap);
+  if (rc < 0) return set_err(rc, "no such sequence in the last step");
+  return rc;
+}
+
+int pgr_kv_step_stats(void* kv, pgr_kv_step_stats_t* out) {
+  if (!kv || !out) return set_err(pgr::kErrInvalid, "null pointer");
+  const pgr::StepStats& s = kv_of(kv)->step_stats();
+  out->resident_tokens = s.resident_tokens;
+  out->host_tokens = s.host_tokens;
+  out->host_blocks = s.host_blocks;
+  out->copies = s.copies;
+  out->chunks = s.chunks;
+  out->launches = s.launches;
+  out->work_items = s.work_items;
+  return pgr::kOk;
+}
+
+int pgr_kv_stats(void* kv, pgr_kv_stats_t* out) {
+  if (!kv || !out) return set_err(pgr::kErrInvalid, "null pointer");
+  const pgr::StoreStats s = kv_of(kv)->stats();
+  out->gpu_to_cpu_bytes = s.gpu_to_cpu_bytes;
+  out->cpu_to_gpu_bytes = s.cpu_to_gpu_bytes;
+  out->gpu_to_cpu_copies = s.gpu_to_cpu_copies;
+  out->cpu_to_gpu_copies = s.cpu_to_gpu_copies;
+  out->gpu_to_cpu_sec = s.gpu_to_cpu_sec;
+  out->cpu_to_gpu_sec = s.cpu_to_gpu_sec;
+  out->evict_bytes_copied = s.evict_bytes_copied;
+  out->load_bytes_copied = s.load_bytes_copied;
+  out->stream_bytes = s.stream_bytes;
+  out->stream_copies = s.stream_copies;
+  return pgr::kOk;
+}
+
+int pgr_kv_resident_bytes(void* kv, int64_t* gpu, int64_t* cpu) {
+  if (!kv || !gpu || !cpu) return set_err(pgr::kErrInvalid, "null pointer");
+  *gpu = kv_of(kv)->resident_gpu_bytes();
+  *cpu = kv_of(kv)->resident_cpu_bytes();
+  return pgr::kOk;
+}
+
+int pgr_kv_block_bytes(void* kv, int32_t sid, int64_t* bytes) {
+  if (!kv || !bytes) return set_err(pgr::kErrInvalid, "null pointer");
+  int64_t info[4];
+  if (kv_of(kv)->session_info(sid, &info[0], &info[1], &info[2], &info[3]) != pgr::kOk)
+    return set_err(pgr::kErrKey, "unknown session");
+  *bytes = kv_of(kv)->block_bytes_all_layers(sid);
+  return pgr::kOk;
+}
+
+int pgr_kv_set_timing(void* kv, int32_t on) {
+  if (!kv) return set_err(pgr::kErrInvalid, "null store");
+  kv_of(kv)->set_timing(on != 0);
+  return pgr::kOk;
+}
+
+int pgr_kv_kernel_time(void* kv, double* ms, int64_t* launches, int64_t* bytes) {
+  if (!kv || !ms || !launches || !bytes) return set_err(pgr::kErrInvalid, "null pointer");
+  return kv_rc(kv_of(kv), kv_of(kv)->kernel_time(ms, launches, bytes));
+}
+
+int pgr_kv_sync(void* kv) {
+  if (!kv) return set_err(pgr::kErrInvalid, "null store");
+  return kv_rc(kv_of(kv), kv_of(kv)->sync());
+}
+
+}  // extern "C"

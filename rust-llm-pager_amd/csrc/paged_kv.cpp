@@ -1,0 +1,1007 @@
+// Native paged KV store and streaming decode executor (see paged_kv.h for the layout).
+//
+// Reference behaviour it replaces, per decode step and layer (paged_model.py:878-1086):
+// a Python loop gathering every block with a blocking .to(device) + permute + torch.cat,
+// then one Triton launch per 64-block group (two passes for attention-scoring policies).
+// Here one plan per step covers all layers: resident blocks are read in place from the HBM
+// pool, host blocks are streamed in contiguous runs into a staging ring on a side stream,
+// and one split-K kernel per staged chunk folds them, with a merge kernel at the end.
+#include "paged_kv.h"
+
+#include <algorithm>
+#include <cstring>
+
+#include "pgr_kernels.h"
+
+namespace pgr {
+
+namespace {
+
+// One workgroup per block of records: converts tokens of one (row, layer) from the
+// [Hkv, n_src, D] layout into records at dst + slot[i] * rec (zero past n_tokens), or back.
+__global__ void hf_to_records_kernel(const uint16_t* k, const uint16_t* v, int64_t n_src, int64_t n_tokens,
+                                     int64_t first_block, const int32_t* dst_slot, uint16_t* dst, int hkv, int tpb,
+                                     int d) {
+  const int i = blockIdx.x;
+  const int64_t b = first_block + i;
+  const size_t rec = (size_t)2 * hkv * tpb * d;
+  uint16_t* kr = dst + (size_t)dst_slot[i] * rec;
+  uint16_t* vr = kr + (size_t)hkv * tpb * d;
+  const int per = hkv * tpb * d;
+  for (int e = threadIdx.x; e < per; e += blockDim.x) {
+    const int h = e / (tpb * d);
+    const int r = e - h * tpb * d;
+    const int t = r / d, dd = r - t * d;
+    const int64_t tok = b * tpb + t;
+    uint16_t kv = 0, vv = 0;
+    if (tok < n_tokens) {
+      const size_t src = ((size_t)h * n_src + tok) * d + dd;
+      kv = k[src];
+      vv = v[src];
+    }
+    kr[e] = kv;
+    vr[e] = vv;
+  }
+}
+
+__global__ void records_to_hf_kernel(const uint16_t* src, const int32_t* src_slot, int64_t first_block,
+                                     int64_t n_tokens, uint16_t* k, uint16_t* v, int hkv, int tpb, int d) {
+  const int i = blockIdx.x;
+  const int64_t b = first_block + i;
+  const size_t rec = (size_t)2 * hkv * tpb * d;
+  const uint16_t* kr = src + (size_t)src_slot[i] * rec;
+  const uint16_t* vr = kr + (size_t)hkv * tpb * d;
+  const int per = hkv * tpb * d;
+  for (int e = threadIdx.x; e < per; e += blockDim.x) {
+    const int h = e / (tpb * d);
+    const int r = e - h * tpb * d;
+    const int t = r / d, dd = r - t * d;
+    const int64_t tok = b * tpb + t;
+    if (tok < n_tokens) {
+      const size_t dst = ((size_t)h * n_tokens + tok) * d + dd;
+      k[dst] = kr[e];
+      v[dst] = vr[e];
+    }
+  }
+}
+
+}  // namespace
+
+PagedKV::PagedKV(const PagedKVConfig& cfg) : cfg_(cfg) {}
+
+PagedKV::~PagedKV() {
+  if (copy_stream_) hipStreamSynchronize(copy_stream_);
+  hipDeviceSynchronize();
+  for (void* p : pool_)
+    if (p) hipFree(p);
+  for (void* p : host_)
+    if (p) hipHostFree(p);
+  if (stage_) hipFree(stage_);
+  if (ws_) hipFree(ws_);
+  if (plan_host_) hipHostFree(plan_host_);
+  for (hipEvent_t e : buf_free_) hipEventDestroy(e);
+  for (hipEvent_t e : chunk_ready_) hipEventDestroy(e);
+  for (auto& t : timing_pending_) {
+    hipEventDestroy(t.start);
+    hipEventDestroy(t.stop);
+  }
+  for (auto& t : move_timing_) {
+    hipEventDestroy(t.start);
+    hipEventDestroy(t.stop);
+  }
+  if (plan_uploaded_) hipEventDestroy(plan_uploaded_);
+  if (compute_mark_) hipEventDestroy(compute_mark_);
+  if (copy_mark_) hipEventDestroy(copy_mark_);
+  if (copy_stream_) hipStreamDestroy(copy_stream_);
+}
+
+int PagedKV::fail(int code, const std::string& msg) {
+  err_ = msg;
+  return code;
+}
+
+int PagedKV::hip_fail(hipError_t e, const char* what) {
+  err_ = std::string(what) + ": " + hipGetErrorString(e);
+  return kErrHip;
+}
+
+#define PGR_HIP(call)                                   \
+  do {                                                  \
+    hipError_t e_ = (call);                             \
+    if (e_ != hipSuccess) return hip_fail(e_, #call);   \
+  } while (0)
+
+size_t PagedKV::rec_bytes() const {
+  return (size_t)2 * cfg_.kv_heads * cfg_.tokens_per_block * cfg_.head_dim * 2;
+}
+
+int PagedKV::init() {
+  if (cfg_.num_layers <= 0 || cfg_.kv_heads <= 0 || cfg_.tokens_per_block <= 0 || cfg_.tokens_per_block % 16 != 0)
+    return fail(kErrInvalid, "num_layers, kv_heads > 0 and tokens_per_block a positive multiple of 16 required");
+  if (!head_dim_supported(cfg_.head_dim)) return fail(kErrUnsupported, "head_dim must be 32, 64 or 128");
+  if (cfg_.query_heads <= 0 || cfg_.query_heads % cfg_.kv_heads != 0)
+    return fail(kErrInvalid, "query_heads must be a positive multiple of kv_heads");
+  if (cfg_.query_heads / cfg_.kv_heads > kMaxRep) return fail(kErrUnsupported, "n_rep above 16 is not supported");
+  if (cfg_.dtype != kF16 && cfg_.dtype != kBF16) return fail(kErrInvalid, "dtype must be fp16 or bf16");
+  if (cfg_.pool_slots <= 0 || cfg_.host_records < 0 || cfg_.staging_slots <= 0 || cfg_.staging_buffers < 1)
+    return fail(kErrInvalid, "pool_slots, staging_slots > 0 and staging_buffers >= 1 required");
+  if (cfg_.pool_slots > INT32_MAX / 2 || cfg_.staging_slots * cfg_.staging_buffers > INT32_MAX / 2)
+    return fail(kErrInvalid, "pool or staging too large for 32-bit record indices");
+  if (cfg_.blocks_per_workgroup < kWaves) cfg_.blocks_per_workgroup = kWaves;
+  const size_t rec = rec_bytes();
+  pool_.assign(cfg_.num_layers, nullptr);
+  host_.assign(cfg_.num_layers, nullptr);
+  for (int l = 0; l < cfg_.num_layers; ++l) {
+    PGR_HIP(hipMalloc(&pool_[l], rec * (size_t)cfg_.pool_slots));
+    if (cfg_.host_records > 0) PGR_HIP(hipHostMalloc(&host_[l], rec * (size_t)cfg_.host_records, hipHostMallocDefault));
+  }
+  PGR_HIP(hipMalloc(&stage_, rec * (size_t)cfg_.staging_slots * cfg_.staging_buffers));
+  PGR_HIP(hipStreamCreateWithFlags(&copy_stream_, hipStreamNonBlocking));
+  buf_free_.resize(cfg_.staging_buffers);
+  chunk_ready_.resize(cfg_.staging_buffers);
+  for (int i = 0; i < cfg_.staging_buffers; ++i) {
+    PGR_HIP(hipEventCreateWithFlags(&buf_free_[i], hipEventDisableTiming));
+    PGR_HIP(hipEventCreateWithFlags(&chunk_ready_[i], hipEventDisableTiming));
+  }
+  PGR_HIP(hipEventCreateWithFlags(&plan_uploaded_, hipEventDisableTiming));
+  PGR_HIP(hipEventCreateWithFlags(&compute_mark_, hipEventDisableTiming));
+  PGR_HIP(hipEventCreateWithFlags(&copy_mark_, hipEventDisableTiming));
+  free_slots_.resize(cfg_.pool_slots);
+  for (int64_t i = 0; i < cfg_.pool_slots; ++i) free_slots_[i] = (int32_t)(cfg_.pool_slots - 1 - i);
+  host_free_.clear();
+  if (cfg_.host_records > 0) host_free_.push_back({0, cfg_.host_records});
+  return kOk;
+}
+
+int PagedKV::alloc_slot() {
+  if (free_slots_.empty()) return -1;
+  const int s = free_slots_.back();
+  free_slots_.pop_back();
+  return s;
+}
+
+void PagedKV::free_slot(int32_t s) { free_slots_.push_back(s); }
+
+int64_t PagedKV::host_alloc(int64_t n) {
+  for (size_t i = 0; i < host_free_.size(); ++i) {
+    if (host_free_[i].second >= n) {
+      const int64_t off = host_free_[i].first;
+      host_free_[i].first += n;
+      host_free_[i].second -= n;
+      if (host_free_[i].second == 0) host_free_.erase(host_free_.begin() + i);
+      return off;
+    }
+  }
+  return -1;
+}
+
+void PagedKV::host_free(int64_t off, int64_t n) {
+  if (n <= 0) return;
+  auto it = std::lower_bound(host_free_.begin(), host_free_.end(), std::make_pair(off, (int64_t)0));
+  it = host_free_.insert(it, {off, n});
+  // Coalesce with neighbours.
+  size_t i = it - host_free_.begin();
+  if (i + 1 < host_free_.size() && host_free_[i].first + host_free_[i].second == host_free_[i + 1].first) {
+    host_free_[i].second += host_free_[i + 1].second;
+    host_free_.erase(host_free_.begin() + i + 1);
+  }
+  if (i > 0 && host_free_[i - 1].first + host_free_[i - 1].second == host_free_[i].first) {
+    host_free_[i - 1].second += host_free_[i].second;
+    host_free_.erase(host_free_.begin() + i);
+  }
+}
+
+int PagedKV::add_session(int rows, int64_t capacity_tokens, const int32_t* lo_per_row) {
+  if (rows <= 0 || capacity_tokens <= 0) return fail(kErrInvalid, "rows and capacity_tokens must be positive");
+  const int64_t T = cfg_.tokens_per_block;
+  Session s;
+  s.live = true;
+  s.rows = rows;
+  s.capacity_blocks = (capacity_tokens + T - 1) / T + 1;
+  s.row.resize(rows);
+  for (int r = 0; r < rows; ++r) {
+    const int64_t off = host_alloc(s.capacity_blocks);
+    if (off < 0) {
+      for (int q = 0; q < r; ++q) host_free(s.row[q].host_off, s.capacity_blocks);
+      return fail(kErrCapacity, "host mirror has no room for this session's capacity");
+    }
+    s.row[r].host_off = off;
+    s.row[r].lo = lo_per_row ? lo_per_row[r] : 0;
+  }
+  s.slot.assign((size_t)s.capacity_blocks * rows, -1);
+  s.host_valid.assign((size_t)s.capacity_blocks * rows, 0);
+  s.on_gpu.assign(s.capacity_blocks, 0);
+  for (size_t i = 0; i < sessions_.size(); ++i)
+    if (!sessions_[i].live) {
+      sessions_[i] = std::move(s);
+      return (int)i;
+    }
+  sessions_.push_back(std::move(s));
+  return (int)sessions_.size() - 1;
+}
+
+int PagedKV::remove_session(int sid) {
+  if (sid < 0 || sid >= (int)sessions_.size() || !sessions_[sid].live) return fail(kErrKey, "unknown session");
+  if (in_step_) return fail(kErrState, "remove_session during a decode step");
+  Session& s = sessions_[sid];
+  // Slots may still be read by queued kernels or copies: drain before recycling them.
+  PGR_HIP(hipDeviceSynchronize());
+  const int64_t T = cfg_.tokens_per_block;
+  const int64_t n_full = s.n_tokens / T;
+  for (int64_t b = 0; b < s.capacity_blocks; ++b)
+    for (int r = 0; r < s.rows; ++r) {
+      const int32_t sl = s.slot[b * s.rows + r];
+      if (sl >= 0) free_slot(sl);
+    }
+  const int64_t bb = block_bytes_all_layers(sid);
+  for (int64_t b = 0; b < n_full; ++b) {
+    if (s.on_gpu[b])
+      gpu_bytes_ -= bb;
+    else
+      cpu_bytes_ -= bb;
+  }
+  for (int r = 0; r < s.rows; ++r) host_free(s.row[r].host_off, s.capacity_blocks);
+  s = Session();
+  return kOk;
+}
+
+int PagedKV::set_lo(int sid, const int32_t* lo_per_row) {
+  if (sid < 0 || sid >= (int)sessions_.size() || !sessions_[sid].live) return fail(kErrKey, "unknown session");
+  Session& s = sessions_[sid];
+  for (int r = 0; r < s.rows; ++r) s.row[r].lo = lo_per_row[r];
+  return kOk;
+}
+
+int64_t PagedKV::block_bytes_all_layers(int sid) const {
+  const Session& s = sessions_[sid];
+  return (int64_t)rec_bytes() * s.rows * cfg_.num_layers;
+}
+
+int PagedKV::set_length(int sid, int64_t n_tokens) {
+  if (sid < 0 || sid >= (int)sessions_.size() || !sessions_[sid].live) return fail(kErrKey, "unknown session");
+  if (in_step_) return fail(kErrState, "set_length during a decode step");
+  Session& s = sessions_[sid];
+  const int64_t T = cfg_.tokens_per_block;
+  if (s.n_tokens != 0) return fail(kErrState, "set_length only applies to an empty session");
+  if (n_tokens < 0 || (n_tokens + T - 1) / T >= s.capacity_blocks)
+    return fail(kErrCapacity, "n_tokens exceeds the session capacity");
+  const int64_t n_full = n_tokens / T;
+  // Full blocks start on the host side (tier 1 in the pager's terms) with no data yet;
+  // the open block, if any, gets its HBM slot now.
+  for (int64_t b = 0; b < n_full; ++b) s.on_gpu[b] = 0;
+  cpu_bytes_ += n_full * block_bytes_all_layers(sid);
+  if (n_tokens % T != 0) {
+    for (int r = 0; r < s.rows; ++r) {
+      const int sl = alloc_slot();
+      if (sl < 0) return fail(kErrCapacity, "HBM pool exhausted");
+      s.slot[n_full * s.rows + r] = sl;
+    }
+  }
+  s.n_tokens = n_tokens;
+  return kOk;
+}
+
+int PagedKV::import_tokens(int sid, int row, int layer, const void* k, const void* v, int64_t n_src, int64_t n_tokens,
+                           hipStream_t stream) {
+  if (sid < 0 || sid >= (int)sessions_.size() || !sessions_[sid].live) return fail(kErrKey, "unknown session");
+  Session& s = sessions_[sid];
+  if (row < 0 || row >= s.rows || layer < 0 || layer >= cfg_.num_layers) return fail(kErrInvalid, "row/layer out of range");
+  if (n_tokens != s.n_tokens || n_src < n_tokens) return fail(kErrInvalid, "n_tokens must equal the session length");
+  if (in_step_) return fail(kErrState, "import during a decode step");
+  const int64_t T = cfg_.tokens_per_block;
+  const int64_t nb = (n_tokens + T - 1) / T;
+  const size_t rec = rec_bytes();
+  const int64_t cap = cfg_.staging_slots * cfg_.staging_buffers;
+  // Earlier streamed work may still read the staging ring.
+  PGR_HIP(hipStreamSynchronize(stream));
+  PGR_HIP(hipStreamSynchronize(copy_stream_));
+  std::vector<int32_t> slots;
+  int32_t* d_slots = nullptr;
+  PGR_HIP(hipMalloc(&d_slots, sizeof(int32_t) * (size_t)std::max<int64_t>(cap, 1)));
+  int rc = kOk;
+  for (int64_t b0 = 0; b0 < nb && rc == kOk; b0 += cap) {
+    const int64_t cnt = std::min(cap, nb - b0);
+    // Pass 1: resident blocks straight into the pool; pass 2: host blocks via staging.
+    for (int pass = 0; pass < 2 && rc == kOk; ++pass) {
+      slots.clear();
+      std::vector<int64_t> ids;
+      for (int64_t i = 0; i < cnt; ++i) {
+        const int64_t b = b0 + i;
+        const int32_t sl = s.slot[b * s.rows + row];
+        if (pass == 0 && sl >= 0) {
+          slots.push_back(sl);
+          ids.push_back(b);
+        }
+        if (pass == 1 && sl < 0) {
+          slots.push_back((int32_t)ids.size());
+          ids.push_back(b);
+        }
+      }
+      if (ids.empty()) continue;
+      // Consecutive ids are processed as runs so each kernel launch covers a contiguous id range.
+      size_t i = 0;
+      while (i < ids.size() && rc == kOk) {
+        size_t j = i + 1;
+        while (j < ids.size() && ids[j] == ids[j - 1] + 1) ++j;
+        const int64_t first = ids[i];
+        const int run = (int)(j - i);
+        std::vector<int32_t> run_slots(slots.begin() + i, slots.begin() + j);
+        if (pass == 1)
+          for (int q = 0; q < run; ++q) run_slots[q] = q;
+        hipError_t e = hipMemcpyAsync(d_slots, run_slots.data(), sizeof(int32_t) * run, hipMemcpyHostToDevice, stream);
+        if (e != hipSuccess) {
+          rc = hip_fail(e, "hipMemcpyAsync(slots)");
+          break;
+        }
+        uint16_t* dst = static_cast<uint16_t*>(pass == 0 ? pool_[layer] : stage_);
+        hf_to_records_kernel<<<run, 256, 0, stream>>>(static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
+                                                      n_src, n_tokens, first, d_slots, dst, cfg_.kv_heads, (int)T,
+                                                      cfg_.head_dim);
+        e = hipGetLastError();
+        if (e != hipSuccess) {
+          rc = hip_fail(e, "hf_to_records_kernel");
+          break;
+        }
+        if (pass == 1) {
+          char* hdst = static_cast<char*>(host_[layer]) + (size_t)(s.row[row].host_off + first) * rec;
+          e = hipMemcpyAsync(hdst, stage_, rec * run, hipMemcpyDeviceToHost, stream);
+          if (e != hipSuccess) {
+            rc = hip_fail(e, "hipMemcpyAsync(D2H import)");
+            break;
+          }
+          for (int q = 0; q < run; ++q) s.host_valid[(first + q) * s.rows + row] = 1;
+        }
+        // The slot list buffer is reused by the next launch.
+        e = hipStreamSynchronize(stream);
+        if (e != hipSuccess) {
+          rc = hip_fail(e, "hipStreamSynchronize(import)");
+          break;
+        }
+        i = j;
+      }
+    }
+  }
+  hipFree(d_slots);
+  return rc;
+}
+
+int PagedKV::export_tokens(int sid, int row, int layer, void* k, void* v, int64_t n_tokens, hipStream_t stream) {
+  if (sid < 0 || sid >= (int)sessions_.size() || !sessions_[sid].live) return fail(kErrKey, "unknown session");
+  Session& s = sessions_[sid];
+  if (row < 0 || row >= s.rows || layer < 0 || layer >= cfg_.num_layers) return fail(kErrInvalid, "row/layer out of range");
+  if (n_tokens > s.n_tokens) return fail(kErrInvalid, "n_tokens exceeds the session length");
+  if (in_step_) return fail(kErrState, "export during a decode step");
+  const int64_t T = cfg_.tokens_per_block;
+  const int64_t nb = (n_tokens + T - 1) / T;
+  const size_t rec = rec_bytes();
+  PGR_HIP(hipStreamSynchronize(stream));
+  PGR_HIP(hipStreamSynchronize(copy_stream_));
+  int32_t* d_slot = nullptr;
+  PGR_HIP(hipMalloc(&d_slot, sizeof(int32_t)));
+  int rc = kOk;
+  for (int64_t b = 0; b < nb && rc == kOk; ++b) {
+    int32_t sl = s.slot[b * s.rows + row];
+    const uint16_t* src = static_cast<const uint16_t*>(pool_[layer]);
+    if (sl < 0) {
+      const char* hsrc = static_cast<const char*>(host_[layer]) + (size_t)(s.row[row].host_off + b) * rec;
+      hipError_t e = hipMemcpyAsync(stage_, hsrc, rec, hipMemcpyHostToDevice, stream);
+      if (e != hipSuccess) {
+        rc = hip_fail(e, "hipMemcpyAsync(H2D export)");
+        break;
+      }
+      sl = 0;
+      src = static_cast<const uint16_t*>(stage_);
+    }
+    hipError_t e = hipMemcpyAsync(d_slot, &sl, sizeof(int32_t), hipMemcpyHostToDevice, stream);
+    if (e == hipSuccess) {
+      records_to_hf_kernel<<<1, 256, 0, stream>>>(src, d_slot, b, n_tokens, static_cast<uint16_t*>(k),
+                                                 static_cast<uint16_t*>(v), cfg_.kv_heads, (int)T, cfg_.head_dim);
+      e = hipGetLastError();
+    }
+    if (e == hipSuccess) e = hipStreamSynchronize(stream);
+    if (e != hipSuccess) rc = hip_fail(e, "export");
+  }
+  hipFree(d_slot);
+  return rc;
+}
+
+int PagedKV::put_block(int sid, int64_t block_id, const void* key, const void* value, hipStream_t stream) {
+  if (sid < 0 || sid >= (int)sessions_.size() || !sessions_[sid].live) return fail(kErrKey, "unknown session");
+  if (in_step_) return fail(kErrState, "put_block during a decode step");
+  Session& s = sessions_[sid];
+  const int64_t T = cfg_.tokens_per_block;
+  if (s.n_tokens % T != 0) return fail(kErrState, "put_block needs a block-aligned session (no open block)");
+  if (block_id != s.n_tokens / T) return fail(kErrInvalid, "put_block: block ids must be registered in order");
+  if (block_id + 1 >= s.capacity_blocks) return fail(kErrCapacity, "session capacity reached");
+  std::vector<int32_t> slots(s.rows);
+  for (int r = 0; r < s.rows; ++r) {
+    const int sl = alloc_slot();
+    if (sl < 0) {
+      for (int q = 0; q < r; ++q) free_slot(slots[q]);
+      return fail(kErrCapacity, "HBM pool exhausted");
+    }
+    slots[r] = sl;
+  }
+  int32_t* d_slots = nullptr;
+  PGR_HIP(hipMalloc(&d_slots, sizeof(int32_t) * s.rows));
+  hipError_t e = hipMemcpyAsync(d_slots, slots.data(), sizeof(int32_t) * s.rows, hipMemcpyHostToDevice, stream);
+  const size_t layer_elems = (size_t)s.rows * T * cfg_.kv_heads * cfg_.head_dim;
+  for (int l = 0; l < cfg_.num_layers && e == hipSuccess; ++l)
+    e = launch_ref_to_records(static_cast<const uint16_t*>(key) + l * layer_elems,
+                              static_cast<const uint16_t*>(value) + l * layer_elems, pool_[l], d_slots, s.rows,
+                              cfg_.kv_heads, (int)T, cfg_.head_dim, stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(stream);
+  hipFree(d_slots);
+  if (e != hipSuccess) {
+    for (int r = 0; r < s.rows; ++r) free_slot(slots[r]);
+    return hip_fail(e, "put_block");
+  }
+  for (int r = 0; r < s.rows; ++r) {
+    s.slot[block_id * s.rows + r] = slots[r];
+    s.host_valid[block_id * s.rows + r] = 0;
+  }
+  s.on_gpu[block_id] = 1;
+  s.n_tokens += T;
+  gpu_bytes_ += block_bytes_all_layers(sid);
+  return kOk;
+}
+
+int PagedKV::get_block(int sid, int64_t block_id, void* key, void* value, hipStream_t stream) {
+  if (sid < 0 || sid >= (int)sessions_.size() || !sessions_[sid].live) return fail(kErrKey, "unknown session");
+  if (in_step_) return fail(kErrState, "get_block during a decode step");
+  Session& s = sessions_[sid];
+  const int64_t T = cfg_.tokens_per_block;
+  if (block_id < 0 || block_id >= s.n_tokens / T) return fail(kErrKey, "block is not a registered full block");
+  const size_t rec = rec_bytes();
+  PGR_HIP(hipStreamSynchronize(stream));
+  PGR_HIP(hipStreamSynchronize(copy_stream_));
+  std::vector<int32_t> slots(s.rows);
+  const bool on_gpu = s.on_gpu[block_id] != 0;
+  int32_t* d_slots = nullptr;
+  PGR_HIP(hipMalloc(&d_slots, sizeof(int32_t) * s.rows));
+  hipError_t e = hipSuccess;
+  const size_t layer_elems = (size_t)s.rows * T * cfg_.kv_heads * cfg_.head_dim;
+  for (int l = 0; l < cfg_.num_layers && e == hipSuccess; ++l) {
+    const void* src = pool_[l];
+    for (int r = 0; r < s.rows; ++r) {
+      if (on_gpu) {
+        slots[r] = s.slot[block_id * s.rows + r];
+      } else {
+        slots[r] = r;
+        const char* h = static_cast<const char*>(host_[l]) + (size_t)(s.row[r].host_off + block_id) * rec;
+        if (e == hipSuccess)
+          e = hipMemcpyAsync(static_cast<char*>(stage_) + (size_t)r * rec, h, rec, hipMemcpyHostToDevice, stream);
+        src = stage_;
+      }
+    }
+    if (e == hipSuccess)
+      e = hipMemcpyAsync(d_slots, slots.data(), sizeof(int32_t) * s.rows, hipMemcpyHostToDevice, stream);
+    if (e == hipSuccess)
+      e = launch_records_to_ref(src, d_slots, static_cast<uint16_t*>(key) + l * layer_elems,
+                                static_cast<uint16_t*>(value) + l * layer_elems, s.rows, cfg_.kv_heads, (int)T,
+                                cfg_.head_dim, stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(stream);
+  }
+  hipFree(d_slots);
+  if (e != hipSuccess) return hip_fail(e, "get_block");
+  return kOk;
+}
+
+double PagedKV::ram_usage_ratio() const {
+  if (ram_budget_ <= 0) return 0.0;
+  return (double)cpu_bytes_ / (double)ram_budget_;
+}
+
+int PagedKV::move_block(Session& s, int64_t b, bool to_gpu, hipStream_t) {
+  const size_t rec = rec_bytes();
+  for (int r = 0; r < s.rows; ++r) {
+    const size_t k = (size_t)b * s.rows + r;
+    if (to_gpu) {
+      const int sl = alloc_slot();
+      if (sl < 0) return fail(kErrCapacity, "HBM pool exhausted while loading a block");
+      s.slot[k] = sl;
+      if (s.host_valid[k]) {
+        for (int l = 0; l < cfg_.num_layers; ++l) {
+          const char* src = static_cast<const char*>(host_[l]) + (size_t)(s.row[r].host_off + b) * rec;
+          char* dst = static_cast<char*>(pool_[l]) + (size_t)sl * rec;
+          PGR_HIP(hipMemcpyAsync(dst, src, rec, hipMemcpyHostToDevice, copy_stream_));
+          stats_.load_bytes_copied += rec;
+        }
+      }
+    } else {
+      const int32_t sl = s.slot[k];
+      if (sl >= 0) {
+        if (!s.host_valid[k]) {
+          for (int l = 0; l < cfg_.num_layers; ++l) {
+            const char* src = static_cast<const char*>(pool_[l]) + (size_t)sl * rec;
+            char* dst = static_cast<char*>(host_[l]) + (size_t)(s.row[r].host_off + b) * rec;
+            PGR_HIP(hipMemcpyAsync(dst, src, rec, hipMemcpyDeviceToHost, copy_stream_));
+            stats_.evict_bytes_copied += rec;
+          }
+          s.host_valid[k] = 1;
+        }
+        // Recycled only by later work ordered after copy_mark_ (see apply_tiers).
+        free_slot(sl);
+        s.slot[k] = -1;
+      }
+    }
+  }
+  s.on_gpu[b] = to_gpu ? 1 : 0;
+  return kOk;
+}
+
+int PagedKV::apply_tiers(int sid, const uint8_t* tiers, int64_t n_tiers, int64_t* to_gpu, int64_t* n_gpu,
+                         int64_t* to_cpu, int64_t* n_cpu, int64_t* fail_block, hipStream_t stream) {
+  if (sid < 0 || sid >= (int)sessions_.size() || !sessions_[sid].live) return fail(kErrKey, "unknown session");
+  if (in_step_) return fail(kErrState, "apply_tiers during a decode step");
+  Session& s = sessions_[sid];
+  const int64_t n_full = s.n_tokens / cfg_.tokens_per_block;
+  const int64_t bb = block_bytes_all_layers(sid);
+  *n_gpu = 0;
+  *n_cpu = 0;
+  *fail_block = -1;
+  // Copies run after everything already queued on the caller's stream (kernels reading
+  // the blocks being evicted), and the caller's stream waits for them before reusing slots.
+  PGR_HIP(hipEventRecord(compute_mark_, stream));
+  PGR_HIP(hipStreamWaitEvent(copy_stream_, compute_mark_, 0));
+  PendingTiming t_cpu{nullptr, nullptr, 0}, t_gpu{nullptr, nullptr, 0};
+  int rc = kOk;
+  for (int64_t b = 0; b < n_full; ++b) {
+    const int desired = b < n_tiers ? tiers[b] : 2;
+    if (desired == 0 && !s.on_gpu[b]) {
+      if (!t_gpu.start) {
+        hipEventCreate(&t_gpu.start);
+        hipEventCreate(&t_gpu.stop);
+        hipEventRecord(t_gpu.start, copy_stream_);
+      }
+      rc = move_block(s, b, true, stream);
+      if (rc != kOk) break;
+      cpu_bytes_ -= bb;
+      gpu_bytes_ += bb;
+      stats_.cpu_to_gpu_bytes += bb;
+      stats_.cpu_to_gpu_copies += 1;
+      to_gpu[(*n_gpu)++] = b;
+    } else if (desired != 0 && s.on_gpu[b]) {
+      if (ram_budget_ >= 0 && cpu_bytes_ + bb > ram_budget_) {
+        *fail_block = b;
+        rc = fail(kErrBudget, "ram_budget exceeded");
+        break;
+      }
+      if (!t_cpu.start) {
+        hipEventCreate(&t_cpu.start);
+        hipEventCreate(&t_cpu.stop);
+        hipEventRecord(t_cpu.start, copy_stream_);
+      }
+      rc = move_block(s, b, false, stream);
+      if (rc != kOk) break;
+      cpu_bytes_ += bb;
+      gpu_bytes_ -= bb;
+      stats_.gpu_to_cpu_bytes += bb;
+      stats_.gpu_to_cpu_copies += 1;
+      to_cpu[(*n_cpu)++] = b;
+    }
+  }
+  if (t_gpu.start) {
+    hipEventRecord(t_gpu.stop, copy_stream_);
+    t_gpu.bytes = 1;  // direction tag: to GPU
+    move_timing_.push_back(t_gpu);
+  }
+  if (t_cpu.start) {
+    hipEventRecord(t_cpu.stop, copy_stream_);
+    t_cpu.bytes = 0;
+    move_timing_.push_back(t_cpu);
+  }
+  PGR_HIP(hipEventRecord(copy_mark_, copy_stream_));
+  PGR_HIP(hipStreamWaitEvent(stream, copy_mark_, 0));
+  return rc;
+}
+
+int PagedKV::ensure_workspace(size_t bytes) {
+  if (bytes <= ws_bytes_) return kOk;
+  PGR_HIP(hipDeviceSynchronize());
+  if (ws_) PGR_HIP(hipFree(ws_));
+  ws_ = nullptr;
+  const size_t want = std::max(bytes, ws_bytes_ * 3 / 2);
+  PGR_HIP(hipMalloc(&ws_, want));
+  ws_bytes_ = want;
+  return kOk;
+}
+
+int PagedKV::begin_step(const int32_t* sids, int n, hipStream_t stream) {
+  if (in_step_) return fail(kErrState, "begin_step while a step is open");
+  const int64_t T = cfg_.tokens_per_block;
+  const int E = std::max(kWaves, cfg_.blocks_per_workgroup);
+  step_sids_.assign(sids, sids + n);
+  step_first_.clear();
+  seqs_.clear();
+  work_.clear();
+  entries_.clear();
+  copies_.clear();
+  append_slot_.clear();
+  append_pos_.clear();
+  step_host_ids_.clear();
+  step_stats_ = StepStats();
+  // Validate and open a block where the new token starts one.
+  for (int i = 0; i < n; ++i) {
+    const int sid = sids[i];
+    if (sid < 0 || sid >= (int)sessions_.size() || !sessions_[sid].live) return fail(kErrKey, "unknown session in step");
+    for (int j = 0; j < i; ++j)
+      if (sids[j] == sid) return fail(kErrInvalid, "session listed twice in one step");
+    Session& s = sessions_[sid];
+    const int64_t p = s.n_tokens;
+    if (p / T + 1 >= s.capacity_blocks) return fail(kErrCapacity, "session capacity reached");
+    if (p % T == 0) {
+      for (int r = 0; r < s.rows; ++r) {
+        if (s.slot[(p / T) * s.rows + r] >= 0) continue;
+        const int sl = alloc_slot();
+        if (sl < 0) return fail(kErrCapacity, "HBM pool exhausted (no slot for the new open block)");
+        s.slot[(p / T) * s.rows + r] = sl;
+      }
+    }
+  }
+  // Per sequence: resident entries now, host runs into chunks of staging records.
+  struct Pending {
+    int seq;
+    BlockEntry e;
+    int launch;
+  };
+  std::vector<Pending> pend;
+  const int64_t chunk_cap = cfg_.staging_slots;
+  int64_t used_in_chunk = 0;
+  int chunk = 0;
+  int max_mass = 1;
+  for (int i = 0; i < n; ++i) {
+    Session& s = sessions_[sids[i]];
+    const int64_t p = s.n_tokens;
+    const int64_t n_full = p / T;
+    step_first_.push_back((int32_t)seqs_.size());
+    for (int r = 0; r < s.rows; ++r) {
+      const int seq = (int)seqs_.size();
+      SeqInfo si{};
+      si.lo = s.row[r].lo;
+      si.hi = (int32_t)(p + 1);
+      si.n_mass = (int32_t)n_full;
+      const int64_t first_blk = std::min<int64_t>(std::max<int64_t>(si.lo, 0) / T, n_full);
+      si.mass_lo = (int32_t)first_blk;
+      si.session = i;
+      seqs_.push_back(si);
+      max_mass = std::max<int>(max_mass, (int)n_full);
+      append_slot_.push_back(s.slot[(p / T) * s.rows + r]);
+      append_pos_.push_back((int32_t)(p % T));
+      std::vector<int64_t> host_ids;
+      int64_t b = first_blk;
+      while (b < n_full) {
+        const int32_t sl = s.slot[b * s.rows + r];
+        if (sl >= 0) {
+          pend.push_back({seq, BlockEntry{sl, (int32_t)b}, 0});
+          step_stats_.resident_tokens += T;
+          ++b;
+          continue;
+        }
+        int64_t e = b;
+        while (e < n_full && s.slot[e * s.rows + r] < 0) ++e;
+        for (int64_t x = b; x < e; ++x) {
+          if (!s.host_valid[x * s.rows + r]) return fail(kErrState, "host block without data (not imported)");
+          host_ids.push_back(x);
+        }
+        int64_t cur = b;
+        while (cur < e) {
+          if (used_in_chunk == chunk_cap) {
+            ++chunk;
+            used_in_chunk = 0;
+          }
+          const int64_t take = std::min(e - cur, chunk_cap - used_in_chunk);
+          const int64_t stage_rec = (int64_t)(chunk % cfg_.staging_buffers) * chunk_cap + used_in_chunk;
+          copies_.push_back(CopyCmd{s.row[r].host_off + cur, stage_rec, take, chunk});
+          for (int64_t x = 0; x < take; ++x)
+            pend.push_back({seq, BlockEntry{(int32_t)(-(stage_rec + x) - 1), (int32_t)(cur + x)}, chunk});
+          used_in_chunk += take;
+          cur += take;
+        }
+        step_stats_.host_blocks += e - b;
+        step_stats_.host_tokens += (e - b) * T;
+        b = e;
+      }
+      // The open block holding the new token.
+      pend.push_back({seq, BlockEntry{s.slot[(p / T) * s.rows + r], (int32_t)(p / T)}, 0});
+      step_stats_.resident_tokens += p % T + 1;
+      step_host_ids_.push_back(std::move(host_ids));
+    }
+  }
+  const bool any_host = !copies_.empty();
+  n_chunks_ = any_host ? chunk + 1 : 0;
+  const int n_launch = std::max(1, n_chunks_);
+  // Workgroups: per launch, per sequence, runs of up to E entries (pend is grouped by sequence
+  // and, within a sequence, by launch order of discovery).
+  std::vector<int> seq_wg(seqs_.size(), 0);
+  launch_work_begin_.assign(n_launch, 0);
+  launch_work_end_.assign(n_launch, 0);
+  std::vector<std::vector<size_t>> by_launch(n_launch);
+  for (size_t i = 0; i < pend.size(); ++i) by_launch[pend[i].launch].push_back(i);
+  for (int L = 0; L < n_launch; ++L) {
+    launch_work_begin_[L] = (int)work_.size();
+    const auto& idx = by_launch[L];
+    size_t i = 0;
+    while (i < idx.size()) {
+      const int seq = pend[idx[i]].seq;
+      WorkItem w{seq, seq_wg[seq]++, (int32_t)entries_.size(), 0};
+      while (i < idx.size() && pend[idx[i]].seq == seq && w.entry_count < E) {
+        entries_.push_back(pend[idx[i]].e);
+        ++w.entry_count;
+        ++i;
+      }
+      work_.push_back(w);
+    }
+    launch_work_end_[L] = (int)work_.size();
+  }
+  int base = 0;
+  for (size_t q = 0; q < seqs_.size(); ++q) {
+    seqs_[q].partial_base = base;
+    seqs_[q].partial_count = seq_wg[q];
+    base += seq_wg[q];
+  }
+  for (WorkItem& w : work_) w.partial += seqs_[w.seq].partial_base;
+  n_partials_ = base;
+  mass_stride_ = max_mass;
+  step_stats_.copies = (int64_t)copies_.size();
+  step_stats_.chunks = n_chunks_;
+  step_stats_.launches = n_launch;
+  step_stats_.work_items = (int64_t)work_.size();
+
+  // Workspace layout.
+  const int S = (int)seqs_.size();
+  const int hq = cfg_.query_heads;
+  std::vector<int32_t> sess_rows, sess_first;
+  for (int i = 0; i < n; ++i) {
+    sess_rows.push_back(sessions_[sids[i]].rows);
+    sess_first.push_back(step_first_[i]);
+  }
+  size_t off = 0;
+  auto carve = [&](size_t bytes) {
+    const size_t at = off;
+    off = align_up(off + bytes, 256);
+    return at;
+  };
+  const size_t o_seqs = carve(sizeof(SeqInfo) * S);
+  const size_t o_work = carve(sizeof(WorkItem) * std::max<size_t>(work_.size(), 1));
+  const size_t o_entries = carve(sizeof(BlockEntry) * std::max<size_t>(entries_.size(), 1));
+  const size_t o_aslot = carve(sizeof(int32_t) * S);
+  const size_t o_apos = carve(sizeof(int32_t) * S);
+  const size_t o_srows = carve(sizeof(int32_t) * std::max(n, 1));
+  const size_t o_sfirst = carve(sizeof(int32_t) * std::max(n, 1));
+  const size_t plan_bytes = off;
+  const size_t o_pm = carve(sizeof(float) * (size_t)n_partials_ * hq);
+  const size_t o_pl = carve(sizeof(float) * (size_t)n_partials_ * hq);
+  const size_t o_pacc = carve(sizeof(float) * (size_t)n_partials_ * hq * cfg_.head_dim);
+  const size_t o_mm = carve(sizeof(float) * (size_t)S * hq * mass_stride_);
+  const size_t o_ms = carve(sizeof(float) * (size_t)S * hq * mass_stride_);
+  const size_t o_mf = carve(sizeof(float) * (size_t)S * hq);
+  const size_t o_lf = carve(sizeof(float) * (size_t)S * hq);
+  int rc = ensure_workspace(off);
+  if (rc != kOk) return rc;
+  // Pinned upload buffer: wait for the previous step's upload before overwriting it.
+  if (plan_bytes > plan_host_bytes_) {
+    PGR_HIP(hipEventSynchronize(plan_uploaded_));
+    if (plan_host_) PGR_HIP(hipHostFree(plan_host_));
+    plan_host_ = nullptr;
+    const size_t want = std::max(plan_bytes, plan_host_bytes_ * 3 / 2);
+    PGR_HIP(hipHostMalloc(&plan_host_, want, hipHostMallocDefault));
+    plan_host_bytes_ = want;
+  } else {
+    PGR_HIP(hipEventSynchronize(plan_uploaded_));
+  }
+  char* h = static_cast<char*>(plan_host_);
+  std::memcpy(h + o_seqs, seqs_.data(), sizeof(SeqInfo) * S);
+  std::memcpy(h + o_work, work_.data(), sizeof(WorkItem) * work_.size());
+  std::memcpy(h + o_entries, entries_.data(), sizeof(BlockEntry) * entries_.size());
+  std::memcpy(h + o_aslot, append_slot_.data(), sizeof(int32_t) * S);
+  std::memcpy(h + o_apos, append_pos_.data(), sizeof(int32_t) * S);
+  std::memcpy(h + o_srows, sess_rows.data(), sizeof(int32_t) * n);
+  std::memcpy(h + o_sfirst, sess_first.data(), sizeof(int32_t) * n);
+  char* d = static_cast<char*>(ws_);
+  PGR_HIP(hipMemcpyAsync(d, h, plan_bytes, hipMemcpyHostToDevice, stream));
+  PGR_HIP(hipEventRecord(plan_uploaded_, stream));
+  d_seqs_ = reinterpret_cast<SeqInfo*>(d + o_seqs);
+  d_work_ = reinterpret_cast<WorkItem*>(d + o_work);
+  d_entries_ = reinterpret_cast<BlockEntry*>(d + o_entries);
+  d_append_slot_ = reinterpret_cast<int32_t*>(d + o_aslot);
+  d_append_pos_ = reinterpret_cast<int32_t*>(d + o_apos);
+  d_sess_rows_ = reinterpret_cast<int32_t*>(d + o_srows);
+  d_sess_first_ = reinterpret_cast<int32_t*>(d + o_sfirst);
+  d_pm_ = reinterpret_cast<float*>(d + o_pm);
+  d_pl_ = reinterpret_cast<float*>(d + o_pl);
+  d_pacc_ = reinterpret_cast<float*>(d + o_pacc);
+  d_mass_m_ = reinterpret_cast<float*>(d + o_mm);
+  d_mass_s_ = reinterpret_cast<float*>(d + o_ms);
+  d_mf_ = reinterpret_cast<float*>(d + o_mf);
+  d_lf_ = reinterpret_cast<float*>(d + o_lf);
+  in_step_ = true;
+  return kOk;
+}
+
+int PagedKV::decode_layer(int layer, const void* q, const void* k_new, const void* v_new, void* out,
+                          float* mass_accum, int64_t accum_stride, float scale, float softcap, hipStream_t stream) {
+  if (!in_step_) return fail(kErrState, "decode_layer outside begin_step/end_step");
+  if (layer < 0 || layer >= cfg_.num_layers) return fail(kErrInvalid, "layer out of range");
+  const int S = (int)seqs_.size();
+  const int hq = cfg_.query_heads;
+  const int T = cfg_.tokens_per_block;
+  const size_t rec = rec_bytes();
+  PGR_HIP(launch_kv_append(k_new, v_new, pool_[layer], d_append_slot_, d_append_pos_, S, cfg_.kv_heads, T,
+                           cfg_.head_dim, stream));
+  PagedLaunch pl{};
+  pl.q = q;
+  pl.pool = pool_[layer];
+  pl.stage = stage_;
+  pl.seqs = d_seqs_;
+  pl.entries = d_entries_;
+  pl.pm = d_pm_;
+  pl.pl = d_pl_;
+  pl.pacc = d_pacc_;
+  pl.mass_m = mass_accum ? d_mass_m_ : nullptr;
+  pl.mass_s = mass_accum ? d_mass_s_ : nullptr;
+  pl.hq = hq;
+  pl.hkv = cfg_.kv_heads;
+  pl.tokens_per_block = T;
+  pl.mass_stride = mass_stride_;
+  pl.scale = scale;
+  pl.softcap = softcap;
+  const int n_launch = (int)launch_work_begin_.size();
+  size_t ci = 0;
+  for (int L = 0; L < n_launch; ++L) {
+    const int buf = L % cfg_.staging_buffers;
+    if (n_chunks_ > 0) {
+      // Side stream: wait until the previous reader of this buffer finished, stream the runs.
+      PGR_HIP(hipStreamWaitEvent(copy_stream_, buf_free_[buf], 0));
+      while (ci < copies_.size() && copies_[ci].chunk == L) {
+        const CopyCmd& c = copies_[ci++];
+        const char* src = static_cast<const char*>(host_[layer]) + (size_t)c.host_rec * rec;
+        char* dst = static_cast<char*>(stage_) + (size_t)c.stage_rec * rec;
+        PGR_HIP(hipMemcpyAsync(dst, src, (size_t)c.count * rec, hipMemcpyHostToDevice, copy_stream_));
+        stats_.stream_bytes += (size_t)c.count * rec;
+        stats_.stream_copies += 1;
+      }
+      PGR_HIP(hipEventRecord(chunk_ready_[buf], copy_stream_));
+      PGR_HIP(hipStreamWaitEvent(stream, chunk_ready_[buf], 0));
+    }
+    pl.work = d_work_ + launch_work_begin_[L];
+    pl.n_work = launch_work_end_[L] - launch_work_begin_[L];
+    PendingTiming t{nullptr, nullptr, 0};
+    if (timing_) {
+      PGR_HIP(hipEventCreate(&t.start));
+      PGR_HIP(hipEventCreate(&t.stop));
+      PGR_HIP(hipEventRecord(t.start, stream));
+    }
+    PGR_HIP(launch_paged(cfg_.dtype, cfg_.head_dim, pl, stream));
+    if (timing_) {
+      PGR_HIP(hipEventRecord(t.stop, stream));
+      int64_t ent = 0;
+      for (int w = launch_work_begin_[L]; w < launch_work_end_[L]; ++w) ent += work_[w].entry_count;
+      t.bytes = ent * (int64_t)T * 2 * cfg_.head_dim * 2 * cfg_.kv_heads;  // K+V bytes read, whole blocks
+      timing_pending_.push_back(t);
+    }
+    if (n_chunks_ > 0) PGR_HIP(hipEventRecord(buf_free_[buf], stream));
+  }
+  PGR_HIP(launch_paged_merge(cfg_.dtype, d_seqs_, S, hq, cfg_.head_dim, d_pm_, d_pl_, d_pacc_, out, d_mf_, d_lf_,
+                             nullptr, stream));
+  if (mass_accum) {
+    PGR_HIP(launch_mass_reduce(d_seqs_, d_sess_rows_, d_sess_first_, d_mass_m_, d_mass_s_, d_mf_, d_lf_, mass_accum,
+                               (int)accum_stride, hq, mass_stride_, (int)step_sids_.size(), mass_stride_, stream));
+  }
+  return kOk;
+}
+
+int PagedKV::end_step(int32_t* completed, int* n_completed) {
+  if (!in_step_) return fail(kErrState, "end_step without begin_step");
+  const int64_t T = cfg_.tokens_per_block;
+  int c = 0;
+  for (size_t i = 0; i < step_sids_.size(); ++i) {
+    Session& s = sessions_[step_sids_[i]];
+    const int64_t p = s.n_tokens;
+    s.n_tokens = p + 1;
+    if ((p + 1) % T == 0) {
+      const int64_t b = p / T;
+      s.on_gpu[b] = 1;
+      for (int r = 0; r < s.rows; ++r) s.host_valid[b * s.rows + r] = 0;
+      gpu_bytes_ += block_bytes_all_layers(step_sids_[i]);
+      if (completed) completed[c] = step_sids_[i];
+      ++c;
+    }
+  }
+  if (n_completed) *n_completed = c;
+  in_step_ = false;
+  return kOk;
+}
+
+int PagedKV::session_info(int sid, int64_t* n_tokens, int64_t* n_full, int64_t* gpu_blocks,
+                          int64_t* cpu_blocks) const {
+  if (sid < 0 || sid >= (int)sessions_.size() || !sessions_[sid].live) return kErrKey;
+  const Session& s = sessions_[sid];
+  const int64_t nf = s.n_tokens / cfg_.tokens_per_block;
+  int64_t g = 0;
+  for (int64_t b = 0; b < nf; ++b) g += s.on_gpu[b];
+  *n_tokens = s.n_tokens;
+  *n_full = nf;
+  *gpu_blocks = g;
+  *cpu_blocks = nf - g;
+  return kOk;
+}
+
+int PagedKV::block_ids(int sid, int gpu, int64_t* out, int64_t cap) const {
+  if (sid < 0 || sid >= (int)sessions_.size() || !sessions_[sid].live) return kErrKey;
+  const Session& s = sessions_[sid];
+  const int64_t nf = s.n_tokens / cfg_.tokens_per_block;
+  int64_t c = 0;
+  for (int64_t b = 0; b < nf; ++b)
+    if ((s.on_gpu[b] != 0) == (gpu != 0)) {
+      if (c < cap) out[c] = b;
+      ++c;
+    }
+  return (int)c;
+}
+
+int PagedKV::step_host_blocks(int seq_index, int64_t* out, int64_t cap) const {
+  if (seq_index < 0 || seq_index >= (int)step_host_ids_.size()) return kErrKey;
+  const auto& v = step_host_ids_[seq_index];
+  for (int64_t i = 0; i < (int64_t)v.size() && i < cap; ++i) out[i] = v[i];
+  return (int)v.size();
+}
+
+int64_t PagedKV::resident_gpu_bytes() const { return gpu_bytes_; }
+int64_t PagedKV::resident_cpu_bytes() const { return cpu_bytes_; }
+
+StoreStats PagedKV::stats() {
+  // Fold finished move timings into the seconds counters.
+  std::vector<PendingTiming> keep;
+  for (auto& t : move_timing_) {
+    if (hipEventQuery(t.stop) == hipSuccess) {
+      float ms = 0.f;
+      hipEventElapsedTime(&ms, t.start, t.stop);
+      if (t.bytes == 1)
+        stats_.cpu_to_gpu_sec += ms / 1000.0;
+      else
+        stats_.gpu_to_cpu_sec += ms / 1000.0;
+      hipEventDestroy(t.start);
+      hipEventDestroy(t.stop);
+    } else {
+      keep.push_back(t);
+    }
+  }
+  move_timing_.swap(keep);
+  return stats_;
+}
+
+int PagedKV::resolve_timing() {
+  for (auto& t : timing_pending_) {
+    PGR_HIP(hipEventSynchronize(t.stop));
+    float ms = 0.f;
+    PGR_HIP(hipEventElapsedTime(&ms, t.start, t.stop));
+    timing_ms_ += ms;
+    timing_launches_ += 1;
+    timing_bytes_ += t.bytes;
+    hipEventDestroy(t.start);
+    hipEventDestroy(t.stop);
+  }
+  timing_pending_.clear();
+  return kOk;
+}
+
+int PagedKV::kernel_time(double* ms, int64_t* launches, int64_t* bytes) {
+  int rc = resolve_timing();
+  if (rc != kOk) return rc;
+  *ms = timing_ms_;
+  *launches = timing_launches_;
+  *bytes = timing_bytes_;
+  timing_ms_ = 0.0;
+  timing_launches_ = 0;
+  timing_bytes_ = 0;
+  return kOk;
+}
+
+int PagedKV::sync() {
+  PGR_HIP(hipStreamSynchronize(copy_stream_));
+  PGR_HIP(hipDeviceSynchronize());
+  return kOk;
+}
+
+}  // namespace pgr

@@ -1,0 +1,222 @@
+// Native paged KV store and streaming decode executor.
+//
+// Memory layout (all of it owned by one PagedKV object):
+//   * HBM pool, one arena per layer: `pool_slots` records. A record holds one block of one
+//     sequence row for one layer: K [Hkv][T][D] then V [Hkv][T][D] (16-bit elements).
+//     A block's slot index is the same in every layer's arena, so one block table serves
+//     all layers.
+//   * Host mirror, one pinned arena per layer: records addressed by (row, block id), each
+//     row owning a contiguous range [host_off, host_off + capacity_blocks). Host-resident
+//     blocks with consecutive ids are therefore one contiguous run, and are streamed to the
+//     GPU with one multi-MiB copy per run.
+//   * Staging ring in HBM: `staging_buffers` buffers of `staging_slots` records, filled by
+//     host-to-device copies on a side stream and read by the attention kernel in place.
+// Blocks are immutable once full, so a host copy stays valid after the block is loaded back
+// to HBM and a later eviction of it needs no copy.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+#include <vector>
+
+#include "pgr_common.h"
+
+namespace pgr {
+
+struct PagedKVConfig {
+  int num_layers = 1;
+  int kv_heads = 0;
+  int query_heads = 0;            // query heads (a multiple of kv_heads, at most 16 per KV head)
+  int head_dim = 0;
+  int tokens_per_block = 0;
+  int dtype = kF16;
+  int64_t pool_slots = 0;        // HBM records per layer
+  int64_t host_records = 0;      // pinned host records per layer
+  int64_t staging_slots = 0;     // records per staging buffer
+  int staging_buffers = 2;       // ring depth
+  int blocks_per_workgroup = 16; // block entries folded by one workgroup (4 waves)
+};
+
+struct StoreStats {
+  // Logical moves, counted the way kv_block_store.py:110-163 counts them.
+  uint64_t gpu_to_cpu_bytes = 0, cpu_to_gpu_bytes = 0;
+  uint64_t gpu_to_cpu_copies = 0, cpu_to_gpu_copies = 0;
+  double gpu_to_cpu_sec = 0.0, cpu_to_gpu_sec = 0.0;
+  // Physical copy traffic issued by this object.
+  uint64_t evict_bytes_copied = 0;    // D2H bytes actually copied (host copy was stale or absent)
+  uint64_t load_bytes_copied = 0;     // H2D bytes into pool slots
+  uint64_t stream_bytes = 0;          // H2D bytes streamed into staging for attention
+  uint64_t stream_copies = 0;         // H2D copy calls for attention streaming
+};
+
+struct StepStats {
+  int64_t resident_tokens = 0;  // in-scope tokens read from the HBM pool (incl. the open block)
+  int64_t host_tokens = 0;      // in-scope tokens streamed from host (whole blocks)
+  int64_t host_blocks = 0;
+  int64_t copies = 0;           // H2D copy calls per layer
+  int64_t chunks = 0;
+  int64_t launches = 0;         // attention kernel launches per layer
+  int64_t work_items = 0;
+};
+
+class PagedKV {
+ public:
+  explicit PagedKV(const PagedKVConfig& cfg);
+  ~PagedKV();
+  int init();  // allocates; returns a Status
+  const std::string& error() const { return err_; }
+
+  // Sessions (rows share placement). Returns the session id or a negative Status.
+  int add_session(int rows, int64_t capacity_tokens, const int32_t* lo_per_row);
+  int remove_session(int sid);
+  int set_lo(int sid, const int32_t* lo_per_row);
+
+  // Setup: write the first n_tokens of one (session, row, layer) from k, v [Hkv, n_src, D]
+  // (device memory, row stride n_src) and set the session length. Blocks go to the pool when
+  // resident, to the host mirror otherwise. Requires the session's token count to be
+  // n_tokens already (set_length) so residency is known.
+  int set_length(int sid, int64_t n_tokens);
+  int import_tokens(int sid, int row, int layer, const void* k, const void* v, int64_t n_src, int64_t n_tokens,
+                    hipStream_t stream);
+  // Read back tokens [0, n) of one (session, row, layer) into k, v [Hkv, n, D] (device).
+  int export_tokens(int sid, int row, int layer, void* k, void* v, int64_t n_tokens, hipStream_t stream);
+
+  // Reference-layout block I/O: key, value [L, B, T, Hkv, D] (device). put_block appends
+  // block `block_id` (== length / T of a block-aligned session) to HBM; get_block copies a
+  // block out wherever it lives.
+  int put_block(int sid, int64_t block_id, const void* key, const void* value, hipStream_t stream);
+  int get_block(int sid, int64_t block_id, void* key, void* value, hipStream_t stream);
+
+  // Placement (kv_block_store.py:206-227 semantics) for full blocks of a session.
+  // tiers[i] == 0 -> HBM, anything else -> host; ids >= n_tiers -> host.
+  // Fills to_gpu / to_cpu (ascending) and returns their counts via *n_gpu / *n_cpu.
+  // On budget overflow returns kErrBudget with *fail_block set; moves done before it stay.
+  int apply_tiers(int sid, const uint8_t* tiers, int64_t n_tiers, int64_t* to_gpu, int64_t* n_gpu, int64_t* to_cpu,
+                  int64_t* n_cpu, int64_t* fail_block, hipStream_t stream);
+  void set_ram_budget(int64_t bytes) { ram_budget_ = bytes; }
+  double ram_usage_ratio() const;
+
+  // Decode step over `sids` (their rows, in order, are the sequences of q/out).
+  int begin_step(const int32_t* sids, int n, hipStream_t stream);
+  int decode_layer(int layer, const void* q, const void* k_new, const void* v_new, void* out, float* mass_accum,
+                   int64_t accum_stride, float scale, float softcap, hipStream_t stream);
+  int end_step(int32_t* completed_sessions, int* n_completed);
+
+  // Introspection.
+  int session_info(int sid, int64_t* n_tokens, int64_t* n_full, int64_t* gpu_blocks, int64_t* cpu_blocks) const;
+  int block_ids(int sid, int gpu, int64_t* out, int64_t cap) const;  // ascending
+  int step_host_blocks(int seq_index, int64_t* out, int64_t cap) const;
+  const StepStats& step_stats() const { return step_stats_; }
+  StoreStats stats();
+  int64_t block_bytes_all_layers(int sid) const;
+  int64_t resident_gpu_bytes() const;
+  int64_t resident_cpu_bytes() const;
+
+  // Optional timing of the attention launches (HIP events on the compute stream).
+  void set_timing(bool on) { timing_ = on; }
+  int kernel_time(double* ms, int64_t* launches, int64_t* bytes);
+  int sync();
+
+  const PagedKVConfig& cfg() const { return cfg_; }
+
+ private:
+  struct Row {
+    int64_t host_off = -1;
+    int32_t lo = 0;
+  };
+  struct Session {
+    bool live = false;
+    int rows = 0;
+    int64_t n_tokens = 0;
+    int64_t capacity_blocks = 0;
+    std::vector<Row> row;
+    // slot[b * rows + r] for block b, row r; -1 when on host.
+    std::vector<int32_t> slot;
+    std::vector<uint8_t> host_valid;  // [b * rows + r]
+    std::vector<uint8_t> on_gpu;      // logical residency per full block [b]
+  };
+  struct CopyCmd {
+    int64_t host_rec;   // first host record
+    int64_t stage_rec;  // first staging record (global index over all buffers)
+    int64_t count;      // records
+    int chunk;
+  };
+  struct PendingTiming {
+    hipEvent_t start, stop;
+    int64_t bytes;
+  };
+
+  int fail(int code, const std::string& msg);
+  int hip_fail(hipError_t e, const char* what);
+  size_t rec_bytes() const;
+  int alloc_slot();
+  void free_slot(int32_t s);
+  int64_t host_alloc(int64_t n);
+  void host_free(int64_t off, int64_t n);
+  int ensure_workspace(size_t bytes);
+  int ensure_block_capacity(Session& s, int64_t blocks);
+  int move_block(Session& s, int64_t b, bool to_gpu, hipStream_t stream);
+  int resolve_timing();
+
+  PagedKVConfig cfg_;
+  std::string err_;
+  std::vector<void*> pool_;   // per layer
+  std::vector<void*> host_;   // per layer (pinned)
+  void* stage_ = nullptr;
+  void* ws_ = nullptr;
+  size_t ws_bytes_ = 0;
+  void* plan_host_ = nullptr;  // pinned upload buffer for the step plan
+  size_t plan_host_bytes_ = 0;
+  hipStream_t copy_stream_ = nullptr;
+  hipEvent_t plan_uploaded_ = nullptr;
+  std::vector<hipEvent_t> buf_free_;
+  std::vector<hipEvent_t> chunk_ready_;
+  hipEvent_t compute_mark_ = nullptr;
+  hipEvent_t copy_mark_ = nullptr;
+  std::vector<int32_t> free_slots_;
+  std::vector<std::pair<int64_t, int64_t>> host_free_;  // (offset, count), sorted by offset
+  std::vector<Session> sessions_;
+  int64_t ram_budget_ = -1;
+  int64_t cpu_bytes_ = 0;
+  int64_t gpu_bytes_ = 0;
+  StoreStats stats_;
+  std::vector<PendingTiming> move_timing_;  // for the *_sec stats
+
+  // Current step.
+  bool in_step_ = false;
+  std::vector<int32_t> step_sids_;
+  std::vector<int32_t> step_first_;  // first sequence index of each session in the step
+  std::vector<SeqInfo> seqs_;
+  std::vector<WorkItem> work_;
+  std::vector<BlockEntry> entries_;
+  std::vector<int> launch_work_begin_;  // per launch: first work item; launches = chunks or 1
+  std::vector<int> launch_work_end_;
+  std::vector<CopyCmd> copies_;
+  std::vector<int32_t> append_slot_, append_pos_;
+  std::vector<std::vector<int64_t>> step_host_ids_;
+  int n_chunks_ = 0;
+  int n_partials_ = 0;
+  int mass_stride_ = 0;
+  int64_t chunk_counter_ = 0;  // global chunk sequence number for ring reuse
+  // Device views into the workspace for the current step.
+  SeqInfo* d_seqs_ = nullptr;
+  WorkItem* d_work_ = nullptr;
+  BlockEntry* d_entries_ = nullptr;
+  int32_t* d_append_slot_ = nullptr;
+  int32_t* d_append_pos_ = nullptr;
+  int32_t* d_sess_rows_ = nullptr;
+  int32_t* d_sess_first_ = nullptr;
+  float *d_pm_ = nullptr, *d_pl_ = nullptr, *d_pacc_ = nullptr;
+  float *d_mass_m_ = nullptr, *d_mass_s_ = nullptr, *d_mf_ = nullptr, *d_lf_ = nullptr;
+  StepStats step_stats_;
+
+  bool timing_ = false;
+  std::vector<PendingTiming> timing_pending_;
+  double timing_ms_ = 0.0;
+  int64_t timing_launches_ = 0;
+  int64_t timing_bytes_ = 0;
+};
+
+}  // namespace pgr

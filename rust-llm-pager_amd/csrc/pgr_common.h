@@ -1,0 +1,58 @@
+// Shared definitions for the native decode-attention library (host and device).
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+
+namespace pgr {
+
+// Element types of Q/K/V/output. Matches PGR_DTYPE_* in include/pgr.h.
+enum DType : int { kF16 = 0, kBF16 = 1 };
+
+// Status codes. Matches PGR_* in include/pgr.h.
+enum Status : int {
+  kOk = 0,
+  kErrInvalid = -1,      // bad argument (shape, null pointer, range)
+  kErrUnsupported = -2,  // valid but unsupported configuration (head_dim, n_rep > 16, ...)
+  kErrHip = -3,          // a HIP runtime call failed
+  kErrCapacity = -4,     // a fixed-capacity pool or workspace is too small
+  kErrState = -5,        // call not valid in the object's current state
+  kErrKey = -6,          // unknown block / sequence id
+  kErrBudget = -7,       // ram budget would be exceeded
+};
+
+// Query heads sharing one KV head are packed into the 16 columns of one MFMA tile.
+constexpr int kMaxRep = 16;
+// Waves per workgroup in the attention kernels.
+constexpr int kWaves = 4;
+constexpr int kWaveSize = 64;
+
+// One workgroup's share of a paged decode step (times num_kv_heads via blockIdx.y).
+struct WorkItem {
+  int32_t seq;          // sequence index: row of q / out
+  int32_t partial;      // partial-result slot written by this workgroup
+  int32_t entry_begin;  // first BlockEntry of this workgroup
+  int32_t entry_count;  // number of BlockEntry records (blocks) it folds
+};
+
+// One KV block as the paged kernel sees it.
+struct BlockEntry {
+  int32_t slot;      // >= 0: record index in the layer's HBM pool; < 0: staging record (-slot - 1)
+  int32_t block_id;  // logical block id within the sequence; first token = block_id * tokens_per_block
+};
+
+// Per-sequence scalars of a paged decode step.
+struct SeqInfo {
+  int32_t lo;            // first valid token position (left padding / sliding window)
+  int32_t hi;            // one past the last valid token (includes the current token)
+  int32_t n_mass;        // blocks [0, n_mass) get a mass entry (the full blocks known before this step)
+  int32_t mass_lo;       // first block id in scope for mass (blocks below were skipped: mass 0)
+  int32_t partial_base;  // first partial slot of this sequence
+  int32_t partial_count; // number of partial slots of this sequence
+  int32_t session;       // session index (rows of one session share placement and mass)
+  int32_t pad_;
+};
+
+inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+}  // namespace pgr

@@ -1,0 +1,72 @@
+// Host-side launchers of the HIP kernels (implemented in attn_kernels.hip, kv_kernels.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "pgr_common.h"
+
+namespace pgr {
+
+struct DenseLaunch {
+  const void* q;
+  const void* k;
+  const void* v;
+  const int32_t* valid;
+  const int32_t* active;
+  float* m;
+  float* l;
+  float* acc;
+  float* block_mass;
+  float* pm;
+  float* pl;
+  float* pacc;
+  int batch, hq, hkv, tc;
+  int wave_tokens, n_split;
+  int tokens_per_block, max_blocks, block_id_offset;
+  float scale, softcap;
+};
+
+struct PagedLaunch {
+  const void* q;
+  const void* pool;
+  const void* stage;
+  const WorkItem* work;
+  const BlockEntry* entries;
+  const SeqInfo* seqs;
+  float* pm;
+  float* pl;
+  float* pacc;
+  float* mass_m;
+  float* mass_s;
+  int n_work, hq, hkv, tokens_per_block, mass_stride;
+  float scale, softcap;
+};
+
+bool head_dim_supported(int d);
+int dense_wave_tokens(int batch, int hkv, int tc, int tokens_per_block, bool mass);
+
+hipError_t launch_dense(int dtype, int mode, int d, const DenseLaunch& p, hipStream_t stream);
+hipError_t launch_finalize(int dtype, const float* acc, const float* l, void* out, int rows, int d,
+                           hipStream_t stream);
+hipError_t launch_paged(int dtype, int d, const PagedLaunch& p, hipStream_t stream);
+hipError_t launch_paged_merge(int dtype, const SeqInfo* seqs, int n_seq, int hq, int d, const float* pm,
+                              const float* pl, const float* pacc, void* out, float* mf, float* lf, float* acc_out,
+                              hipStream_t stream);
+hipError_t launch_mass_reduce(const SeqInfo* seqs, const int32_t* session_rows, const int32_t* session_first,
+                              const float* mass_m, const float* mass_s, const float* mf, const float* lf,
+                              float* mass_accum, int accum_stride, int hq, int mass_stride, int n_sessions,
+                              int max_blocks, hipStream_t stream);
+
+// kv_kernels.hip
+// Write one new token's K/V per sequence into its open block record:
+// k_new, v_new [S, Hkv, D]; slot[S], pos[S] (token offset inside the block).
+hipError_t launch_kv_append(const void* k_new, const void* v_new, void* pool, const int32_t* slots,
+                            const int32_t* pos, int n_seq, int hkv, int tokens_per_block, int d, hipStream_t stream);
+// Reference block layout <-> pool records for one layer:
+// ref [B, T, Hkv, D] (a layer slice of the [L, B, T, Hkv, D] block) <-> records [B][2][Hkv][T][D].
+hipError_t launch_ref_to_records(const void* key, const void* value, void* pool, const int32_t* slots, int rows,
+                                 int hkv, int tokens_per_block, int d, hipStream_t stream);
+hipError_t launch_records_to_ref(const void* pool, const int32_t* slots, void* key, void* value, int rows, int hkv,
+                                 int tokens_per_block, int d, hipStream_t stream);
+
+}  // namespace pgr

@@ -1,0 +1,237 @@
+"""Python handle of the native paged KV store (``pgr_kv_*`` in include/pgr.h).
+
+One NativeKVPool owns, for every layer, an HBM slot pool, a pinned host mirror and an HBM
+staging ring, plus the per-session block tables. Sessions are groups of rows that share one
+placement (the reference's one-PagedModel-per-session model, kv_block_store.py:36-56).
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _native as N
+
+nat = N.nat
+
+
+def _i64_array(n: int):
+    return (ctypes.c_int64 * max(n, 1))()
+
+
+class NativeKVPool:
+    def __init__(
+        self,
+        *,
+        num_layers: int,
+        num_query_heads: int,
+        num_kv_heads: int,
+        head_dim: int,
+        tokens_per_block: int,
+        dtype: torch.dtype,
+        device: torch.device | str = "cuda",
+        pool_blocks: int,
+        host_blocks: int,
+        staging_blocks: int = 2048,
+        staging_buffers: int = 2,
+        blocks_per_workgroup: int = 16,
+    ):
+        self.device = torch.device(device)
+        if self.device.type != "cuda":
+            raise ValueError("NativeKVPool needs a CUDA (HIP) device")
+        if self.device.index is None:
+            self.device = torch.device("cuda", torch.cuda.current_device())
+        self.num_layers = num_layers
+        self.num_query_heads = num_query_heads
+        self.num_kv_heads = num_kv_heads
+        self.head_dim = head_dim
+        self.tokens_per_block = tokens_per_block
+        self.dtype = dtype
+        self.lib = N.lib()
+        cfg = nat.KVConfig(
+            num_layers=num_layers,
+            kv_heads=num_kv_heads,
+            query_heads=num_query_heads,
+            head_dim=head_dim,
+            tokens_per_block=tokens_per_block,
+            dtype=N.dtype_code(dtype),
+            pool_slots=pool_blocks,
+            host_records=host_blocks,
+            staging_slots=staging_blocks,
+            staging_buffers=staging_buffers,
+            blocks_per_workgroup=blocks_per_workgroup,
+        )
+        with torch.cuda.device(self.device):
+            handle = self.lib.pgr_kv_create(ctypes.byref(cfg))
+        if not handle:
+            raise MemoryError(f"pgr_kv_create failed: {nat.last_error()}")
+        self.handle = handle
+        self.record_bytes = 2 * num_kv_heads * tokens_per_block * head_dim * torch.tensor([], dtype=dtype).element_size()
+
+    # -- lifetime ------------------------------------------------------------------------
+    def close(self) -> None:
+        if getattr(self, "handle", None):
+            with torch.cuda.device(self.device):
+                self.lib.pgr_kv_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _stream(self) -> int:
+        return N.stream_of(self.device)
+
+    def _call(self, what: str, fn, *args):
+        with torch.cuda.device(self.device):
+            return nat.check(fn(self.handle, *args), what)
+
+    # -- sessions ------------------------------------------------------------------------
+    def add_session(self, rows: int, capacity_tokens: int, lo=None) -> int:
+        arr = None
+        if lo is not None:
+            arr = (ctypes.c_int32 * rows)(*[int(x) for x in lo])
+        return self._call("add_session", self.lib.pgr_kv_add_session, rows, capacity_tokens, arr)
+
+    def remove_session(self, sid: int) -> None:
+        self._call("remove_session", self.lib.pgr_kv_remove_session, sid)
+
+    def set_lo(self, sid: int, lo) -> None:
+        arr = (ctypes.c_int32 * len(lo))(*[int(x) for x in lo])
+        self._call("set_lo", self.lib.pgr_kv_set_lo, sid, arr)
+
+    def set_length(self, sid: int, n_tokens: int) -> None:
+        self._call("set_length", self.lib.pgr_kv_set_length, sid, n_tokens)
+
+    def import_tokens(self, sid: int, row: int, layer: int, k: torch.Tensor, v: torch.Tensor, n_tokens: int) -> None:
+        """k, v [Hkv, n_src, D] on this device (n_src >= n_tokens)."""
+        k = k.contiguous()
+        v = v.contiguous()
+        self._check_kv(k, v)
+        self._call("import", self.lib.pgr_kv_import, sid, row, layer, k.data_ptr(), v.data_ptr(), k.shape[1],
+                   n_tokens, self._stream())
+
+    def export_tokens(self, sid: int, row: int, layer: int, n_tokens: int):
+        k = torch.empty((self.num_kv_heads, n_tokens, self.head_dim), dtype=self.dtype, device=self.device)
+        v = torch.empty_like(k)
+        if n_tokens:
+            self._call("export", self.lib.pgr_kv_export, sid, row, layer, k.data_ptr(), v.data_ptr(), n_tokens,
+                       self._stream())
+        return k, v
+
+    def put_block(self, sid: int, block_id: int, key: torch.Tensor, value: torch.Tensor) -> None:
+        key = key.contiguous()
+        value = value.contiguous()
+        self._check_kv(key, value)
+        self._call("put_block", self.lib.pgr_kv_put_block, sid, block_id, key.data_ptr(), value.data_ptr(),
+                   self._stream())
+
+    def get_block(self, sid: int, block_id: int, rows: int):
+        shape = (self.num_layers, rows, self.tokens_per_block, self.num_kv_heads, self.head_dim)
+        key = torch.empty(shape, dtype=self.dtype, device=self.device)
+        value = torch.empty_like(key)
+        self._call("get_block", self.lib.pgr_kv_get_block, sid, block_id, key.data_ptr(), value.data_ptr(),
+                   self._stream())
+        return key, value
+
+    def _check_kv(self, k: torch.Tensor, v: torch.Tensor) -> None:
+        if k.device != self.device or v.device != self.device:
+            raise ValueError(f"tensors must be on {self.device}")
+        if k.dtype != self.dtype or v.dtype != self.dtype:
+            raise TypeError(f"tensors must be {self.dtype}")
+
+    # -- placement -----------------------------------------------------------------------
+    def apply_tiers(self, sid: int, tiers) -> tuple[list[int], list[int], int, int]:
+        """Returns (to_gpu, to_cpu, status, fail_block); status PGR_ERR_BUDGET is not raised here."""
+        n = len(tiers)
+        tarr = (ctypes.c_uint8 * max(n, 1))(*[int(t) for t in tiers])
+        info = self.session_info(sid)
+        cap = info[1] + 1
+        to_gpu, to_cpu = _i64_array(cap), _i64_array(cap)
+        n_gpu, n_cpu, fail_block = ctypes.c_int64(0), ctypes.c_int64(0), ctypes.c_int64(-1)
+        with torch.cuda.device(self.device):
+            rc = self.lib.pgr_kv_apply_tiers(
+                self.handle, sid, tarr, n, to_gpu, ctypes.byref(n_gpu), to_cpu, ctypes.byref(n_cpu),
+                ctypes.byref(fail_block), self._stream(),
+            )
+        if rc not in (nat.PGR_OK, nat.PGR_ERR_BUDGET):
+            nat.check(rc, "apply_tiers")
+        return list(to_gpu[: n_gpu.value]), list(to_cpu[: n_cpu.value]), rc, fail_block.value
+
+    def set_ram_budget(self, nbytes: int | None) -> None:
+        self._call("set_ram_budget", self.lib.pgr_kv_set_ram_budget, -1 if nbytes is None else int(nbytes))
+
+    # -- decode ---------------------------------------------------------------------------
+    def begin_step(self, sids) -> None:
+        arr = (ctypes.c_int32 * max(len(sids), 1))(*sids)
+        self._call("begin_step", self.lib.pgr_kv_begin_step, arr, len(sids), self._stream())
+
+    def decode_layer(self, layer: int, q, k_new, v_new, out, mass_accum=None, scale=None, softcap=None) -> None:
+        if scale is None:
+            scale = 1.0 / (self.head_dim**0.5)
+        stride = mass_accum.shape[1] if mass_accum is not None else 0
+        self._call(
+            "decode_layer", self.lib.pgr_kv_decode_layer, layer, q.data_ptr(), k_new.data_ptr(), v_new.data_ptr(),
+            out.data_ptr(), N.ptr(mass_accum), stride, float(scale), float(softcap or 0.0), self._stream(),
+        )
+
+    def end_step(self, n_sessions: int) -> list[int]:
+        arr = (ctypes.c_int32 * max(n_sessions, 1))()
+        n = ctypes.c_int32(0)
+        self._call("end_step", self.lib.pgr_kv_end_step, arr, ctypes.byref(n))
+        return list(arr[: n.value])
+
+    # -- introspection ----------------------------------------------------------------------
+    def session_info(self, sid: int) -> tuple[int, int, int, int]:
+        """(n_tokens, n_full_blocks, gpu_blocks, cpu_blocks)."""
+        info = (ctypes.c_int64 * 4)()
+        nat.check(self.lib.pgr_kv_session_info(self.handle, sid, info), "session_info")
+        return tuple(int(x) for x in info)
+
+    def block_ids(self, sid: int, gpu: bool) -> list[int]:
+        n = nat.check(self.lib.pgr_kv_block_ids(self.handle, sid, int(gpu), None, 0), "block_ids")
+        arr = _i64_array(n)
+        nat.check(self.lib.pgr_kv_block_ids(self.handle, sid, int(gpu), arr, n), "block_ids")
+        return list(arr[:n])
+
+    def step_host_blocks(self, seq: int) -> list[int]:
+        n = nat.check(self.lib.pgr_kv_step_host_blocks(self.handle, seq, None, 0), "step_host_blocks")
+        arr = _i64_array(n)
+        nat.check(self.lib.pgr_kv_step_host_blocks(self.handle, seq, arr, n), "step_host_blocks")
+        return list(arr[:n])
+
+    def step_stats(self) -> dict:
+        s = nat.KVStepStats()
+        nat.check(self.lib.pgr_kv_step_stats(self.handle, ctypes.byref(s)), "step_stats")
+        return {name: getattr(s, name) for name, _ in nat.KVStepStats._fields_}
+
+    def stats(self) -> dict:
+        s = nat.KVStats()
+        nat.check(self.lib.pgr_kv_stats(self.handle, ctypes.byref(s)), "stats")
+        return {name: getattr(s, name) for name, _ in nat.KVStats._fields_}
+
+    def resident_bytes(self) -> tuple[int, int]:
+        g, c = ctypes.c_int64(0), ctypes.c_int64(0)
+        nat.check(self.lib.pgr_kv_resident_bytes(self.handle, ctypes.byref(g), ctypes.byref(c)), "resident_bytes")
+        return g.value, c.value
+
+    def block_bytes(self, sid: int) -> int:
+        b = ctypes.c_int64(0)
+        nat.check(self.lib.pgr_kv_block_bytes(self.handle, sid, ctypes.byref(b)), "block_bytes")
+        return b.value
+
+    def set_timing(self, on: bool) -> None:
+        nat.check(self.lib.pgr_kv_set_timing(self.handle, int(on)), "set_timing")
+
+    def kernel_time(self) -> tuple[float, int, int]:
+        """(milliseconds, launches, K/V bytes read) of timed attention launches since the last call."""
+        ms, launches, nbytes = ctypes.c_double(0), ctypes.c_int64(0), ctypes.c_int64(0)
+        with torch.cuda.device(self.device):
+            nat.check(self.lib.pgr_kv_kernel_time(self.handle, ctypes.byref(ms), ctypes.byref(launches),
+                                                  ctypes.byref(nbytes)), "kernel_time")
+        return ms.value, launches.value, nbytes.value
+
+    def sync(self) -> None:
+        self._call("sync", self.lib.pgr_kv_sync)

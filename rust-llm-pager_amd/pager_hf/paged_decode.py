@@ -1,0 +1,250 @@
+"""Fused streaming decode over many paged sessions: the hot path of the reference's
+patched layer forward (paged_model.py:926-1086) plus its per-step placement glue
+(paged_model.py:768-812), batched across sessions.
+
+Per decode step::
+
+    dec.begin_step(handles)                      # plan: which blocks are resident / streamed
+    for layer in range(num_layers):
+        out = dec.decode_layer(layer, q, k_new, v_new)   # append + attend + mass, one call
+    step_stats = dec.end_step()                  # new blocks -> pager.on_step -> apply_tiers
+
+``q`` is [S, Hq, D] (post-RoPE), ``k_new``/``v_new`` [S, Hkv, D], where the S sequences are
+the rows of the stepped sessions in order. The append writes the new token into the
+session's open block in HBM before attention, so the current token attends to itself
+exactly as in the reference (tail + current token, paged_model.py:955, :984-987). Blocks
+outside the valid range [lo, position] are neither read nor streamed (the reference reads
+and masks them, paged_model.py:961).
+
+Placement glue follows paged_model.py:768-812: with N full blocks after the step,
+``on_step(N - 1, 0, scores)`` then ``force_rebalance(N - 1)`` if a block completed, then
+``apply_tiers(tiers())``. Scores are uniform ``[1/N]*N`` for recent_only / sinks_recent
+(:788-790); otherwise the per-block attention mass of this step, averaged over layers and
+normalized to sum 1 (:865-876), with the reference's length rule (one entry per block known
+before the step; uniform over N if the total is not positive).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import torch
+
+import pager as _pager
+
+from .kv_pool import NativeKVPool
+
+_POLICIES_WITHOUT_ATTENTION_SIGNAL = frozenset({"recent_only", "sinks_recent"})  # paged_model.py:40
+
+
+@dataclass
+class DecodeSession:
+    sid: int
+    rows: int
+    pager: object
+    policy: str
+    needs_attention: bool
+    lo: list[int]
+    step_stats: list[dict] = field(default_factory=list)
+
+
+class PagedDecoder:
+    def __init__(
+        self,
+        *,
+        num_layers: int,
+        num_query_heads: int,
+        num_kv_heads: int,
+        head_dim: int,
+        tokens_per_block: int,
+        dtype: torch.dtype,
+        device: torch.device | str = "cuda",
+        pool_blocks: int,
+        host_blocks: int,
+        staging_blocks: int = 2048,
+        staging_buffers: int = 2,
+        ram_budget_bytes: int | None = None,
+        blocks_per_workgroup: int = 16,
+        scale: float | None = None,
+        softcap: float | None = None,
+    ):
+        self.pool = NativeKVPool(
+            num_layers=num_layers,
+            num_query_heads=num_query_heads,
+            num_kv_heads=num_kv_heads,
+            head_dim=head_dim,
+            tokens_per_block=tokens_per_block,
+            dtype=dtype,
+            device=device,
+            pool_blocks=pool_blocks,
+            host_blocks=host_blocks,
+            staging_blocks=staging_blocks,
+            staging_buffers=staging_buffers,
+            blocks_per_workgroup=blocks_per_workgroup,
+        )
+        self.pool.set_ram_budget(ram_budget_bytes)
+        self.device = self.pool.device
+        self.num_layers = num_layers
+        self.num_query_heads = num_query_heads
+        self.num_kv_heads = num_kv_heads
+        self.head_dim = head_dim
+        self.tokens_per_block = tokens_per_block
+        self.dtype = dtype
+        self.scale = scale
+        self.softcap = softcap
+        self.sessions: dict[int, DecodeSession] = {}
+        self._step: list[int] | None = None
+        self._mass: torch.Tensor | None = None
+        self._n_mass: list[int] = []
+
+    # -- sessions ------------------------------------------------------------------------
+    def add_session(
+        self,
+        *,
+        capacity_tokens: int,
+        rows: int = 1,
+        vram_budget: int,
+        ram_budget: int,
+        recent_window: int = 64,
+        rebalance_interval: int = 4,
+        promote_margin: float = 0.05,
+        ram_promote_margin: float = 0.20,
+        policy: str = "sinks_heavy_hitter",
+        lo: list[int] | None = None,
+    ) -> int:
+        """A new session; the pager arguments and defaults are PagedModel's (paged_model.py:200-215)."""
+        lo = list(lo) if lo is not None else [0] * rows
+        sid = self.pool.add_session(rows, capacity_tokens, lo)
+        pg = _pager.PyPager(vram_budget, ram_budget, recent_window, rebalance_interval, promote_margin,
+                            ram_promote_margin, policy)
+        self.sessions[sid] = DecodeSession(sid, rows, pg, policy, policy not in _POLICIES_WITHOUT_ATTENTION_SIGNAL, lo)
+        return sid
+
+    def remove_session(self, sid: int) -> None:
+        self.pool.remove_session(sid)
+        del self.sessions[sid]
+
+    def set_lo(self, sid: int, lo: list[int]) -> None:
+        """First valid position per row (left padding and/or a sliding window bound)."""
+        self.pool.set_lo(sid, lo)
+        self.sessions[sid].lo = list(lo)
+
+    def prefill(self, sid: int, keys, values, n_tokens: int, *, place: bool = True) -> dict[str, list[int]]:
+        """Install a prompt's KV: keys[layer], values[layer] are [rows, Hkv, n_src, D] on this device.
+
+        With place=True the pager places the blocks right away (on_step over a uniform score
+        then force_rebalance, as a first decode step would) so that host blocks are streamed
+        from the first step; with place=False every full block starts in HBM, like the
+        reference's initial store (paged_model.py:1183-1192).
+        """
+        s = self.sessions[sid]
+        self.pool.set_length(sid, n_tokens)
+        n_blocks = n_tokens // self.tokens_per_block
+        moves = {"to_gpu": [], "to_cpu": []}
+        if n_blocks:
+            if place:
+                s.pager.on_step(n_blocks - 1, 0, [1.0 / n_blocks] * n_blocks)
+                s.pager.force_rebalance(n_blocks - 1)
+                tiers = s.pager.tiers()
+            else:
+                tiers = [0] * n_blocks
+            to_gpu, to_cpu, rc, fail_block = self.pool.apply_tiers(sid, tiers)
+            if rc != 0:
+                raise RuntimeError(f"ram_budget exceeded while placing block {fail_block}")
+            moves = {"to_gpu": to_gpu, "to_cpu": to_cpu}
+        for layer in range(self.num_layers):
+            for row in range(s.rows):
+                self.pool.import_tokens(sid, row, layer, keys[layer][row], values[layer][row], n_tokens)
+        return moves
+
+    def num_blocks(self, sid: int) -> int:
+        return self.pool.session_info(sid)[1]
+
+    def num_tokens(self, sid: int) -> int:
+        return self.pool.session_info(sid)[0]
+
+    # -- decode --------------------------------------------------------------------------
+    def begin_step(self, sids: list[int]) -> None:
+        if self._step is not None:
+            raise RuntimeError("begin_step called while a step is open")
+        self.pool.begin_step(list(sids))
+        self._step = list(sids)
+        self._n_mass = [self.pool.session_info(sid)[0] // self.tokens_per_block for sid in sids]
+        if any(self.sessions[sid].needs_attention for sid in sids):
+            self._mass = torch.zeros((len(sids), max(self._n_mass) + 1), dtype=torch.float32, device=self.device)
+        else:
+            self._mass = None
+
+    def num_sequences(self) -> int:
+        return sum(self.sessions[sid].rows for sid in (self._step or []))
+
+    def decode_layer(self, layer: int, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor,
+                     out: torch.Tensor | None = None) -> torch.Tensor:
+        if self._step is None:
+            raise RuntimeError("decode_layer outside begin_step/end_step")
+        S = self.num_sequences()
+        exp_q = (S, self.num_query_heads, self.head_dim)
+        exp_kv = (S, self.num_kv_heads, self.head_dim)
+        if tuple(q.shape) != exp_q or tuple(k_new.shape) != exp_kv or tuple(v_new.shape) != exp_kv:
+            raise ValueError(f"expected q {exp_q}, k_new/v_new {exp_kv}")
+        for t in (q, k_new, v_new):
+            if t.dtype != self.dtype or t.device != self.device:
+                raise TypeError(f"q/k_new/v_new must be {self.dtype} on {self.device}")
+        q, k_new, v_new = q.contiguous(), k_new.contiguous(), v_new.contiguous()
+        if out is None:
+            out = torch.empty(exp_q, dtype=self.dtype, device=self.device)
+        self.pool.decode_layer(layer, q, k_new, v_new, out, self._mass, self.scale, self.softcap)
+        return out
+
+    def step_host_blocks(self, seq: int) -> list[int]:
+        """Ascending host-resident block ids streamed for sequence `seq` in the open step."""
+        return self.pool.step_host_blocks(seq)
+
+    def end_step(self) -> dict[int, dict]:
+        if self._step is None:
+            raise RuntimeError("end_step without begin_step")
+        sids = self._step
+        mass_rows = None
+        if self._mass is not None:
+            mass_rows = (self._mass / self.num_layers).tolist()  # one device->host sync per step
+        completed = set(self.pool.end_step(len(sids)))
+        self._step = None
+        self._mass = None
+        results = {}
+        for i, sid in enumerate(sids):
+            s = self.sessions[sid]
+            n_blocks = self.pool.session_info(sid)[1]
+            added = [n_blocks - 1] if sid in completed else []
+            stats_before = self.pool.stats()
+            if n_blocks == 0:
+                block_attention: list[float] = []
+                to_gpu, to_cpu = [], []
+            else:
+                if s.needs_attention:
+                    averaged = mass_rows[i][: self._n_mass[i]]
+                    total = sum(averaged)
+                    block_attention = [x / total for x in averaged] if total > 0 else [1.0 / n_blocks] * n_blocks
+                else:
+                    block_attention = [1.0 / n_blocks] * n_blocks
+                query_block = n_blocks - 1
+                s.pager.on_step(query_block, 0, block_attention)
+                if added:
+                    s.pager.force_rebalance(query_block)
+                to_gpu, to_cpu, rc, fail_block = self.pool.apply_tiers(sid, s.pager.tiers())
+                if rc != 0:
+                    raise RuntimeError(f"ram_budget exceeded: moving block {fail_block} to CPU")
+            stats_after = self.pool.stats()
+            gpu_ids = self.pool.block_ids(sid, True)
+            attention_in_gpu = sum(block_attention[b] for b in gpu_ids if b < len(block_attention))
+            st = {
+                "new_blocks": len(added),
+                "added_block_ids": added,
+                "to_gpu": to_gpu,
+                "to_cpu": to_cpu,
+                "gpu_to_cpu_mb": (stats_after["gpu_to_cpu_bytes"] - stats_before["gpu_to_cpu_bytes"]) / 1_000_000,
+                "gpu_to_cpu_copies": stats_after["gpu_to_cpu_copies"] - stats_before["gpu_to_cpu_copies"],
+                "attention_in_gpu": attention_in_gpu,
+                "block_attention": block_attention,
+            }
+            s.step_stats.append(st)
+            results[sid] = st
+        return results

@@ -1,0 +1,185 @@
+"""Fused paged decode (pager_hf.PagedDecoder over libpgr.so) against the CPU oracle.
+
+Per step: attention output within max-abs 2e-3 of the fp32 oracle, and bit-exact
+integer results: the gather index lists (host-resident in-scope block ids per sequence),
+the apply_tiers move lists and the new-block ids. Geometries are the measured
+configurations: Qwen2.5-0.5B layer (14q/2kv, D 64, fp16, 32-token blocks) at 4096 context
+with 8 resident blocks, the same at batch 8 with contexts drawn in [1024, 32768] and 64
+resident blocks over 128 steps, and a Mistral-7B layer (32q/8kv, D 128, bf16) at 131072
+context with a 4096-token window, 32 HBM + 96 host blocks in the window.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.paged_decode import PagedDecodeOracle
+from pager_hf import PagedDecoder
+
+pytestmark = pytest.mark.gpu
+
+MIB16 = 16 * 1024 * 1024
+TOL = 2e-3
+
+
+def np32(t):
+    return t.detach().float().cpu().numpy()
+
+
+class Pair:
+    """A PagedDecoder and the oracle driven with the same inputs."""
+
+    def __init__(self, *, layers, hq, hkv, d, tpb, dtype, pool_blocks, host_blocks, staging_blocks=1024,
+                 blocks_per_workgroup=16):
+        self.dtype = dtype
+        self.dec = PagedDecoder(num_layers=layers, num_query_heads=hq, num_kv_heads=hkv, head_dim=d,
+                                tokens_per_block=tpb, dtype=dtype, device="cuda", pool_blocks=pool_blocks,
+                                host_blocks=host_blocks, staging_blocks=staging_blocks,
+                                blocks_per_workgroup=blocks_per_workgroup)
+        self.ora = PagedDecodeOracle(num_layers=layers, num_query_heads=hq, num_kv_heads=hkv, head_dim=d,
+                                     tokens_per_block=tpb)
+        self.layers, self.hq, self.hkv, self.d, self.tpb = layers, hq, hkv, d, tpb
+        self.sids = []
+
+    def add(self, *, ctx, rows=1, capacity, gen, scale=0.5, zero_before=0, **pager_kw):
+        sid = self.dec.add_session(capacity_tokens=capacity, rows=rows, **pager_kw)
+        self.ora.add_session(sid, rows=rows, **pager_kw)
+        keys, values = [], []
+        for _ in range(self.layers):
+            # Positions before `zero_before` are never in scope; they hold zeros.
+            k = torch.zeros(rows, self.hkv, ctx, self.d, dtype=self.dtype)
+            v = torch.zeros(rows, self.hkv, ctx, self.d, dtype=self.dtype)
+            n = ctx - zero_before
+            k[:, :, zero_before:] = (torch.randn(rows, self.hkv, n, self.d, generator=gen) * scale).to(self.dtype)
+            v[:, :, zero_before:] = (torch.randn(rows, self.hkv, n, self.d, generator=gen) * scale).to(self.dtype)
+            keys.append(k)
+            values.append(v)
+        moves = self.dec.prefill(sid, [k.cuda() for k in keys], [v.cuda() for v in values], ctx)
+        omoves = self.ora.prefill(sid, [np32(k) for k in keys], [np32(v) for v in values], ctx)
+        assert (moves["to_gpu"], moves["to_cpu"]) == tuple(omoves)
+        self.sids.append(sid)
+        return sid
+
+    def set_lo(self, sid, lo):
+        self.dec.set_lo(sid, lo)
+        self.ora.set_lo(sid, lo)
+
+    def step(self, gen, *, compute=True, scale=0.5, sids=None):
+        sids = self.sids if sids is None else sids
+        S = sum(self.dec.sessions[s].rows for s in sids)
+        qs, ks, vs = [], [], []
+        for _ in range(self.layers):
+            qs.append((torch.randn(S, self.hq, self.d, generator=gen) * scale).to(self.dtype))
+            ks.append((torch.randn(S, self.hkv, self.d, generator=gen) * scale).to(self.dtype))
+            vs.append((torch.randn(S, self.hkv, self.d, generator=gen) * scale).to(self.dtype))
+        self.dec.begin_step(sids)
+        outs = [self.dec.decode_layer(l, qs[l].cuda(), ks[l].cuda(), vs[l].cuda()) for l in range(self.layers)]
+        gather = [self.dec.step_host_blocks(i) for i in range(S)]
+        res = self.dec.end_step()
+        ref = self.ora.step(sids, [np32(x) for x in qs], [np32(x) for x in ks], [np32(x) for x in vs],
+                            compute=compute)
+        assert gather == ref["gather"], "gather index lists differ"
+        for sid in sids:
+            got, want = res[sid], ref["placement"][sid]
+            assert got["added_block_ids"] == want["added"]
+            assert (got["to_gpu"], got["to_cpu"]) == (want["to_gpu"], want["to_cpu"])
+        err = None
+        if compute:
+            err = max(np.abs(np32(o) - r).max() for o, r in zip(outs, ref["out"]))
+            assert err < TOL, f"max-abs error {err}"
+        return res, ref, err
+
+
+def test_config1_single_layer_4096_ctx_8_resident():
+    g = torch.Generator().manual_seed(1)
+    p = Pair(layers=1, hq=14, hkv=2, d=64, tpb=32, dtype=torch.float16, pool_blocks=32, host_blocks=256)
+    sid = p.add(ctx=4096, capacity=4096 + 128, gen=g, vram_budget=8 * MIB16, ram_budget=1024 * MIB16,
+                recent_window=7, policy="recent_only")
+    assert p.dec.pool.block_ids(sid, True) == list(range(120, 128))
+    res, ref, err = p.step(g)
+    assert ref["gather"] == [list(range(0, 120))]
+    st = p.dec.pool.step_stats()
+    assert st["host_blocks"] == 120 and st["resident_tokens"] == 8 * 32 + 1
+    for _ in range(40):  # crosses a block boundary: block 128 completes, block 120 is evicted
+        p.step(g)
+    assert p.dec.pool.block_ids(sid, True) == list(range(121, 129))
+
+
+def test_config2_batch8_ragged_contexts_128_steps():
+    g = torch.Generator().manual_seed(2)
+    ctx = torch.randint(1024, 32769, (8,), generator=g).tolist()
+    host_blocks = sum(c // 32 + 8 for c in ctx)
+    p = Pair(layers=1, hq=14, hkv=2, d=64, tpb=32, dtype=torch.float16, pool_blocks=8 * 70, host_blocks=host_blocks)
+    for c in ctx:
+        p.add(ctx=c, capacity=c + 160, gen=g, vram_budget=64 * MIB16, ram_budget=4096 * MIB16, recent_window=63,
+              policy="recent_only")
+    check_at = {0, 1, 31, 32, 63, 64, 100, 127}
+    errs = []
+    for step in range(128):
+        _, _, err = p.step(g, compute=step in check_at)
+        if err is not None:
+            errs.append(err)
+    assert len(errs) == len(check_at)
+    for sid, c in zip(p.sids, ctx):
+        n_full = (c + 128) // 32
+        assert p.dec.pool.block_ids(sid, True) == list(range(n_full - 64, n_full))
+
+
+@pytest.mark.parametrize("staging_blocks", [96, 4096])
+def test_config4_mistral_layer_window_bf16(staging_blocks):
+    """131072 tokens, window 4096: valid iff position > current - 4096 (paged_model.py:981)."""
+    g = torch.Generator().manual_seed(4)
+    ctx, window = 131072, 4096
+    p = Pair(layers=1, hq=32, hkv=8, d=128, tpb=32, dtype=torch.bfloat16, pool_blocks=4 * 40,
+             host_blocks=4 * (ctx // 32 + 8), staging_blocks=staging_blocks)
+    for _ in range(4):
+        p.add(ctx=ctx, capacity=ctx + 64, gen=g, zero_before=ctx - 2 * window, vram_budget=32 * MIB16,
+              ram_budget=8192 * MIB16, recent_window=31, policy="recent_only")
+    for step in range(3):
+        pos = ctx + step  # position of the token this step appends
+        for sid in p.sids:
+            p.set_lo(sid, [pos - window + 1])
+        p.step(g)
+        if step == 0:
+            st = p.dec.pool.step_stats()
+            assert st["host_blocks"] == 4 * 96  # in-window host blocks only
+    assert p.ora.host_ids(p.sids[0], 0)[0] == (ctx + 3 - window) // 32
+
+
+def test_scoring_policy_mass_drives_placement():
+    """sinks_heavy_hitter over two layers: the per-block mass handed to the pager matches the
+    oracle's within float tolerance and, where score gaps are clear, placement is identical."""
+    g = torch.Generator().manual_seed(5)
+    p = Pair(layers=2, hq=32, hkv=4, d=64, tpb=32, dtype=torch.float16, pool_blocks=64, host_blocks=256)
+    sid = p.add(ctx=1500, capacity=1500 + 128, gen=g, scale=1.0, vram_budget=12 * MIB16, ram_budget=512 * MIB16,
+                recent_window=4, rebalance_interval=4, policy="sinks_heavy_hitter")
+    for _ in range(40):
+        res, ref, _ = p.step(g, scale=1.0)
+        got = np.array(res[sid]["block_attention"])
+        want = np.array(ref["placement"][sid]["scores"])
+        assert got.shape == want.shape
+        assert np.abs(got - want).max() < 2e-5
+        assert abs(got.sum() - 1.0) < 1e-5
+
+
+def test_multi_row_session_with_left_padding():
+    g = torch.Generator().manual_seed(6)
+    p = Pair(layers=2, hq=14, hkv=2, d=64, tpb=32, dtype=torch.float16, pool_blocks=64, host_blocks=256)
+    sid = p.add(ctx=700, rows=2, capacity=800, gen=g, vram_budget=6 * MIB16, ram_budget=512 * MIB16,
+                recent_window=5, policy="sinks_recent", lo=[0, 133])
+    for _ in range(10):
+        p.step(g)
+    p.step(g)
+    assert p.ora.host_ids(sid, 1)[0] >= 133 // 32
+
+
+def test_short_prompt_below_one_block():
+    """A prompt shorter than one block: no full blocks, no placement, the open block only."""
+    g = torch.Generator().manual_seed(7)
+    p = Pair(layers=1, hq=14, hkv=2, d=64, tpb=32, dtype=torch.float16, pool_blocks=16, host_blocks=64)
+    sid = p.add(ctx=5, capacity=200, gen=g, vram_budget=2 * MIB16, ram_budget=64 * MIB16, recent_window=1,
+                policy="recent_only")
+    for _ in range(60):
+        p.step(g)
+    assert p.dec.num_tokens(sid) == 65 and p.dec.num_blocks(sid) == 2
