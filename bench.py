@@ -33,17 +33,21 @@ def draw_contexts(seed, batch, lo, hi):
     return torch.randint(lo, hi + 1, (batch,), generator=g).tolist()
 
 
-def build(steps_total):
+def build(steps_total, staging_blocks=2048, staging_buffers=3, blocks_per_wg=16, resident_blocks=None,
+          target_wg=0):
     import torch
 
     from pager_hf import PagedDecoder
 
-    c = CFG
+    c = dict(CFG)
+    if resident_blocks is not None:
+        c["resident_blocks"] = resident_blocks
     ctx = draw_contexts(c["seed"], c["batch"], c["ctx_lo"], c["ctx_hi"])
     dec = PagedDecoder(
         num_layers=1, num_query_heads=c["hq"], num_kv_heads=c["hkv"], head_dim=c["d"], tokens_per_block=c["tpb"],
         dtype=torch.float16, device="cuda", pool_blocks=c["batch"] * (c["resident_blocks"] + 4),
-        host_blocks=sum(n // c["tpb"] + steps_total // c["tpb"] + 8 for n in ctx), staging_blocks=2048,
+        host_blocks=sum(n // c["tpb"] + steps_total // c["tpb"] + 8 for n in ctx), staging_blocks=staging_blocks,
+        staging_buffers=staging_buffers, blocks_per_workgroup=blocks_per_wg, target_workgroups=target_wg,
     )
     gen = torch.Generator(device="cuda").manual_seed(c["seed"])
     sids = []
@@ -73,7 +77,7 @@ def run_steps(dec, sids, q, kn, vn, out, first, count, stats):
         stats["copies"] += st["copies"]
         stats["launches"] += st["launches"]
         dec.decode_layer(0, q[i], kn[i], vn[i], out)
-        dec.end_step()
+        dec.end_step(collect=False)
 
 
 def cpu_baseline(ctx, budget_s=15.0):
@@ -117,6 +121,14 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--staging-blocks", type=int, default=2048, help="records per staging buffer")
+    ap.add_argument("--staging-buffers", type=int, default=3)
+    ap.add_argument("--blocks-per-wg", type=int, default=16, help="largest block count per workgroup")
+    ap.add_argument("--resident-blocks", type=int, default=CFG["resident_blocks"],
+                    help="HBM-resident blocks per sequence (1100 keeps every block resident)")
+    ap.add_argument("--target-wg", type=int, default=0, help="workgroups per attention launch (0 = library default)")
+    ap.add_argument("--calibration-copy-mib", type=int, default=0,
+                    help="after timing, run one device copy of this size (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1).", file=sys.stderr)
@@ -129,7 +141,8 @@ def main() -> int:
         return 2
     c = CFG
     total = args.warmup + args.steps
-    dec, sids, ctx, q, kn, vn, out = build(total)
+    dec, sids, ctx, q, kn, vn, out = build(total, args.staging_blocks, args.staging_buffers, args.blocks_per_wg,
+                                          args.resident_blocks, args.target_wg)
     warm = {"resident_tokens": 0, "host_tokens": 0, "copies": 0, "launches": 0}
     run_steps(dec, sids, q, kn, vn, out, 0, args.warmup, warm)
     torch.cuda.synchronize()
@@ -171,6 +184,7 @@ def main() -> int:
                         "HBM and the rest in pinned host RAM, 1 token appended per sequence per step",
             "contexts": ctx,
             "batch": c["batch"],
+            "staging": {"records_per_buffer": args.staging_blocks, "buffers": args.staging_buffers},
         },
         "tokens_per_s": round(c["batch"] * args.steps / dt, 2),
         "host_link": {
@@ -181,7 +195,7 @@ def main() -> int:
             "bytes_per_step": host_bytes // args.steps,
             "copies_per_step": stats["copies"] / args.steps,
         },
-        "hbm_resident": {"bytes_per_step": hbm_bytes // args.steps},
+        "hbm_resident": {"bytes_per_step": hbm_bytes // args.steps, "blocks_per_sequence": args.resident_blocks},
         "roofline": {
             "bound": "hbm",
             "kernel": "paged_attn_kernel",
@@ -195,8 +209,16 @@ def main() -> int:
             "bytes_per_launch": k_bytes // max(k_launches, 1),
         },
     }
+    if args.calibration_copy_mib:
+        n = args.calibration_copy_mib << 20
+        src = torch.ones(n // 4, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        line["calibration_copy_bytes"] = n
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(ctx, args.cpu_seconds)
+    dec.pool.close()
     print(json.dumps(line), flush=True)
     return 0
 

@@ -140,7 +140,8 @@ typedef struct pgr_kv_config_s {
   int64_t host_records;     /* pinned host records per layer */
   int64_t staging_slots;    /* records per staging buffer */
   int32_t staging_buffers;  /* ring depth, >= 1 (2 = double buffering) */
-  int32_t blocks_per_workgroup;
+  int32_t blocks_per_workgroup; /* most block entries per workgroup (4..16) */
+  int32_t target_workgroups;    /* workgroups a launch aims for (0 = 768) */
 } pgr_kv_config_t;
 
 typedef struct pgr_kv_stats_s {
@@ -205,6 +206,20 @@ int pgr_kv_decode_layer(void* kv, int32_t layer, const void* q, const void* k_ne
  * are written to completed[] (the new block id is then length / T - 1).
  * Replaces _append_new_full_blocks_from_grown_tail, paged_model.py:1210-1233. */
 int pgr_kv_end_step(void* kv, int32_t* completed, int32_t* n_completed);
+/* Attaches a placement handle (pgr_pager_new) to session sid; the store does not own it.
+ * scores_from_mass != 0 for attention-scored policies (mass-driven scores). */
+int pgr_kv_attach_pager(void* kv, int32_t sid, void* pager, int32_t scores_from_mass);
+/* Closes the step like pgr_kv_end_step, then runs the per-step placement glue for every
+ * session of the step that has a pager: scores (uniform, or this step's mass_accum averaged
+ * over num_layers and normalized to sum 1), on_step(N-1), force_rebalance(N-1) when a block
+ * completed, apply_tiers(tiers()). counts[5*i..] = {new block id or -1, n to HBM, n to host,
+ * failing block or -1, n scores}; moves / scores (may be NULL) receive each session's moved
+ * ids (to HBM then to host) and the scores handed to the pager.
+ * Replaces _forward_step's placement tail and _finalize_streaming_block_attention,
+ * paged_model.py:768-812 and :865-876. */
+int pgr_kv_end_step_place(void* kv, const float* mass_accum, int64_t accum_stride, int32_t num_layers,
+                          int32_t* completed, int32_t* n_completed, int64_t* counts, int64_t* moves,
+                          int64_t moves_cap, double* scores, int64_t scores_cap, void* stream);
 /* info[4] = {n_tokens, n_full_blocks, gpu_blocks, cpu_blocks}. */
 int pgr_kv_session_info(void* kv, int32_t sid, int64_t* info);
 /* Ascending full-block ids on HBM (gpu != 0) or host. Returns the count.

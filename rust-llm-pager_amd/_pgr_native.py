@@ -62,6 +62,7 @@ class KVConfig(ctypes.Structure):
         ("staging_slots", c_i64),
         ("staging_buffers", c_i32),
         ("blocks_per_workgroup", c_i32),
+        ("target_workgroups", c_i32),
     ]
 
 
@@ -147,6 +148,11 @@ SIGNATURES: dict[str, tuple] = {
         [c_vp, c_i32, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_f32, c_f32, c_vp],
     ),
     "pgr_kv_end_step": (ctypes.c_int, [c_vp, P(c_i32), P(c_i32)]),
+    "pgr_kv_attach_pager": (ctypes.c_int, [c_vp, c_i32, c_vp, c_i32]),
+    "pgr_kv_end_step_place": (
+        ctypes.c_int,
+        [c_vp, c_vp, c_i64, c_i32, P(c_i32), P(c_i32), P(c_i64), P(c_i64), c_i64, P(c_f64), c_i64, c_vp],
+    ),
     "pgr_kv_session_info": (ctypes.c_int, [c_vp, c_i32, P(c_i64)]),
     "pgr_kv_block_ids": (ctypes.c_int, [c_vp, c_i32, c_i32, P(c_i64), c_i64]),
     "pgr_kv_step_host_blocks": (ctypes.c_int, [c_vp, c_i32, P(c_i64), c_i64]),

@@ -431,7 +431,6 @@ struct PagedArgs {
   const uint16_t* pool;  // layer pool base
   const uint16_t* stage; // staging base
   const WorkItem* work;
-  const BlockEntry* entries;
   const SeqInfo* seqs;
   float* pm;             // [slot][Hq]
   float* pl;
@@ -445,9 +444,8 @@ struct PagedArgs {
 template <class Ty, int D, bool kMass>
 __global__ __launch_bounds__(256) void paged_attn_kernel(PagedArgs a) {
   __shared__ MergeSmem<D> sm;
-  const WorkItem wi = a.work[blockIdx.x];
+  const WorkItem& wi = a.work[blockIdx.x];
   const int h = blockIdx.y;
-  const SeqInfo si = a.seqs[wi.seq];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int g = lane >> 4, n = lane & 15;
   const bool real = n < a.n_rep;
@@ -468,22 +466,30 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(PagedArgs a) {
 
   const int my_blocks = wi.entry_count > wave ? (wi.entry_count - wave + kWaves - 1) / kWaves : 0;
   const int tiles = my_blocks * tiles_per_block;
-  for (int ti = 0; ti < tiles; ++ti) {
+  struct Meta {
+    int t0, block_id, tb;
+  };
+  // Issues the loads of the wave's tile ti (no wait): K row n and four V rows per lane.
+  auto fetch = [&](int ti, Tile<D>& t, Meta& mt) {
     const int e = ti / tiles_per_block, tb = ti - e * tiles_per_block;
-    const BlockEntry be = a.entries[wi.entry_begin + wave + kWaves * e];
+    const BlockEntry be = wi.entries[wave + kWaves * e];
     const uint16_t* base = be.slot >= 0 ? a.pool + (size_t)be.slot * rec : a.stage + (size_t)(-be.slot - 1) * rec;
     const uint16_t* kt = base + head_off + (size_t)tb * 16 * D;
     const uint16_t* vt = base + v_off + head_off + (size_t)tb * 16 * D;
-    const int t0 = be.block_id * T + tb * 16;
-    Tile<D> t;
     load_k<D>(t, kt, n, g);
     const int rows[4] = {4 * g, 4 * g + 1, 4 * g + 2, 4 * g + 3};
     load_v<D>(t, vt, rows, n);
+    mt.t0 = be.block_id * T + tb * 16;
+    mt.block_id = be.block_id;
+    mt.tb = tb;
+  };
+  // Folds one fetched tile into the running (m, l, acc) and the block's mass sum.
+  auto fold = [&](Tile<D>& t, const Meta& mt) {
     bool ok[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int tok = t0 + 4 * g + i;
-      ok[i] = tok >= si.lo && tok < si.hi;
+      const int tok = mt.t0 + 4 * g + i;
+      ok[i] = tok >= wi.lo && tok < wi.hi;
       if (!ok[i]) zero_v_row<D>(t, i);
     }
     const f32x4 s4 = qk_tile<Ty, D>(t, q);
@@ -504,14 +510,48 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(PagedArgs a) {
     m_run = m_new;
     if constexpr (kMass) {
       blk = blk * alpha + psum;
-      if (tb == tiles_per_block - 1) {
+      if (mt.tb == tiles_per_block - 1) {
         const float bs = wave_sum_g(blk);
-        if (g == 0 && real && be.block_id < si.n_mass) {
-          const size_t mi = ((size_t)wi.seq * a.hq + qh) * a.mass_stride + be.block_id;
+        if (g == 0 && real && mt.block_id < wi.n_mass) {
+          const size_t mi = ((size_t)wi.seq * a.hq + qh) * a.mass_stride + mt.block_id;
           a.mass_m[mi] = m_run;
           a.mass_s[mi] = bs;
         }
         blk = 0.f;
+      }
+    }
+  };
+  if constexpr (D <= 64) {
+    // Four tiles in registers as two pairs: while one pair is folded the other pair's loads
+    // are in flight (prefetch distance two tiles, 2 x 4 KiB per wave at head_dim 64).
+    Tile<D> a0, a1, b0, b1;
+    Meta ma0{}, ma1{}, mb0{}, mb1{};
+    if (tiles > 0) fetch(0, a0, ma0);
+    if (tiles > 1) fetch(1, a1, ma1);
+    for (int ti = 0; ti < tiles; ti += 4) {
+      if (ti + 2 < tiles) fetch(ti + 2, b0, mb0);
+      if (ti + 3 < tiles) fetch(ti + 3, b1, mb1);
+      fold(a0, ma0);
+      if (ti + 1 < tiles) fold(a1, ma1);
+      if (ti + 2 < tiles) {
+        if (ti + 4 < tiles) fetch(ti + 4, a0, ma0);
+        if (ti + 5 < tiles) fetch(ti + 5, a1, ma1);
+        fold(b0, mb0);
+        if (ti + 3 < tiles) fold(b1, mb1);
+      }
+    }
+  } else {
+    // head_dim 128: tiles are twice as large; one tile ahead keeps 8 KiB per wave in flight
+    // at a register count that still allows three waves per SIMD.
+    Tile<D> ta, tb;
+    Meta ma{}, mb{};
+    if (tiles > 0) fetch(0, ta, ma);
+    for (int ti = 0; ti < tiles; ti += 2) {
+      if (ti + 1 < tiles) fetch(ti + 1, tb, mb);
+      fold(ta, ma);
+      if (ti + 1 < tiles) {
+        if (ti + 2 < tiles) fetch(ti + 2, ta, ma);
+        fold(tb, mb);
       }
     }
   }
@@ -522,33 +562,77 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(PagedArgs a) {
 }
 
 // Per (sequence, query head): combine the partial slots, write the output in the element
-// type and the final (m, l) for the mass pass. One wave per row.
-template <class Ty>
-__global__ __launch_bounds__(64) void paged_merge_kernel(const SeqInfo* seqs, const float* pm, const float* pl,
-                                                         const float* pacc, uint16_t* out, float* mf_out,
-                                                         float* lf_out, float* acc_out, int hq, int d) {
+// type and the final (m, l) for the mass pass. One 256-thread workgroup per row: the
+// partial weights exp(m_k - m_final) are computed once into LDS, then 256/D thread groups
+// each sum a strided subset of the partials for all D dims and the groups are reduced.
+constexpr int kMergeThreads = 256;
+constexpr int kMergeWeights = 2048;
+
+__device__ __forceinline__ float block_reduce_max(float x, float* red) {
+  for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) red[w] = x;
+  __syncthreads();
+  x = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  __syncthreads();
+  return x;
+}
+
+__device__ __forceinline__ float block_reduce_sum(float x, float* red) {
+  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) red[w] = x;
+  __syncthreads();
+  x = (red[0] + red[1]) + (red[2] + red[3]);
+  __syncthreads();
+  return x;
+}
+
+template <class Ty, int D>
+__global__ __launch_bounds__(kMergeThreads) void paged_merge_kernel(const SeqInfo* seqs, const float* pm,
+                                                                    const float* pl, const float* pacc, uint16_t* out,
+                                                                    float* mf_out, float* lf_out, float* acc_out,
+                                                                    int hq) {
+  constexpr int G = kMergeThreads / D;  // partial groups
+  __shared__ float w_s[kMergeWeights];
+  __shared__ float red[4];
+  __shared__ float part[G][D];
   const int row = blockIdx.x;
   const int s = row / hq, qh = row - s * hq;
   const SeqInfo si = seqs[s];
+  const int tid = threadIdx.x;
   float mf = kNegInf;
-  for (int k = 0; k < si.partial_count; ++k) mf = fmaxf(mf, pm[(size_t)(si.partial_base + k) * hq + qh]);
-  float lf = 0.f;
-  if (mf != kNegInf)
-    for (int k = 0; k < si.partial_count; ++k) {
-      const size_t pi = (size_t)(si.partial_base + k) * hq + qh;
-      lf += pl[pi] * __expf(pm[pi] - mf);
+  for (int k = tid; k < si.partial_count; k += kMergeThreads)
+    mf = fmaxf(mf, pm[(size_t)(si.partial_base + k) * hq + qh]);
+  mf = block_reduce_max(mf, red);
+  const int grp = tid / D, dd = tid - grp * D;
+  float lf_part = 0.f, x = 0.f;
+  for (int k0 = 0; k0 < si.partial_count; k0 += kMergeWeights) {
+    const int cnt = min(kMergeWeights, si.partial_count - k0);
+    for (int k = tid; k < cnt; k += kMergeThreads) {
+      const size_t pi = (size_t)(si.partial_base + k0 + k) * hq + qh;
+      const float w = mf == kNegInf ? 0.f : __expf(pm[pi] - mf);
+      w_s[k] = w;
+      lf_part += pl[pi] * w;
     }
-  for (int dd = threadIdx.x; dd < d; dd += 64) {
-    float x = 0.f;
-    if (mf != kNegInf)
-      for (int k = 0; k < si.partial_count; ++k) {
-        const size_t pi = (size_t)(si.partial_base + k) * hq + qh;
-        x += pacc[pi * d + dd] * __expf(pm[pi] - mf);
-      }
-    out[(size_t)row * d + dd] = Ty::cvt(x / lf);
-    if (acc_out != nullptr) acc_out[(size_t)row * d + dd] = x;
+    __syncthreads();
+    for (int k = grp; k < cnt; k += G) {
+      const size_t pi = (size_t)(si.partial_base + k0 + k) * hq + qh;
+      x += pacc[pi * D + dd] * w_s[k];
+    }
+    __syncthreads();
   }
-  if (threadIdx.x == 0) {
+  const float lf = block_reduce_sum(lf_part, red);
+  part[grp][dd] = x;
+  __syncthreads();
+  if (tid < D) {
+    float acc = 0.f;
+#pragma unroll
+    for (int q = 0; q < G; ++q) acc += part[q][tid];
+    out[(size_t)row * D + tid] = Ty::cvt(acc / lf);
+    if (acc_out != nullptr) acc_out[(size_t)row * D + tid] = acc;
+  }
+  if (tid == 0) {
     mf_out[row] = mf;
     lf_out[row] = lf;
   }
@@ -706,7 +790,6 @@ hipError_t launch_paged(int dtype, int d, const PagedLaunch& p, hipStream_t stre
   a.pool = static_cast<const uint16_t*>(p.pool);
   a.stage = static_cast<const uint16_t*>(p.stage);
   a.work = p.work;
-  a.entries = p.entries;
   a.seqs = p.seqs;
   a.pm = p.pm;
   a.pl = p.pl;
@@ -746,12 +829,19 @@ hipError_t launch_paged_merge(int dtype, const SeqInfo* seqs, int n_seq, int hq,
                               hipStream_t stream) {
   if (n_seq == 0) return hipSuccess;
   dim3 grid(n_seq * hq);
-  if (dtype == kF16)
-    paged_merge_kernel<F16><<<grid, 64, 0, stream>>>(seqs, pm, pl, pacc, static_cast<uint16_t*>(out), mf, lf, acc_out,
-                                                     hq, d);
-  else
-    paged_merge_kernel<BF16><<<grid, 64, 0, stream>>>(seqs, pm, pl, pacc, static_cast<uint16_t*>(out), mf, lf,
-                                                      acc_out, hq, d);
+  uint16_t* o = static_cast<uint16_t*>(out);
+#define PGR_MERGE(TY, DD) \
+  paged_merge_kernel<TY, DD><<<grid, kMergeThreads, 0, stream>>>(seqs, pm, pl, pacc, o, mf, lf, acc_out, hq)
+  if (dtype == kF16) {
+    if (d == 32) PGR_MERGE(F16, 32);
+    else if (d == 64) PGR_MERGE(F16, 64);
+    else PGR_MERGE(F16, 128);
+  } else {
+    if (d == 32) PGR_MERGE(BF16, 32);
+    else if (d == 64) PGR_MERGE(BF16, 64);
+    else PGR_MERGE(BF16, 128);
+  }
+#undef PGR_MERGE
   return hipGetLastError();
 }
 

@@ -261,6 +261,7 @@ void* pgr_kv_create(const pgr_kv_config_t* c) {
   cfg.staging_slots = c->staging_slots;
   cfg.staging_buffers = c->staging_buffers;
   cfg.blocks_per_workgroup = c->blocks_per_workgroup > 0 ? c->blocks_per_workgroup : 16;
+  cfg.target_workgroups = c->target_workgroups > 0 ? c->target_workgroups : 768;
   auto* kv = new (std::nothrow) pgr::PagedKV(cfg);
   if (!kv) {
     set_err(pgr::kErrCapacity, "out of host memory");
@@ -350,6 +351,23 @@ int pgr_kv_end_step(void* kv, int32_t* completed, int32_t* n_completed) {
   if (!kv) return set_err(pgr::kErrInvalid, "null store");
   int c = 0;
   const int rc = kv_of(kv)->end_step(completed, &c);
+  if (n_completed) *n_completed = c;
+  return kv_rc(kv_of(kv), rc);
+}
+
+int pgr_kv_attach_pager(void* kv, int32_t sid, void* pager, int32_t scores_from_mass) {
+  if (!kv) return set_err(pgr::kErrInvalid, "null store");
+  return kv_rc(kv_of(kv), kv_of(kv)->attach_pager(sid, static_cast<pgr::PlacementPager*>(pager), scores_from_mass));
+}
+
+int pgr_kv_end_step_place(void* kv, const float* mass_accum, int64_t accum_stride, int32_t num_layers,
+                          int32_t* completed, int32_t* n_completed, int64_t* counts, int64_t* moves,
+                          int64_t moves_cap, double* scores, int64_t scores_cap, void* stream) {
+  if (!kv) return set_err(pgr::kErrInvalid, "null store");
+  if (num_layers <= 0) return set_err(pgr::kErrInvalid, "num_layers must be positive");
+  int c = 0;
+  const int rc = kv_of(kv)->end_step_place(mass_accum, accum_stride, num_layers, as_stream(stream), completed, &c,
+                                           counts, moves, moves_cap, scores, scores_cap);
   if (n_completed) *n_completed = c;
   return kv_rc(kv_of(kv), rc);
 }

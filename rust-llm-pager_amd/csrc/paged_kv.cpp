@@ -11,6 +11,7 @@
 #include <algorithm>
 #include <cstring>
 
+#include "pager_core.h"
 #include "pgr_kernels.h"
 
 namespace pgr {
@@ -79,6 +80,7 @@ PagedKV::~PagedKV() {
   if (stage_) hipFree(stage_);
   if (ws_) hipFree(ws_);
   if (plan_host_) hipHostFree(plan_host_);
+  if (mass_host_) hipHostFree(mass_host_);
   for (hipEvent_t e : buf_free_) hipEventDestroy(e);
   for (hipEvent_t e : chunk_ready_) hipEventDestroy(e);
   for (auto& t : timing_pending_) {
@@ -542,13 +544,22 @@ int PagedKV::apply_tiers(int sid, const uint8_t* tiers, int64_t n_tiers, int64_t
   *fail_block = -1;
   // Copies run after everything already queued on the caller's stream (kernels reading
   // the blocks being evicted), and the caller's stream waits for them before reusing slots.
-  PGR_HIP(hipEventRecord(compute_mark_, stream));
-  PGR_HIP(hipStreamWaitEvent(copy_stream_, compute_mark_, 0));
+  // Both orderings are set up on the first move only: a call that moves nothing leaves the
+  // two streams independent.
+  bool ordered = false;
+  auto order_streams = [&]() -> int {
+    if (ordered) return kOk;
+    ordered = true;
+    PGR_HIP(hipEventRecord(compute_mark_, stream));
+    PGR_HIP(hipStreamWaitEvent(copy_stream_, compute_mark_, 0));
+    return kOk;
+  };
   PendingTiming t_cpu{nullptr, nullptr, 0}, t_gpu{nullptr, nullptr, 0};
   int rc = kOk;
   for (int64_t b = 0; b < n_full; ++b) {
     const int desired = b < n_tiers ? tiers[b] : 2;
     if (desired == 0 && !s.on_gpu[b]) {
+      if ((rc = order_streams()) != kOk) break;
       if (!t_gpu.start) {
         hipEventCreate(&t_gpu.start);
         hipEventCreate(&t_gpu.stop);
@@ -567,6 +578,7 @@ int PagedKV::apply_tiers(int sid, const uint8_t* tiers, int64_t n_tiers, int64_t
         rc = fail(kErrBudget, "ram_budget exceeded");
         break;
       }
+      if ((rc = order_streams()) != kOk) break;
       if (!t_cpu.start) {
         hipEventCreate(&t_cpu.start);
         hipEventCreate(&t_cpu.stop);
@@ -591,8 +603,10 @@ int PagedKV::apply_tiers(int sid, const uint8_t* tiers, int64_t n_tiers, int64_t
     t_cpu.bytes = 0;
     move_timing_.push_back(t_cpu);
   }
-  PGR_HIP(hipEventRecord(copy_mark_, copy_stream_));
-  PGR_HIP(hipStreamWaitEvent(stream, copy_mark_, 0));
+  if (ordered) {
+    PGR_HIP(hipEventRecord(copy_mark_, copy_stream_));
+    PGR_HIP(hipStreamWaitEvent(stream, copy_mark_, 0));
+  }
   return rc;
 }
 
@@ -610,12 +624,12 @@ int PagedKV::ensure_workspace(size_t bytes) {
 int PagedKV::begin_step(const int32_t* sids, int n, hipStream_t stream) {
   if (in_step_) return fail(kErrState, "begin_step while a step is open");
   const int64_t T = cfg_.tokens_per_block;
-  const int E = std::max(kWaves, cfg_.blocks_per_workgroup);
+  const int E_max = std::min(kMaxWorkEntries, std::max(kWaves, cfg_.blocks_per_workgroup));
+  const int64_t kTargetWorkgroups = std::max(1, cfg_.target_workgroups);
   step_sids_.assign(sids, sids + n);
   step_first_.clear();
   seqs_.clear();
   work_.clear();
-  entries_.clear();
   copies_.clear();
   append_slot_.clear();
   append_pos_.clear();
@@ -691,7 +705,7 @@ int PagedKV::begin_step(const int32_t* sids, int n, hipStream_t stream) {
             used_in_chunk = 0;
           }
           const int64_t take = std::min(e - cur, chunk_cap - used_in_chunk);
-          const int64_t stage_rec = (int64_t)(chunk % cfg_.staging_buffers) * chunk_cap + used_in_chunk;
+          const int64_t stage_rec = (int64_t)((stage_base_ + chunk) % cfg_.staging_buffers) * chunk_cap + used_in_chunk;
           copies_.push_back(CopyCmd{s.row[r].host_off + cur, stage_rec, take, chunk});
           for (int64_t x = 0; x < take; ++x)
             pend.push_back({seq, BlockEntry{(int32_t)(-(stage_rec + x) - 1), (int32_t)(cur + x)}, chunk});
@@ -710,6 +724,10 @@ int PagedKV::begin_step(const int32_t* sids, int n, hipStream_t stream) {
   }
   const bool any_host = !copies_.empty();
   n_chunks_ = any_host ? chunk + 1 : 0;
+  // The next step starts on the buffer after this step's last one, so its first copy does
+  // not wait for this step's last reader.
+  step_stage_base_ = stage_base_;
+  stage_base_ = (stage_base_ + n_chunks_) % cfg_.staging_buffers;
   const int n_launch = std::max(1, n_chunks_);
   // Workgroups: per launch, per sequence, runs of up to E entries (pend is grouped by sequence
   // and, within a sequence, by launch order of discovery).
@@ -721,13 +739,22 @@ int PagedKV::begin_step(const int32_t* sids, int n, hipStream_t stream) {
   for (int L = 0; L < n_launch; ++L) {
     launch_work_begin_[L] = (int)work_.size();
     const auto& idx = by_launch[L];
+    // Blocks per workgroup: enough that the launch needs about kTargetWorkgroups workgroups
+    // (4 resident per CU, 16 waves): one round, each wave streaming several blocks, between
+    // one block per wave and the configured maximum.
+    const int64_t per_wg = ((int64_t)idx.size() * cfg_.kv_heads + kTargetWorkgroups - 1) / kTargetWorkgroups;
+    const int E = (int)std::max<int64_t>(kWaves, std::min<int64_t>(E_max, (per_wg + kWaves - 1) / kWaves * kWaves));
     size_t i = 0;
     while (i < idx.size()) {
       const int seq = pend[idx[i]].seq;
-      WorkItem w{seq, seq_wg[seq]++, (int32_t)entries_.size(), 0};
+      WorkItem w{};
+      w.seq = seq;
+      w.partial = seq_wg[seq]++;
+      w.lo = seqs_[seq].lo;
+      w.hi = seqs_[seq].hi;
+      w.n_mass = seqs_[seq].n_mass;
       while (i < idx.size() && pend[idx[i]].seq == seq && w.entry_count < E) {
-        entries_.push_back(pend[idx[i]].e);
-        ++w.entry_count;
+        w.entries[w.entry_count++] = pend[idx[i]].e;
         ++i;
       }
       work_.push_back(w);
@@ -764,7 +791,6 @@ int PagedKV::begin_step(const int32_t* sids, int n, hipStream_t stream) {
   };
   const size_t o_seqs = carve(sizeof(SeqInfo) * S);
   const size_t o_work = carve(sizeof(WorkItem) * std::max<size_t>(work_.size(), 1));
-  const size_t o_entries = carve(sizeof(BlockEntry) * std::max<size_t>(entries_.size(), 1));
   const size_t o_aslot = carve(sizeof(int32_t) * S);
   const size_t o_apos = carve(sizeof(int32_t) * S);
   const size_t o_srows = carve(sizeof(int32_t) * std::max(n, 1));
@@ -793,7 +819,6 @@ int PagedKV::begin_step(const int32_t* sids, int n, hipStream_t stream) {
   char* h = static_cast<char*>(plan_host_);
   std::memcpy(h + o_seqs, seqs_.data(), sizeof(SeqInfo) * S);
   std::memcpy(h + o_work, work_.data(), sizeof(WorkItem) * work_.size());
-  std::memcpy(h + o_entries, entries_.data(), sizeof(BlockEntry) * entries_.size());
   std::memcpy(h + o_aslot, append_slot_.data(), sizeof(int32_t) * S);
   std::memcpy(h + o_apos, append_pos_.data(), sizeof(int32_t) * S);
   std::memcpy(h + o_srows, sess_rows.data(), sizeof(int32_t) * n);
@@ -803,7 +828,6 @@ int PagedKV::begin_step(const int32_t* sids, int n, hipStream_t stream) {
   PGR_HIP(hipEventRecord(plan_uploaded_, stream));
   d_seqs_ = reinterpret_cast<SeqInfo*>(d + o_seqs);
   d_work_ = reinterpret_cast<WorkItem*>(d + o_work);
-  d_entries_ = reinterpret_cast<BlockEntry*>(d + o_entries);
   d_append_slot_ = reinterpret_cast<int32_t*>(d + o_aslot);
   d_append_pos_ = reinterpret_cast<int32_t*>(d + o_apos);
   d_sess_rows_ = reinterpret_cast<int32_t*>(d + o_srows);
@@ -834,7 +858,6 @@ int PagedKV::decode_layer(int layer, const void* q, const void* k_new, const voi
   pl.pool = pool_[layer];
   pl.stage = stage_;
   pl.seqs = d_seqs_;
-  pl.entries = d_entries_;
   pl.pm = d_pm_;
   pl.pl = d_pl_;
   pl.pacc = d_pacc_;
@@ -849,7 +872,7 @@ int PagedKV::decode_layer(int layer, const void* q, const void* k_new, const voi
   const int n_launch = (int)launch_work_begin_.size();
   size_t ci = 0;
   for (int L = 0; L < n_launch; ++L) {
-    const int buf = L % cfg_.staging_buffers;
+    const int buf = (step_stage_base_ + L) % cfg_.staging_buffers;
     if (n_chunks_ > 0) {
       // Side stream: wait until the previous reader of this buffer finished, stream the runs.
       PGR_HIP(hipStreamWaitEvent(copy_stream_, buf_free_[buf], 0));
@@ -910,6 +933,108 @@ int PagedKV::end_step(int32_t* completed, int* n_completed) {
   }
   if (n_completed) *n_completed = c;
   in_step_ = false;
+  return kOk;
+}
+
+int PagedKV::attach_pager(int sid, PlacementPager* pager, bool scores_from_mass) {
+  if (sid < 0 || sid >= (int)sessions_.size() || !sessions_[sid].live) return fail(kErrKey, "unknown session");
+  sessions_[sid].pager = pager;
+  sessions_[sid].scores_from_mass = scores_from_mass;
+  return kOk;
+}
+
+int PagedKV::end_step_place(const float* mass_accum, int64_t accum_stride, int num_layers, hipStream_t stream,
+                            int32_t* completed, int* n_completed, int64_t* counts, int64_t* moves,
+                            int64_t moves_cap, double* scores, int64_t scores_cap) {
+  if (!in_step_) return fail(kErrState, "end_step_place without begin_step");
+  const int64_t T = cfg_.tokens_per_block;
+  const std::vector<int32_t> sids = step_sids_;
+  const int n = (int)sids.size();
+  std::vector<int64_t> n_mass_old(n);
+  bool need_mass = false;
+  for (int i = 0; i < n; ++i) {
+    const Session& s = sessions_[sids[i]];
+    n_mass_old[i] = s.n_tokens / T;
+    need_mass = need_mass || (s.pager && s.scores_from_mass);
+  }
+  if (need_mass) {
+    if (!mass_accum || accum_stride <= 0) return fail(kErrInvalid, "scoring policy needs the mass accumulator");
+    const size_t want = (size_t)n * accum_stride;
+    if (want > mass_host_floats_) {
+      PGR_HIP(hipStreamSynchronize(stream));
+      if (mass_host_) PGR_HIP(hipHostFree(mass_host_));
+      mass_host_ = nullptr;
+      PGR_HIP(hipHostMalloc(reinterpret_cast<void**>(&mass_host_), want * sizeof(float), hipHostMallocDefault));
+      mass_host_floats_ = want;
+    }
+    // The reference reads the mass back with .tolist() (a full sync) at this point too.
+    PGR_HIP(hipMemcpyAsync(mass_host_, mass_accum, want * sizeof(float), hipMemcpyDeviceToHost, stream));
+    PGR_HIP(hipStreamSynchronize(stream));
+  }
+  std::vector<int32_t> done(n);
+  int n_done = 0;
+  int rc = end_step(done.data(), &n_done);
+  if (rc != kOk) return rc;
+  if (completed)
+    for (int i = 0; i < n_done; ++i) completed[i] = done[i];
+  if (n_completed) *n_completed = n_done;
+  int64_t mo = 0, so = 0;
+  std::vector<float> fscores;
+  std::vector<double> dscores;
+  std::vector<uint8_t> tiers;
+  for (int i = 0; i < n; ++i) {
+    const int sid = sids[i];
+    Session& s = sessions_[sid];
+    int64_t* c = counts ? counts + 5 * i : nullptr;
+    const int64_t n_blocks = s.n_tokens / T;
+    const bool added = std::find(done.begin(), done.begin() + n_done, sid) != done.begin() + n_done;
+    if (c) {
+      c[0] = added ? n_blocks - 1 : -1;
+      c[1] = c[2] = c[4] = 0;
+      c[3] = -1;
+    }
+    if (!s.pager || n_blocks == 0) continue;
+    // paged_model.py:781-790 and :865-876.
+    dscores.clear();
+    if (s.scores_from_mass) {
+      const float* row = mass_host_ + (size_t)i * accum_stride;
+      std::vector<float> averaged(n_mass_old[i]);
+      double total = 0.0;
+      for (int64_t b = 0; b < n_mass_old[i]; ++b) {
+        averaged[b] = row[b] / (float)num_layers;  // fp32 tensor / int
+        total += (double)averaged[b];
+      }
+      if (total > 0.0)
+        for (int64_t b = 0; b < n_mass_old[i]; ++b) dscores.push_back((double)averaged[b] / total);
+    }
+    // Score-free policy, or no positive mass: uniform over the blocks after the step.
+    if (dscores.empty()) dscores.assign(n_blocks, 1.0 / (double)n_blocks);
+    fscores.assign(dscores.size(), 0.f);
+    for (size_t b = 0; b < dscores.size(); ++b) fscores[b] = (float)dscores[b];
+    if (scores && so + (int64_t)dscores.size() <= scores_cap)
+      std::copy(dscores.begin(), dscores.end(), scores + so);
+    so += (int64_t)dscores.size();
+    if (c) c[4] = (int64_t)dscores.size();
+    if (!s.pager->on_step((uint64_t)(n_blocks - 1), fscores.data(), fscores.size()))
+      return fail(kErrState, "attempt to calculate the remainder with a divisor of zero");
+    if (added) s.pager->force_rebalance((uint64_t)(n_blocks - 1));
+    tiers.assign(s.pager->num_blocks(), 0);
+    s.pager->tiers(tiers.data());
+    std::vector<int64_t> tg(n_blocks + 1), tc(n_blocks + 1);
+    int64_t ng = 0, nc = 0, fb = -1;
+    rc = apply_tiers(sid, tiers.data(), (int64_t)tiers.size(), tg.data(), &ng, tc.data(), &nc, &fb, stream);
+    if (c) {
+      c[1] = ng;
+      c[2] = nc;
+      c[3] = fb;
+    }
+    if (moves && mo + ng + nc <= moves_cap) {
+      std::copy(tg.begin(), tg.begin() + ng, moves + mo);
+      std::copy(tc.begin(), tc.begin() + nc, moves + mo + ng);
+    }
+    mo += ng + nc;
+    if (rc != kOk) return rc;
+  }
   return kOk;
 }
 

@@ -25,6 +25,8 @@
 
 namespace pgr {
 
+class PlacementPager;
+
 struct PagedKVConfig {
   int num_layers = 1;
   int kv_heads = 0;
@@ -36,7 +38,8 @@ struct PagedKVConfig {
   int64_t host_records = 0;      // pinned host records per layer
   int64_t staging_slots = 0;     // records per staging buffer
   int staging_buffers = 2;       // ring depth
-  int blocks_per_workgroup = 16; // block entries folded by one workgroup (4 waves)
+  int blocks_per_workgroup = 16; // most block entries folded by one workgroup (4 waves)
+  int target_workgroups = 768;   // workgroups a launch aims for: 3 resident per CU
 };
 
 struct StoreStats {
@@ -104,6 +107,18 @@ class PagedKV {
                    int64_t accum_stride, float scale, float softcap, hipStream_t stream);
   int end_step(int32_t* completed_sessions, int* n_completed);
 
+  // Per-step placement glue of paged_model.py:768-812 for sessions with an attached pager:
+  // scores (uniform, or this step's block mass averaged over layers and normalized), then
+  // pager on_step(N-1), force_rebalance(N-1) if a block completed, apply_tiers(tiers()).
+  // Closes the step like end_step. counts gets 5 values per session of the step:
+  // {new block id or -1, n moved to HBM, n moved to host, failing block or -1, n scores};
+  // moves gets each session's to-HBM then to-host ids, scores the values handed to the
+  // pager (before f32 rounding); both may be null.
+  int attach_pager(int sid, PlacementPager* pager, bool scores_from_mass);
+  int end_step_place(const float* mass_accum, int64_t accum_stride, int num_layers, hipStream_t stream,
+                     int32_t* completed, int* n_completed, int64_t* counts, int64_t* moves, int64_t moves_cap,
+                     double* scores, int64_t scores_cap);
+
   // Introspection.
   int session_info(int sid, int64_t* n_tokens, int64_t* n_full, int64_t* gpu_blocks, int64_t* cpu_blocks) const;
   int block_ids(int sid, int gpu, int64_t* out, int64_t cap) const;  // ascending
@@ -136,6 +151,8 @@ class PagedKV {
     std::vector<int32_t> slot;
     std::vector<uint8_t> host_valid;  // [b * rows + r]
     std::vector<uint8_t> on_gpu;      // logical residency per full block [b]
+    PlacementPager* pager = nullptr;  // not owned
+    bool scores_from_mass = false;
   };
   struct CopyCmd {
     int64_t host_rec;   // first host record
@@ -169,6 +186,8 @@ class PagedKV {
   size_t ws_bytes_ = 0;
   void* plan_host_ = nullptr;  // pinned upload buffer for the step plan
   size_t plan_host_bytes_ = 0;
+  float* mass_host_ = nullptr;  // pinned readback of the step's block mass
+  size_t mass_host_floats_ = 0;
   hipStream_t copy_stream_ = nullptr;
   hipEvent_t plan_uploaded_ = nullptr;
   std::vector<hipEvent_t> buf_free_;
@@ -190,7 +209,6 @@ class PagedKV {
   std::vector<int32_t> step_first_;  // first sequence index of each session in the step
   std::vector<SeqInfo> seqs_;
   std::vector<WorkItem> work_;
-  std::vector<BlockEntry> entries_;
   std::vector<int> launch_work_begin_;  // per launch: first work item; launches = chunks or 1
   std::vector<int> launch_work_end_;
   std::vector<CopyCmd> copies_;
@@ -199,11 +217,11 @@ class PagedKV {
   int n_chunks_ = 0;
   int n_partials_ = 0;
   int mass_stride_ = 0;
-  int64_t chunk_counter_ = 0;  // global chunk sequence number for ring reuse
+  int stage_base_ = 0;       // staging buffer of the next step's first chunk
+  int step_stage_base_ = 0;  // staging buffer of the open step's first chunk
   // Device views into the workspace for the current step.
   SeqInfo* d_seqs_ = nullptr;
   WorkItem* d_work_ = nullptr;
-  BlockEntry* d_entries_ = nullptr;
   int32_t* d_append_slot_ = nullptr;
   int32_t* d_append_pos_ = nullptr;
   int32_t* d_sess_rows_ = nullptr;

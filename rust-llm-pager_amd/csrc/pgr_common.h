@@ -27,18 +27,26 @@ constexpr int kMaxRep = 16;
 constexpr int kWaves = 4;
 constexpr int kWaveSize = 64;
 
-// One workgroup's share of a paged decode step (times num_kv_heads via blockIdx.y).
-struct WorkItem {
-  int32_t seq;          // sequence index: row of q / out
-  int32_t partial;      // partial-result slot written by this workgroup
-  int32_t entry_begin;  // first BlockEntry of this workgroup
-  int32_t entry_count;  // number of BlockEntry records (blocks) it folds
-};
-
 // One KV block as the paged kernel sees it.
 struct BlockEntry {
   int32_t slot;      // >= 0: record index in the layer's HBM pool; < 0: staging record (-slot - 1)
   int32_t block_id;  // logical block id within the sequence; first token = block_id * tokens_per_block
+};
+
+// Block entries one workgroup folds at most (4 waves x 4 blocks).
+constexpr int kMaxWorkEntries = 16;
+
+// One workgroup's share of a paged decode step (times num_kv_heads via blockIdx.y). Self-
+// contained, so a workgroup needs a single (scalar) read before it issues its K/V loads.
+struct WorkItem {
+  int32_t seq;          // sequence index: row of q / out
+  int32_t partial;      // partial-result slot written by this workgroup
+  int32_t entry_count;  // number of entries (blocks) it folds
+  int32_t lo;           // valid token range [lo, hi) of the sequence
+  int32_t hi;
+  int32_t n_mass;       // blocks below this id get a mass entry
+  int32_t pad_[2];
+  BlockEntry entries[kMaxWorkEntries];
 };
 
 // Per-sequence scalars of a paged decode step.

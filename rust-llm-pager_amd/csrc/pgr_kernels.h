@@ -31,7 +31,6 @@ struct PagedLaunch {
   const void* pool;
   const void* stage;
   const WorkItem* work;
-  const BlockEntry* entries;
   const SeqInfo* seqs;
   float* pm;
   float* pl;

@@ -6,13 +6,28 @@ placement (the reference's one-PagedModel-per-session model, kv_block_store.py:3
 """
 from __future__ import annotations
 
+import atexit
 import ctypes
+import weakref
 
 import torch
 
 from . import _native as N
 
 nat = N.nat
+
+
+_LIVE_POOLS: "weakref.WeakSet[NativeKVPool]" = weakref.WeakSet()
+
+
+@atexit.register
+def _close_live_pools() -> None:
+    # Release native stores while the HIP runtime is still up (before interpreter teardown).
+    for pool in list(_LIVE_POOLS):
+        try:
+            pool.close()
+        except Exception:
+            pass
 
 
 def _i64_array(n: int):
@@ -35,6 +50,7 @@ class NativeKVPool:
         staging_blocks: int = 2048,
         staging_buffers: int = 2,
         blocks_per_workgroup: int = 16,
+        target_workgroups: int = 0,
     ):
         self.device = torch.device(device)
         if self.device.type != "cuda":
@@ -60,12 +76,14 @@ class NativeKVPool:
             staging_slots=staging_blocks,
             staging_buffers=staging_buffers,
             blocks_per_workgroup=blocks_per_workgroup,
+            target_workgroups=target_workgroups,
         )
         with torch.cuda.device(self.device):
             handle = self.lib.pgr_kv_create(ctypes.byref(cfg))
         if not handle:
             raise MemoryError(f"pgr_kv_create failed: {nat.last_error()}")
         self.handle = handle
+        _LIVE_POOLS.add(self)
         self.record_bytes = 2 * num_kv_heads * tokens_per_block * head_dim * torch.tensor([], dtype=dtype).element_size()
 
     # -- lifetime ------------------------------------------------------------------------
@@ -176,6 +194,28 @@ class NativeKVPool:
             "decode_layer", self.lib.pgr_kv_decode_layer, layer, q.data_ptr(), k_new.data_ptr(), v_new.data_ptr(),
             out.data_ptr(), N.ptr(mass_accum), stride, float(scale), float(softcap or 0.0), self._stream(),
         )
+
+    def attach_pager(self, sid: int, pager_handle: int, scores_from_mass: bool) -> None:
+        self._call("attach_pager", self.lib.pgr_kv_attach_pager, sid, pager_handle, int(scores_from_mass))
+
+    def end_step_place(self, n_sessions: int, mass_accum, num_layers: int, moves_cap: int, scores_cap: int):
+        """Closes the step and runs the native placement glue. Returns (completed, counts[n, 5],
+        moves, scores) with counts rows {new block id or -1, n to HBM, n to host, fail block, n scores}."""
+        completed = (ctypes.c_int32 * max(n_sessions, 1))()
+        n_done = ctypes.c_int32(0)
+        counts = (ctypes.c_int64 * (5 * max(n_sessions, 1)))()
+        moves = _i64_array(moves_cap)
+        scores = (ctypes.c_double * max(scores_cap, 1))()
+        stride = mass_accum.shape[1] if mass_accum is not None else 0
+        with torch.cuda.device(self.device):
+            rc = self.lib.pgr_kv_end_step_place(
+                self.handle, N.ptr(mass_accum), stride, num_layers, completed, ctypes.byref(n_done), counts, moves,
+                moves_cap, scores if scores_cap else None, scores_cap, self._stream(),
+            )
+        rows = [tuple(counts[5 * i: 5 * i + 5]) for i in range(n_sessions)]
+        if rc not in (nat.PGR_OK, nat.PGR_ERR_BUDGET):
+            nat.check(rc, "end_step_place")
+        return rc, list(completed[: n_done.value]), rows, moves, scores
 
     def end_step(self, n_sessions: int) -> list[int]:
         arr = (ctypes.c_int32 * max(n_sessions, 1))()

@@ -64,6 +64,7 @@ class PagedDecoder:
         staging_buffers: int = 2,
         ram_budget_bytes: int | None = None,
         blocks_per_workgroup: int = 16,
+        target_workgroups: int = 0,
         scale: float | None = None,
         softcap: float | None = None,
     ):
@@ -80,6 +81,7 @@ class PagedDecoder:
             staging_blocks=staging_blocks,
             staging_buffers=staging_buffers,
             blocks_per_workgroup=blocks_per_workgroup,
+            target_workgroups=target_workgroups,
         )
         self.pool.set_ram_budget(ram_budget_bytes)
         self.device = self.pool.device
@@ -92,6 +94,7 @@ class PagedDecoder:
         self.scale = scale
         self.softcap = softcap
         self.sessions: dict[int, DecodeSession] = {}
+        self._tokens: dict[int, int] = {}  # session length, mirrored to avoid native round trips
         self._step: list[int] | None = None
         self._mass: torch.Tensor | None = None
         self._n_mass: list[int] = []
@@ -116,12 +119,16 @@ class PagedDecoder:
         sid = self.pool.add_session(rows, capacity_tokens, lo)
         pg = _pager.PyPager(vram_budget, ram_budget, recent_window, rebalance_interval, promote_margin,
                             ram_promote_margin, policy)
-        self.sessions[sid] = DecodeSession(sid, rows, pg, policy, policy not in _POLICIES_WITHOUT_ATTENTION_SIGNAL, lo)
+        needs = policy not in _POLICIES_WITHOUT_ATTENTION_SIGNAL
+        self.sessions[sid] = DecodeSession(sid, rows, pg, policy, needs, lo)
+        self.pool.attach_pager(sid, pg._handle, needs)
+        self._tokens[sid] = 0
         return sid
 
     def remove_session(self, sid: int) -> None:
         self.pool.remove_session(sid)
         del self.sessions[sid]
+        del self._tokens[sid]
 
     def set_lo(self, sid: int, lo: list[int]) -> None:
         """First valid position per row (left padding and/or a sliding window bound)."""
@@ -138,6 +145,7 @@ class PagedDecoder:
         """
         s = self.sessions[sid]
         self.pool.set_length(sid, n_tokens)
+        self._tokens[sid] = n_tokens
         n_blocks = n_tokens // self.tokens_per_block
         moves = {"to_gpu": [], "to_cpu": []}
         if n_blocks:
@@ -168,7 +176,9 @@ class PagedDecoder:
             raise RuntimeError("begin_step called while a step is open")
         self.pool.begin_step(list(sids))
         self._step = list(sids)
-        self._n_mass = [self.pool.session_info(sid)[0] // self.tokens_per_block for sid in sids]
+        self._n_mass = [self._tokens[sid] // self.tokens_per_block for sid in sids]
+        for sid in sids:
+            self._tokens[sid] += 1
         if any(self.sessions[sid].needs_attention for sid in sids):
             self._mass = torch.zeros((len(sids), max(self._n_mass) + 1), dtype=torch.float32, device=self.device)
         else:
@@ -199,52 +209,49 @@ class PagedDecoder:
         """Ascending host-resident block ids streamed for sequence `seq` in the open step."""
         return self.pool.step_host_blocks(seq)
 
-    def end_step(self) -> dict[int, dict]:
+    def end_step(self, *, collect: bool = True) -> dict[int, dict]:
+        """Close the step and place blocks natively (one call for every session).
+
+        With collect=True returns per-session step stats in the reference's terms
+        (paged_model.py:801-812): new blocks, moves, the scores handed to the pager and the
+        share of them that sits in HBM after placement; with collect=False returns {}.
+        """
         if self._step is None:
             raise RuntimeError("end_step without begin_step")
         sids = self._step
-        mass_rows = None
-        if self._mass is not None:
-            mass_rows = (self._mass / self.num_layers).tolist()  # one device->host sync per step
-        completed = set(self.pool.end_step(len(sids)))
+        blocks_after = [n + 1 for n in self._n_mass]  # upper bound on full blocks after the step
+        cap = sum(blocks_after)
+        rc, completed, rows, moves, scores = self.pool.end_step_place(
+            len(sids), self._mass, self.num_layers, cap, cap if collect else 0
+        )
         self._step = None
         self._mass = None
+        if rc != 0:
+            bad = next(r[3] for r in rows if r[3] >= 0)
+            raise RuntimeError(f"ram_budget exceeded: moving block {bad} to CPU")
+        if not collect:
+            return {}
         results = {}
-        for i, sid in enumerate(sids):
-            s = self.sessions[sid]
-            n_blocks = self.pool.session_info(sid)[1]
-            added = [n_blocks - 1] if sid in completed else []
-            stats_before = self.pool.stats()
-            if n_blocks == 0:
-                block_attention: list[float] = []
-                to_gpu, to_cpu = [], []
-            else:
-                if s.needs_attention:
-                    averaged = mass_rows[i][: self._n_mass[i]]
-                    total = sum(averaged)
-                    block_attention = [x / total for x in averaged] if total > 0 else [1.0 / n_blocks] * n_blocks
-                else:
-                    block_attention = [1.0 / n_blocks] * n_blocks
-                query_block = n_blocks - 1
-                s.pager.on_step(query_block, 0, block_attention)
-                if added:
-                    s.pager.force_rebalance(query_block)
-                to_gpu, to_cpu, rc, fail_block = self.pool.apply_tiers(sid, s.pager.tiers())
-                if rc != 0:
-                    raise RuntimeError(f"ram_budget exceeded: moving block {fail_block} to CPU")
-            stats_after = self.pool.stats()
-            gpu_ids = self.pool.block_ids(sid, True)
-            attention_in_gpu = sum(block_attention[b] for b in gpu_ids if b < len(block_attention))
+        mo = so = 0
+        bb = None
+        for sid, (added, ng, nc, _, ns) in zip(sids, rows):
+            to_gpu = list(moves[mo: mo + ng])
+            to_cpu = list(moves[mo + ng: mo + ng + nc])
+            mo += ng + nc
+            block_attention = list(scores[so: so + ns])
+            so += ns
+            gpu_ids = self.pool.block_ids(sid, True) if ns else []
+            bb = self.pool.block_bytes(sid) if bb is None else bb
             st = {
-                "new_blocks": len(added),
-                "added_block_ids": added,
+                "new_blocks": int(added >= 0),
+                "added_block_ids": [added] if added >= 0 else [],
                 "to_gpu": to_gpu,
                 "to_cpu": to_cpu,
-                "gpu_to_cpu_mb": (stats_after["gpu_to_cpu_bytes"] - stats_before["gpu_to_cpu_bytes"]) / 1_000_000,
-                "gpu_to_cpu_copies": stats_after["gpu_to_cpu_copies"] - stats_before["gpu_to_cpu_copies"],
-                "attention_in_gpu": attention_in_gpu,
+                "gpu_to_cpu_mb": nc * bb / 1_000_000,
+                "gpu_to_cpu_copies": nc,
+                "attention_in_gpu": sum(block_attention[b] for b in gpu_ids if b < len(block_attention)),
                 "block_attention": block_attention,
             }
-            s.step_stats.append(st)
+            self.sessions[sid].step_stats.append(st)
             results[sid] = st
         return results
