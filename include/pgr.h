@@ -141,7 +141,7 @@ typedef struct pgr_kv_config_s {
   int64_t staging_slots;    /* records per staging buffer */
   int32_t staging_buffers;  /* ring depth, >= 1 (2 = double buffering) */
   int32_t blocks_per_workgroup; /* most block entries per workgroup (4..16) */
-  int32_t target_workgroups;    /* workgroups a launch aims for (0 = 768) */
+  int32_t target_workgroups;    /* workgroups a launch aims for (0 = a multiple of the CU count) */
 } pgr_kv_config_t;
 
 typedef struct pgr_kv_stats_s {

@@ -17,8 +17,10 @@ OUT = os.path.join(HERE, "libpgr.so")
 OBJ_DIR = os.path.join(HERE, "_build")
 
 ARCH = "gfx950"
-# Packed FP32 instructions stay disabled for all device code.
-DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+# Packed FP32 instructions stay disabled for all device code. MFMA results live in VGPRs
+# (gfx950 allows it): the decode kernels rescale their accumulators with VALU ops, and
+# AGPR accumulators would cost a copy in and out per tile.
+DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-mllvm", "-amdgpu-mfma-vgpr-form=1"]
 
 # (source, language, extra flags)
 SOURCES = [

@@ -54,6 +54,7 @@ struct F16 {
     return __builtin_bit_cast(uint32_t, h);
   }
   static __device__ __forceinline__ uint16_t cvt(float x) { return __builtin_bit_cast(uint16_t, (_Float16)x); }
+  static __device__ __forceinline__ float to_f(uint16_t x) { return (float)__builtin_bit_cast(_Float16, x); }
 };
 
 struct BF16 {
@@ -66,6 +67,7 @@ struct BF16 {
     return __builtin_bit_cast(uint32_t, h);
   }
   static __device__ __forceinline__ uint16_t cvt(float x) { return __builtin_bit_cast(uint16_t, (__bf16)x); }
+  static __device__ __forceinline__ float to_f(uint16_t x) { return __builtin_bit_cast(float, (uint32_t)x << 16); }
 };
 
 __device__ __forceinline__ float wave_max_g(float x) {
@@ -179,6 +181,14 @@ __device__ __forceinline__ void load_q(u32x4 (&q)[D / 32], const uint16_t* qptr,
   }
 }
 
+template <bool kLog2>
+__device__ __forceinline__ float exp_w(float x) {
+  if constexpr (kLog2)
+    return __builtin_amdgcn_exp2f(x);
+  else
+    return __expf(x);
+}
+
 // ---------------------------------------------------------------------------------------
 // Workgroup merge of the four waves' (m, l, acc) and store of one partial slot.
 // FOLD: online-softmax partials; FIXED: plain acc sums (m is the caller's fixed max).
@@ -189,7 +199,8 @@ struct MergeSmem {
   float acc[kWaves][kMaxRep][D + 1];
 };
 
-template <int D, bool kFold, bool kWithAcc>
+// kLog2: (m, scores) are in log2 units and the weights are exp2(m_w - m); otherwise e-based.
+template <int D, bool kFold, bool kWithAcc, bool kLog2 = false>
 __device__ __forceinline__ void wg_merge_store(MergeSmem<D>& sm, int wave, int g, int n, float m_run, float l_lane,
                                                const f32x4 (&acc)[D / 16], int n_rep, float* pm, float* pl,
                                                float* pacc) {
@@ -215,7 +226,7 @@ __device__ __forceinline__ void wg_merge_store(MergeSmem<D>& sm, int wave, int g
       float lw = 0.f;
       if (mw != kNegInf) {
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) lw += sm.l[w][r] * __expf(sm.m[w][r] - mw);
+        for (int w = 0; w < kWaves; ++w) lw += sm.l[w][r] * exp_w<kLog2>(sm.m[w][r] - mw);
       }
       pm[r] = mw;
       pl[r] = lw;
@@ -231,7 +242,7 @@ __device__ __forceinline__ void wg_merge_store(MergeSmem<D>& sm, int wave, int g
         for (int w = 0; w < kWaves; ++w) mw = fmaxf(mw, sm.m[w][r]);
         if (mw != kNegInf) {
 #pragma unroll
-          for (int w = 0; w < kWaves; ++w) a += sm.acc[w][r][d] * __expf(sm.m[w][r] - mw);
+          for (int w = 0; w < kWaves; ++w) a += sm.acc[w][r][d] * exp_w<kLog2>(sm.m[w][r] - mw);
         }
       } else {
 #pragma unroll
@@ -426,220 +437,386 @@ __global__ void finalize_f32_kernel(const float* acc, const float* l, float* out
 // Paged kernel: the fused decode path. Blocks are read in place from the layer's HBM
 // pool or from a staging buffer filled by host-to-device copies; record layout per
 // (block, sequence): K [Hkv][T][D] then V [Hkv][T][D]. Grid (n_work, Hkv).
+//
+// Each wave streams the blocks w, w+4, ... of its work item through a ring of NB register
+// tiles (NB-1 tiles of loads in flight while one is folded). Everything that selects a
+// tile (entry, slot, block id, tile index) is wave-uniform and lives in SGPRs; a lane's
+// part of a tile is a fixed byte offset, so every load is one `global_load saddr + voffset`.
+//
+// Scores are kept in log2 units (x = s * scale * log2 e, p = 2^(x - m)). The running max m
+// is refreshed lazily: a tile rescales (m, l, acc) only when one of its scores exceeds m
+// by more than kLazyRescale, so p <= 2^kLazyRescale and most tiles skip the cross-lane max
+// and the acc rescale. The final (m, l, acc) describe the same softmax exactly; P is still
+// rounded to the K/V type before P.V (streaming_attention.py:178).
 struct PagedArgs {
-  const uint16_t* q;     // [S, Hq, D]
-  const uint16_t* pool;  // layer pool base
-  const uint16_t* stage; // staging base
+  const uint16_t* q;      // [S, Hq, D]
+  const uint16_t* k_new;  // [S, Hkv, D]: the current token (appended here, attended in the merge)
+  const uint16_t* v_new;
+  uint16_t* pool;         // layer pool base
+  const uint16_t* stage;  // staging base
   const WorkItem* work;
   const SeqInfo* seqs;
-  float* pm;             // [slot][Hq]
+  float* pm;              // [slot][Hq], log2 units
   float* pl;
-  float* pacc;           // [slot][Hq][D]
-  float* mass_m;         // [S][Hq][mass_stride] (null: no mass)
+  float* pacc;            // [slot][Hq][D]
+  float* mass_m;          // [S][Hq][mass_stride], log2 units (null: no mass)
   float* mass_s;
+  uint16_t* out;          // [S, Hq, D]
+  float* mf;              // [S, Hq]: final max (log2 units) and sum, for the mass pass
+  float* lf;
   int hq, hkv, n_rep, tokens_per_block, mass_stride;
   float scale, softcap;
 };
 
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLazyRescale = 8.0f;
+constexpr float kMInit = -1.0e30f;  // running max before any valid score (finite: 2^(-inf - kMInit) = 0)
+
+template <class T>
+__device__ __forceinline__ T load_at(const uint16_t* base, uint32_t byte_off) {
+  return *reinterpret_cast<const T*>(reinterpret_cast<const char*>(base) + byte_off);
+}
+
+// K row n (bytes k_lane from the tile base) and V rows 4g..4g+3 (v_lane, then +D elements).
+template <int D>
+__device__ __forceinline__ void load_tile(Tile<D>& t, const uint16_t* kb, const uint16_t* vb, uint32_t k_lane,
+                                          uint32_t v_lane) {
+#pragma unroll
+  for (int i = 0; i < Tile<D>::KV4; ++i) t.k[i] = load_at<u32x4>(kb, k_lane + 16u * i);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t off = v_lane + (uint32_t)(i * D * 2);
+    if constexpr (D == 32) {
+      t.v[i][0] = load_at<uint32_t>(vb, off);
+    } else if constexpr (D == 64) {
+      const u32x2 x = load_at<u32x2>(vb, off);
+      t.v[i][0] = x.x;
+      t.v[i][1] = x.y;
+    } else {
+      const u32x4 x = load_at<u32x4>(vb, off);
+      t.v[i][0] = x.x;
+      t.v[i][1] = x.y;
+      t.v[i][2] = x.z;
+      t.v[i][3] = x.w;
+    }
+  }
+}
+
+struct TileMeta {
+  int t0;        // first token position of the tile
+  int block_id;
+  int last;      // last tile of its block
+};
+
+template <int D>
+struct PagedRing {
+  static constexpr int NB = D <= 64 ? 4 : 3;  // register tiles per wave
+};
+
 template <class Ty, int D, bool kMass>
 __global__ __launch_bounds__(256) void paged_attn_kernel(PagedArgs a) {
+  constexpr int NB = PagedRing<D>::NB;
+  constexpr int kWaveEntries = kMaxWorkEntries / kWaves;  // entries one wave folds at most
   __shared__ MergeSmem<D> sm;
-  const WorkItem& wi = a.work[blockIdx.x];
+  __shared__ float mass_sm[kMass ? kWaves : 1][kWaveEntries][2][kMaxRep];
+  const WorkItem* wi = a.work + blockIdx.x;
   const int h = blockIdx.y;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
   const int g = lane >> 4, n = lane & 15;
   const bool real = n < a.n_rep;
   const int qh = h * a.n_rep + (real ? n : 0);
   const int T = a.tokens_per_block;
-  const int tiles_per_block = T >> 4;
+  const int tpb = T >> 4;  // tiles per block
   const size_t rec = (size_t)2 * a.hkv * T * D;  // elements per record
   const size_t head_off = (size_t)h * T * D;
   const size_t v_off = (size_t)a.hkv * T * D;
+  const int seq = wi->seq, lo = wi->lo, hi = wi->hi, n_mass = wi->n_mass;
+  const int count = wi->entry_count, partial = wi->partial;
+  const int append_slot = wi->append_slot, append_pos = wi->append_pos;
+  const uint32_t k_lane = (uint32_t)(n * D + (D / 4) * g) * 2u;
+  const uint32_t v_lane = (uint32_t)(4 * g * D + (D / 16) * n) * 2u;
+
+  // This wave's entries wave, wave+4, wave+8, wave+12 (slot, block id), held in SGPRs.
+  // Entries past entry_count are never fetched (the slots exist in every work item).
+  static_assert(kWaveEntries == 4, "one wave folds at most four entries");
+  const BlockEntry en0 = wi->entries[wave], en1 = wi->entries[wave + kWaves];
+  const BlockEntry en2 = wi->entries[wave + 2 * kWaves], en3 = wi->entries[wave + 3 * kWaves];
 
   u32x4 q[D / 32];
-  load_q<D>(q, a.q + ((size_t)wi.seq * a.hq + qh) * D, real, g);
+  load_q<D>(q, a.q + ((size_t)seq * a.hq + qh) * D, real, g);
 
-  float m_run = kNegInf, l_run = 0.f, blk = 0.f;
+  // Score transform: x = mult * s' with s' = s (no softcap) or cap * tanh(s * scale / cap).
+  const bool capped = a.softcap > 0.f;
+  const float mult = capped ? kLog2e : a.scale * kLog2e;
+  const float cap_in = capped ? a.scale / a.softcap : 0.f;
+
+  float m_run = kMInit, m_thr = kMInit, l_run = 0.f, blk = 0.f;
   f32x4 acc[D / 16];
 #pragma unroll
   for (int j = 0; j < D / 16; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  const int my_blocks = wi.entry_count > wave ? (wi.entry_count - wave + kWaves - 1) / kWaves : 0;
-  const int tiles = my_blocks * tiles_per_block;
-  struct Meta {
-    int t0, block_id, tb;
-  };
-  // Issues the loads of the wave's tile ti (no wait): K row n and four V rows per lane.
-  auto fetch = [&](int ti, Tile<D>& t, Meta& mt) {
-    const int e = ti / tiles_per_block, tb = ti - e * tiles_per_block;
-    const BlockEntry be = wi.entries[wave + kWaves * e];
-    const uint16_t* base = be.slot >= 0 ? a.pool + (size_t)be.slot * rec : a.stage + (size_t)(-be.slot - 1) * rec;
-    const uint16_t* kt = base + head_off + (size_t)tb * 16 * D;
-    const uint16_t* vt = base + v_off + head_off + (size_t)tb * 16 * D;
-    load_k<D>(t, kt, n, g);
-    const int rows[4] = {4 * g, 4 * g + 1, 4 * g + 2, 4 * g + 3};
-    load_v<D>(t, vt, rows, n);
-    mt.t0 = be.block_id * T + tb * 16;
-    mt.block_id = be.block_id;
-    mt.tb = tb;
-  };
-  // Folds one fetched tile into the running (m, l, acc) and the block's mass sum.
-  auto fold = [&](Tile<D>& t, const Meta& mt) {
-    bool ok[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int tok = mt.t0 + 4 * g + i;
-      ok[i] = tok >= wi.lo && tok < wi.hi;
-      if (!ok[i]) zero_v_row<D>(t, i);
+  const int my_blocks = count > wave ? (count - wave + kWaves - 1) / kWaves : 0;
+  const int tiles = my_blocks * tpb;
+
+  // Next tile to fetch: flat index nf, entry fe, tile ftb within the block. A fetch past the
+  // wave's last tile reloads the last tile (an L2 hit) so that every fetch in the loop is
+  // unconditional and the load counter stays in order.
+  int nf = 0, fe = 0, ftb = 0;
+  auto fetch = [&](Tile<D>& t, TileMeta& mt) {
+    const int slot = fe == 0 ? en0.slot : fe == 1 ? en1.slot : fe == 2 ? en2.slot : en3.slot;
+    const int bid = fe == 0 ? en0.block_id : fe == 1 ? en1.block_id : fe == 2 ? en2.block_id : en3.block_id;
+    const uint16_t* rb = slot >= 0 ? a.pool + (size_t)slot * rec : a.stage + (size_t)(-slot - 1) * rec;
+    const uint16_t* kb = rb + head_off + (size_t)ftb * 16 * D;
+    load_tile<D>(t, kb, kb + v_off, k_lane, v_lane);
+    mt.t0 = bid * T + ftb * 16;
+    mt.block_id = bid;
+    mt.last = (ftb == tpb - 1) ? fe : -1;
+    if (nf + 1 < tiles) {
+      ++nf;
+      if (++ftb == tpb) {
+        ftb = 0;
+        ++fe;
+      }
     }
-    const f32x4 s4 = qk_tile<Ty, D>(t, q);
-    float s[4], p[4];
+  };
+
+  auto fold = [&](Tile<D>& t, const TileMeta& mt) {
+    f32x4 s4 = qk_tile<Ty, D>(t, q);
+    if (capped) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) s[i] = ok[i] ? transform_score(s4[i], a.scale, a.softcap) : kNegInf;
-    const float tmax = wave_max_g(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])));
-    const float m_new = fmaxf(m_run, tmax);
-    const bool empty = (m_new == kNegInf);
-    const float alpha = empty ? 0.f : __expf(m_run - m_new);
+      for (int i = 0; i < 4; ++i) s4[i] = a.softcap * tanhf(s4[i] * cap_in);
+    }
+    if (mt.t0 < lo || mt.t0 + 16 > hi) {  // tile straddles the valid range: mask per token
 #pragma unroll
-    for (int i = 0; i < 4; ++i) p[i] = empty ? 0.f : __expf(s[i] - m_new);
+      for (int i = 0; i < 4; ++i) {
+        const int tok = mt.t0 + 4 * g + i;
+        if (tok < lo || tok >= hi) {
+          s4[i] = kNegInf;
+          zero_v_row<D>(t, i);
+        }
+      }
+    }
+    const float lmax = fmaxf(fmaxf(s4[0], s4[1]), fmaxf(s4[2], s4[3])) * mult;
+    if (__builtin_amdgcn_ballot_w64(lmax > m_thr) != 0) {
+      const float m_new = fmaxf(m_run, wave_max_g(lmax));
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+      l_run *= alpha;
+      blk *= alpha;
+#pragma unroll
+      for (int j = 0; j < D / 16; ++j) acc[j] *= alpha;
+      m_run = m_new;
+      m_thr = m_new + kLazyRescale;
+    }
+    float p[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s4[i], mult, -m_run));
     const float psum = (p[0] + p[1]) + (p[2] + p[3]);
-    l_run = l_run * alpha + psum;
-#pragma unroll
-    for (int j = 0; j < D / 16; ++j) acc[j] *= alpha;
+    l_run += psum;
     pv_tile<Ty, D>(acc, t, p);
-    m_run = m_new;
     if constexpr (kMass) {
-      blk = blk * alpha + psum;
-      if (mt.tb == tiles_per_block - 1) {
+      blk += psum;
+      if (mt.last >= 0) {  // block complete: (m_b, s_b) of this block to LDS, stored after the loop
         const float bs = wave_sum_g(blk);
-        if (g == 0 && real && mt.block_id < wi.n_mass) {
-          const size_t mi = ((size_t)wi.seq * a.hq + qh) * a.mass_stride + mt.block_id;
-          a.mass_m[mi] = m_run;
-          a.mass_s[mi] = bs;
+        if (g == 0) {
+          mass_sm[wave][mt.last][0][n] = m_run;
+          mass_sm[wave][mt.last][1][n] = bs;
         }
         blk = 0.f;
       }
     }
   };
-  if constexpr (D <= 64) {
-    // Four tiles in registers as two pairs: while one pair is folded the other pair's loads
-    // are in flight (prefetch distance two tiles, 2 x 4 KiB per wave at head_dim 64).
-    Tile<D> a0, a1, b0, b1;
-    Meta ma0{}, ma1{}, mb0{}, mb1{};
-    if (tiles > 0) fetch(0, a0, ma0);
-    if (tiles > 1) fetch(1, a1, ma1);
-    for (int ti = 0; ti < tiles; ti += 4) {
-      if (ti + 2 < tiles) fetch(ti + 2, b0, mb0);
-      if (ti + 3 < tiles) fetch(ti + 3, b1, mb1);
-      fold(a0, ma0);
-      if (ti + 1 < tiles) fold(a1, ma1);
-      if (ti + 2 < tiles) {
-        if (ti + 4 < tiles) fetch(ti + 4, a0, ma0);
-        if (ti + 5 < tiles) fetch(ti + 5, a1, ma1);
-        fold(b0, mb0);
-        if (ti + 3 < tiles) fold(b1, mb1);
+
+  if (tiles > 0) {
+    Tile<D> buf[NB];
+    TileMeta meta[NB];
+#pragma unroll
+    for (int j = 0; j < NB - 1; ++j) fetch(buf[j], meta[j]);
+    // q is needed by the first fold; waiting for it here (behind the prologue loads) keeps
+    // the loop's wait counts independent of it.
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i) asm volatile("" ::"v"(q[i]));
+    for (int ti = 0; ti < tiles; ti += NB) {
+#pragma unroll
+      for (int j = 0; j < NB; ++j) {
+        fetch(buf[(j + NB - 1) % NB], meta[(j + NB - 1) % NB]);
+        if (ti + j < tiles) fold(buf[j], meta[j]);
       }
     }
-  } else {
-    // head_dim 128: tiles are twice as large; one tile ahead keeps 8 KiB per wave in flight
-    // at a register count that still allows three waves per SIMD.
-    Tile<D> ta, tb;
-    Meta ma{}, mb{};
-    if (tiles > 0) fetch(0, ta, ma);
-    for (int ti = 0; ti < tiles; ti += 2) {
-      if (ti + 1 < tiles) fetch(ti + 1, tb, mb);
-      fold(ta, ma);
-      if (ti + 1 < tiles) {
-        if (ti + 2 < tiles) fetch(ti + 2, ta, ma);
-        fold(tb, mb);
+  }
+  if constexpr (kMass) {
+    if (g == 0 && real) {
+      for (int e = 0; e < my_blocks; ++e) {
+        const int bid = e == 0 ? en0.block_id : e == 1 ? en1.block_id : e == 2 ? en2.block_id : en3.block_id;
+        if (bid < n_mass) {
+          const size_t mi = ((size_t)seq * a.hq + qh) * a.mass_stride + bid;
+          a.mass_m[mi] = mass_sm[wave][e][0][n];
+          a.mass_s[mi] = mass_sm[wave][e][1][n];
+        }
       }
     }
   }
 
-  const size_t slot = (size_t)wi.partial;
-  wg_merge_store<D, true, true>(sm, wave, g, n, m_run, l_run, acc, a.n_rep, a.pm + slot * a.hq + h * a.n_rep,
-                                a.pl + slot * a.hq + h * a.n_rep, a.pacc + (slot * a.hq + h * a.n_rep) * D);
+  // Append (one work item per sequence): the current token's K/V of this head into its
+  // block record. No workgroup of this launch reads that position (work covers [lo, hi)).
+  if (append_slot >= 0 && threadIdx.x < D) {
+    const size_t src = ((size_t)seq * a.hkv + h) * D + threadIdx.x;
+    uint16_t* dst = a.pool + (size_t)append_slot * rec + head_off + (size_t)append_pos * D + threadIdx.x;
+    dst[0] = a.k_new[src];
+    dst[v_off] = a.v_new[src];
+  }
+
+  const size_t slot = (size_t)partial;
+  const float m_out = m_run == kMInit ? kNegInf : m_run;
+  wg_merge_store<D, true, true, true>(sm, wave, g, n, m_out, l_run, acc, a.n_rep, a.pm + slot * a.hq + h * a.n_rep,
+                                      a.pl + slot * a.hq + h * a.n_rep, a.pacc + (slot * a.hq + h * a.n_rep) * D);
 }
 
-// Per (sequence, query head): combine the partial slots, write the output in the element
-// type and the final (m, l) for the mass pass. One 256-thread workgroup per row: the
-// partial weights exp(m_k - m_final) are computed once into LDS, then 256/D thread groups
-// each sum a strided subset of the partials for all D dims and the groups are reduced.
-constexpr int kMergeThreads = 256;
-constexpr int kMergeWeights = 2048;
+// ---------------------------------------------------------------------------------------
+// Split-K merge: one workgroup per (sequence, KV head) combines the sequence's partial slots
+// for the group's n_rep query heads with the current token (score q.k_new, weight 2^(x - m),
+// P rounded like every other P), and writes the output and the final (m, l) for the mass
+// pass. Each phase keeps many independent loads in flight: the partials are a few KB per
+// slot and the kernel is latency-bound.
+constexpr int kSeqMergeChunk = 128;  // partial weights staged in LDS at a time
 
-__device__ __forceinline__ float block_reduce_max(float x, float* red) {
-  for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
-  const int w = threadIdx.x >> 6;
-  if ((threadIdx.x & 63) == 0) red[w] = x;
-  __syncthreads();
-  x = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  __syncthreads();
-  return x;
+__device__ __forceinline__ float sum16(float x) {
+  x += __shfl_xor(x, 8);
+  x += __shfl_xor(x, 4);
+  x += __shfl_xor(x, 2);
+  return x + __shfl_xor(x, 1);
 }
-
-__device__ __forceinline__ float block_reduce_sum(float x, float* red) {
-  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
-  const int w = threadIdx.x >> 6;
-  if ((threadIdx.x & 63) == 0) red[w] = x;
-  __syncthreads();
-  x = (red[0] + red[1]) + (red[2] + red[3]);
-  __syncthreads();
-  return x;
+__device__ __forceinline__ float max16(float x) {
+  x = fmaxf(x, __shfl_xor(x, 8));
+  x = fmaxf(x, __shfl_xor(x, 4));
+  x = fmaxf(x, __shfl_xor(x, 2));
+  return fmaxf(x, __shfl_xor(x, 1));
 }
 
 template <class Ty, int D>
-__global__ __launch_bounds__(kMergeThreads) void paged_merge_kernel(const SeqInfo* seqs, const float* pm,
-                                                                    const float* pl, const float* pacc, uint16_t* out,
-                                                                    float* mf_out, float* lf_out, float* acc_out,
-                                                                    int hq) {
-  constexpr int G = kMergeThreads / D;  // partial groups
-  __shared__ float w_s[kMergeWeights];
-  __shared__ float red[4];
-  __shared__ float part[G][D];
-  const int row = blockIdx.x;
-  const int s = row / hq, qh = row - s * hq;
-  const SeqInfo si = seqs[s];
+__global__ __launch_bounds__(256) void paged_merge_kernel(PagedArgs a) {
+  constexpr int kC = (kMaxRep * D / 2 + 255) / 256;  // float2 chunks of the group's acc per thread
+  constexpr int kU = 32 / kC;                        // partials loaded per chunk per batch
+  __shared__ float w_s[kMaxRep][kSeqMergeChunk];
+  __shared__ float lf_s[kMaxRep], pc_s[kMaxRep];
+  const int seq = blockIdx.x, h = blockIdx.y;
   const int tid = threadIdx.x;
-  float mf = kNegInf;
-  for (int k = tid; k < si.partial_count; k += kMergeThreads)
-    mf = fmaxf(mf, pm[(size_t)(si.partial_base + k) * hq + qh]);
-  mf = block_reduce_max(mf, red);
-  const int grp = tid / D, dd = tid - grp * D;
-  float lf_part = 0.f, x = 0.f;
-  for (int k0 = 0; k0 < si.partial_count; k0 += kMergeWeights) {
-    const int cnt = min(kMergeWeights, si.partial_count - k0);
-    for (int k = tid; k < cnt; k += kMergeThreads) {
-      const size_t pi = (size_t)(si.partial_base + k0 + k) * hq + qh;
-      const float w = mf == kNegInf ? 0.f : __expf(pm[pi] - mf);
-      w_s[k] = w;
-      lf_part += pl[pi] * w;
-    }
-    __syncthreads();
-    for (int k = grp; k < cnt; k += G) {
-      const size_t pi = (size_t)(si.partial_base + k0 + k) * hq + qh;
-      x += pacc[pi * D + dd] * w_s[k];
-    }
-    __syncthreads();
-  }
-  const float lf = block_reduce_sum(lf_part, red);
-  part[grp][dd] = x;
-  __syncthreads();
-  if (tid < D) {
-    float acc = 0.f;
+  const int r = tid >> 4, j = tid & 15;  // 16 lanes per query head of the group
+  const bool rv = r < a.n_rep;
+  const int hq = a.hq;
+  const int qh = h * a.n_rep + (rv ? r : 0);
+  const SeqInfo* si = a.seqs + seq;
+  const int P = si->partial_count, base = si->partial_base;
+  const size_t kv_row = ((size_t)seq * a.hkv + h) * D;
+
+  // Current token: x = mult * s' (s' softcapped like every score); it is always valid.
+  float dot = 0.f;
+  if (rv) {
+    const uint16_t* qp = a.q + ((size_t)seq * hq + qh) * D;
 #pragma unroll
-    for (int q = 0; q < G; ++q) acc += part[q][tid];
-    out[(size_t)row * D + tid] = Ty::cvt(acc / lf);
-    if (acc_out != nullptr) acc_out[(size_t)row * D + tid] = acc;
+    for (int d = j; d < D; d += 16) dot += Ty::to_f(qp[d]) * Ty::to_f(a.k_new[kv_row + d]);
   }
-  if (tid == 0) {
-    mf_out[row] = mf;
-    lf_out[row] = lf;
+  dot = sum16(dot);
+  float x_cur;
+  if (a.softcap > 0.f)
+    x_cur = a.softcap * tanhf(dot * (a.scale / a.softcap)) * kLog2e;
+  else
+    x_cur = dot * (a.scale * kLog2e);
+
+  float mx = kNegInf;
+  if (rv) {
+    for (int p0 = 0; p0 < P; p0 += 128) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int p = p0 + j + 16 * u;
+        v[u] = p < P ? a.pm[(size_t)(base + p) * hq + qh] : kNegInf;
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) mx = fmaxf(mx, v[u]);
+    }
+  }
+  const float mf = fmaxf(max16(mx), x_cur);
+
+  const int C = a.n_rep * D / 2;  // float2 chunks of the group's acc rows
+  float2 acc[kC];
+#pragma unroll
+  for (int k = 0; k < kC; ++k) acc[k] = float2{0.f, 0.f};
+  float ls = 0.f;
+  const size_t stride = (size_t)hq * D;  // floats between consecutive partial slots
+  const float* acc_base = a.pacc + ((size_t)base * hq + (size_t)h * a.n_rep) * D;
+  for (int p0 = 0; p0 < P; p0 += kSeqMergeChunk) {
+    const int cnt = min(kSeqMergeChunk, P - p0);
+    if (rv) {
+      float vm[8], vl[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int p = j + 16 * u;
+        const size_t pi = (size_t)(base + p0 + p) * hq + qh;
+        vm[u] = p < cnt ? a.pm[pi] : kNegInf;
+        vl[u] = p < cnt ? a.pl[pi] : 0.f;
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int p = j + 16 * u;
+        const float w = __builtin_amdgcn_exp2f(vm[u] - mf);  // empty partial: m = -inf, w = 0
+        if (p < cnt) w_s[r][p] = w;
+        ls += vl[u] * w;
+      }
+    }
+    __syncthreads();
+    for (int q0 = 0; q0 < cnt; q0 += kU) {
+      float2 v[kC][kU];
+#pragma unroll
+      for (int k = 0; k < kC; ++k) {
+        const int c = tid + 256 * k;
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+          const int p = q0 + u;
+          v[k][u] = (c < C && p < cnt) ? *reinterpret_cast<const float2*>(acc_base + (size_t)(p0 + p) * stride + 2 * c)
+                                       : float2{0.f, 0.f};
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < kC; ++k) {
+        const int c = tid + 256 * k;
+        const int ro = min(2 * c / D, kMaxRep - 1);
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+          const float w = q0 + u < cnt ? w_s[ro][q0 + u] : 0.f;
+          acc[k].x += v[k][u].x * w;
+          acc[k].y += v[k][u].y * w;
+        }
+      }
+    }
+    __syncthreads();
+  }
+  ls = sum16(ls);
+  const float pc = __builtin_amdgcn_exp2f(x_cur - mf);
+  if (rv && j == 0) {
+    lf_s[r] = ls + pc;
+    pc_s[r] = Ty::to_f(Ty::cvt(pc));  // P rounded to the K/V type before P.V
+    a.mf[(size_t)seq * hq + qh] = mf;
+    a.lf[(size_t)seq * hq + qh] = ls + pc;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < kC; ++k) {
+    const int c = tid + 256 * k;
+    if (c < C) {
+      const int e = 2 * c, ro = e / D, d = e - ro * D;
+      const float pcr = pc_s[ro], lf = lf_s[ro];
+      const float v0 = acc[k].x + pcr * Ty::to_f(a.v_new[kv_row + d]);
+      const float v1 = acc[k].y + pcr * Ty::to_f(a.v_new[kv_row + d + 1]);
+      uint16_t* o = a.out + ((size_t)seq * hq + h * a.n_rep + ro) * D + d;
+      o[0] = Ty::cvt(v0 / lf);
+      o[1] = Ty::cvt(v1 / lf);
+    }
   }
 }
 
 // Per (session, block): mean over the session's rows and all query heads of
-// s_b * exp(m_b - m_final) / l_final, added into the session's mass accumulator
+// s_b * 2^(m_b - m_final) / l_final (log2 units), added into the session's mass accumulator
 // (paged_model.py:1041-1048 per layer).
 __global__ void mass_reduce_kernel(const SeqInfo* seqs, const int32_t* session_rows, const int32_t* session_first,
                                    const float* mass_m, const float* mass_s, const float* mf, const float* lf,
@@ -658,7 +835,7 @@ __global__ void mass_reduce_kernel(const SeqInfo* seqs, const int32_t* session_r
     for (int qh = 0; qh < hq; ++qh) {
       const size_t row = (size_t)(first + r) * hq + qh;
       const size_t mi = row * mass_stride + blk;
-      total += mass_s[mi] * __expf(mass_m[mi] - mf[row]) / lf[row];
+      if (lf[row] > 0.f) total += mass_s[mi] * __builtin_amdgcn_exp2f(mass_m[mi] - mf[row]) / lf[row];
     }
   }
   mass_accum[(size_t)sess * accum_stride + blk] += total / (float)(rows * hq);
@@ -787,7 +964,9 @@ hipError_t launch_paged(int dtype, int d, const PagedLaunch& p, hipStream_t stre
   if (p.n_work == 0) return hipSuccess;
   PagedArgs a;
   a.q = static_cast<const uint16_t*>(p.q);
-  a.pool = static_cast<const uint16_t*>(p.pool);
+  a.k_new = static_cast<const uint16_t*>(p.k_new);
+  a.v_new = static_cast<const uint16_t*>(p.v_new);
+  a.pool = static_cast<uint16_t*>(p.pool);
   a.stage = static_cast<const uint16_t*>(p.stage);
   a.work = p.work;
   a.seqs = p.seqs;
@@ -796,6 +975,9 @@ hipError_t launch_paged(int dtype, int d, const PagedLaunch& p, hipStream_t stre
   a.pacc = p.pacc;
   a.mass_m = p.mass_m;
   a.mass_s = p.mass_s;
+  a.out = static_cast<uint16_t*>(p.out);
+  a.mf = p.mf;
+  a.lf = p.lf;
   a.hq = p.hq;
   a.hkv = p.hkv;
   a.n_rep = p.hq / p.hkv;
@@ -824,14 +1006,26 @@ hipError_t launch_paged(int dtype, int d, const PagedLaunch& p, hipStream_t stre
   }
 }
 
-hipError_t launch_paged_merge(int dtype, const SeqInfo* seqs, int n_seq, int hq, int d, const float* pm,
-                              const float* pl, const float* pacc, void* out, float* mf, float* lf, float* acc_out,
-                              hipStream_t stream) {
+hipError_t launch_paged_merge(int dtype, int d, const PagedLaunch& p, int n_seq, hipStream_t stream) {
   if (n_seq == 0) return hipSuccess;
-  dim3 grid(n_seq * hq);
-  uint16_t* o = static_cast<uint16_t*>(out);
-#define PGR_MERGE(TY, DD) \
-  paged_merge_kernel<TY, DD><<<grid, kMergeThreads, 0, stream>>>(seqs, pm, pl, pacc, o, mf, lf, acc_out, hq)
+  PagedArgs a{};
+  a.q = static_cast<const uint16_t*>(p.q);
+  a.k_new = static_cast<const uint16_t*>(p.k_new);
+  a.v_new = static_cast<const uint16_t*>(p.v_new);
+  a.seqs = p.seqs;
+  a.pm = p.pm;
+  a.pl = p.pl;
+  a.pacc = p.pacc;
+  a.out = static_cast<uint16_t*>(p.out);
+  a.mf = p.mf;
+  a.lf = p.lf;
+  a.hq = p.hq;
+  a.hkv = p.hkv;
+  a.n_rep = p.hq / p.hkv;
+  a.scale = p.scale;
+  a.softcap = p.softcap;
+  dim3 grid(n_seq, p.hkv);
+#define PGR_MERGE(TY, DD) paged_merge_kernel<TY, DD><<<grid, 256, 0, stream>>>(a)
   if (dtype == kF16) {
     if (d == 32) PGR_MERGE(F16, 32);
     else if (d == 64) PGR_MERGE(F16, 64);

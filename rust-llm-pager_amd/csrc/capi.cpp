@@ -261,7 +261,7 @@ void* pgr_kv_create(const pgr_kv_config_t* c) {
   cfg.staging_slots = c->staging_slots;
   cfg.staging_buffers = c->staging_buffers;
   cfg.blocks_per_workgroup = c->blocks_per_workgroup > 0 ? c->blocks_per_workgroup : 16;
-  cfg.target_workgroups = c->target_workgroups > 0 ? c->target_workgroups : 768;
+  cfg.target_workgroups = c->target_workgroups > 0 ? c->target_workgroups : 0;
   auto* kv = new (std::nothrow) pgr::PagedKV(cfg);
   if (!kv) {
     set_err(pgr::kErrCapacity, "out of host memory");

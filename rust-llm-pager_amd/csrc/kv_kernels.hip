@@ -1,4 +1,5 @@
-// KV block-store data movement kernels (append of the decode token, layout conversions).
+// KV block-store data movement kernels: reference block layout <-> pool records.
+// (The decode token is appended by the fused attention kernel.)
 //
 // Pool record layout for one (block, sequence row, layer): K [Hkv][T][D] followed by
 // V [Hkv][T][D]; every element is 16-bit (fp16 or bf16) and moved as raw bits.
@@ -9,24 +10,6 @@
 
 namespace pgr {
 namespace {
-
-// One workgroup per sequence; threads stride over Hkv * D of K and of V.
-__global__ void kv_append_kernel(const uint16_t* k_new, const uint16_t* v_new, uint16_t* pool, const int32_t* slots,
-                                 const int32_t* pos, int hkv, int tpb, int d) {
-  const int s = blockIdx.x;
-  const int slot = slots[s];
-  const int p = pos[s];
-  const size_t rec = (size_t)2 * hkv * tpb * d;
-  uint16_t* kr = pool + (size_t)slot * rec;
-  uint16_t* vr = kr + (size_t)hkv * tpb * d;
-  const int n = hkv * d;
-  for (int i = threadIdx.x; i < n; i += blockDim.x) {
-    const int h = i / d, dd = i - h * d;
-    const size_t dst = ((size_t)h * tpb + p) * d + dd;
-    kr[dst] = k_new[(size_t)s * n + i];
-    vr[dst] = v_new[(size_t)s * n + i];
-  }
-}
 
 // ref [B, T, Hkv, D] -> record of row b at slots[b].
 __global__ void ref_to_records_kernel(const uint16_t* key, const uint16_t* value, uint16_t* pool,
@@ -75,14 +58,6 @@ unsigned grid_for(size_t total) {
 }
 
 }  // namespace
-
-hipError_t launch_kv_append(const void* k_new, const void* v_new, void* pool, const int32_t* slots, const int32_t* pos,
-                            int n_seq, int hkv, int tokens_per_block, int d, hipStream_t stream) {
-  if (n_seq == 0) return hipSuccess;
-  kv_append_kernel<<<n_seq, 256, 0, stream>>>(static_cast<const uint16_t*>(k_new), static_cast<const uint16_t*>(v_new),
-                                              static_cast<uint16_t*>(pool), slots, pos, hkv, tokens_per_block, d);
-  return hipGetLastError();
-}
 
 hipError_t launch_ref_to_records(const void* key, const void* value, void* pool, const int32_t* slots, int rows,
                                  int hkv, int tokens_per_block, int d, hipStream_t stream) {

@@ -130,6 +130,9 @@ int PagedKV::init() {
   if (cfg_.pool_slots > INT32_MAX / 2 || cfg_.staging_slots * cfg_.staging_buffers > INT32_MAX / 2)
     return fail(kErrInvalid, "pool or staging too large for 32-bit record indices");
   if (cfg_.blocks_per_workgroup < kWaves) cfg_.blocks_per_workgroup = kWaves;
+  int dev = 0;
+  PGR_HIP(hipGetDevice(&dev));
+  PGR_HIP(hipDeviceGetAttribute(&n_cu_, hipDeviceAttributeMultiprocessorCount, dev));
   const size_t rec = rec_bytes();
   pool_.assign(cfg_.num_layers, nullptr);
   host_.assign(cfg_.num_layers, nullptr);
@@ -621,18 +624,23 @@ int PagedKV::ensure_workspace(size_t bytes) {
   return kOk;
 }
 
+int PagedKV::default_workgroups() const {
+  // Whole workgroups per CU, all resident in one round: three at head_dim <= 64 (four fit),
+  // two at 128 (the register ring allows two).
+  const int per_cu = cfg_.head_dim <= 64 ? 3 : 2;
+  return per_cu * std::max(1, n_cu_);
+}
+
 int PagedKV::begin_step(const int32_t* sids, int n, hipStream_t stream) {
   if (in_step_) return fail(kErrState, "begin_step while a step is open");
   const int64_t T = cfg_.tokens_per_block;
   const int E_max = std::min(kMaxWorkEntries, std::max(kWaves, cfg_.blocks_per_workgroup));
-  const int64_t kTargetWorkgroups = std::max(1, cfg_.target_workgroups);
+  const int64_t target_wg = cfg_.target_workgroups > 0 ? cfg_.target_workgroups : default_workgroups();
   step_sids_.assign(sids, sids + n);
   step_first_.clear();
   seqs_.clear();
   work_.clear();
   copies_.clear();
-  append_slot_.clear();
-  append_pos_.clear();
   step_host_ids_.clear();
   step_stats_ = StepStats();
   // Validate and open a block where the new token starts one.
@@ -653,13 +661,17 @@ int PagedKV::begin_step(const int32_t* sids, int n, hipStream_t stream) {
       }
     }
   }
-  // Per sequence: resident entries now, host runs into chunks of staging records.
+  // Per sequence: the stored blocks holding valid tokens [lo, p) -- resident ones read in
+  // place, host runs cut into chunks of staging records. The current token (position p) is
+  // not read from the store: the merge kernel takes it from k_new / v_new, and the
+  // sequence's first work item appends it to the open block.
   struct Pending {
     int seq;
     BlockEntry e;
     int launch;
   };
   std::vector<Pending> pend;
+  std::vector<int32_t> append_slot, append_pos;  // per sequence: record and offset of the current token
   const int64_t chunk_cap = cfg_.staging_slots;
   int64_t used_in_chunk = 0;
   int chunk = 0;
@@ -673,15 +685,15 @@ int PagedKV::begin_step(const int32_t* sids, int n, hipStream_t stream) {
       const int seq = (int)seqs_.size();
       SeqInfo si{};
       si.lo = s.row[r].lo;
-      si.hi = (int32_t)(p + 1);
+      si.hi = (int32_t)p;
       si.n_mass = (int32_t)n_full;
       const int64_t first_blk = std::min<int64_t>(std::max<int64_t>(si.lo, 0) / T, n_full);
       si.mass_lo = (int32_t)first_blk;
       si.session = i;
       seqs_.push_back(si);
+      append_slot.push_back(s.slot[(p / T) * s.rows + r]);
+      append_pos.push_back((int32_t)(p % T));
       max_mass = std::max<int>(max_mass, (int)n_full);
-      append_slot_.push_back(s.slot[(p / T) * s.rows + r]);
-      append_pos_.push_back((int32_t)(p % T));
       std::vector<int64_t> host_ids;
       int64_t b = first_blk;
       while (b < n_full) {
@@ -716,9 +728,10 @@ int PagedKV::begin_step(const int32_t* sids, int n, hipStream_t stream) {
         step_stats_.host_tokens += (e - b) * T;
         b = e;
       }
-      // The open block holding the new token.
-      pend.push_back({seq, BlockEntry{s.slot[(p / T) * s.rows + r], (int32_t)(p / T)}, 0});
-      step_stats_.resident_tokens += p % T + 1;
+      // The open block, when it already holds valid tokens before the current one.
+      if (p % T > 0 && p > si.lo)
+        pend.push_back({seq, BlockEntry{s.slot[(p / T) * s.rows + r], (int32_t)(p / T)}, 0});
+      step_stats_.resident_tokens += p % T + 1;  // stored part of the open block + the current token
       step_host_ids_.push_back(std::move(host_ids));
     }
   }
@@ -729,35 +742,55 @@ int PagedKV::begin_step(const int32_t* sids, int n, hipStream_t stream) {
   step_stage_base_ = stage_base_;
   stage_base_ = (stage_base_ + n_chunks_) % cfg_.staging_buffers;
   const int n_launch = std::max(1, n_chunks_);
-  // Workgroups: per launch, per sequence, runs of up to E entries (pend is grouped by sequence
-  // and, within a sequence, by launch order of discovery).
+  // Work items. Each launch is cut into about target_wg / Hkv work items of nearly equal
+  // size, so that every CU streams the same number of bytes in one round of workgroups;
+  // each sequence gets work items in proportion to its entries in that launch (at most
+  // E_max entries each, at least one entry per wave when the launch is small). A sequence
+  // with nothing stored in scope gets one empty work item: its workgroup runs the merge.
   std::vector<int> seq_wg(seqs_.size(), 0);
+  std::vector<int> seq_entries(seqs_.size(), 0);
+  for (const Pending& pe : pend) ++seq_entries[pe.seq];
   launch_work_begin_.assign(n_launch, 0);
   launch_work_end_.assign(n_launch, 0);
   std::vector<std::vector<size_t>> by_launch(n_launch);
   for (size_t i = 0; i < pend.size(); ++i) by_launch[pend[i].launch].push_back(i);
+  auto new_item = [&](int seq) {
+    WorkItem w{};
+    w.seq = seq;
+    w.partial = seq_wg[seq];
+    w.lo = seqs_[seq].lo;
+    w.hi = seqs_[seq].hi;
+    w.n_mass = seqs_[seq].n_mass;
+    w.append_slot = seq_wg[seq] == 0 ? append_slot[seq] : -1;
+    w.append_pos = append_pos[seq];
+    ++seq_wg[seq];
+    return w;
+  };
   for (int L = 0; L < n_launch; ++L) {
     launch_work_begin_[L] = (int)work_.size();
     const auto& idx = by_launch[L];
-    // Blocks per workgroup: enough that the launch needs about kTargetWorkgroups workgroups
-    // (4 resident per CU, 16 waves): one round, each wave streaming several blocks, between
-    // one block per wave and the configured maximum.
-    const int64_t per_wg = ((int64_t)idx.size() * cfg_.kv_heads + kTargetWorkgroups - 1) / kTargetWorkgroups;
-    const int E = (int)std::max<int64_t>(kWaves, std::min<int64_t>(E_max, (per_wg + kWaves - 1) / kWaves * kWaves));
+    const int64_t N = (int64_t)idx.size();
+    const int64_t want_items = std::max<int64_t>(1, target_wg / cfg_.kv_heads);
+    const int64_t items = std::max<int64_t>((N + E_max - 1) / E_max, std::min<int64_t>(want_items, (N + kWaves - 1) / kWaves));
     size_t i = 0;
     while (i < idx.size()) {
       const int seq = pend[idx[i]].seq;
-      WorkItem w{};
-      w.seq = seq;
-      w.partial = seq_wg[seq]++;
-      w.lo = seqs_[seq].lo;
-      w.hi = seqs_[seq].hi;
-      w.n_mass = seqs_[seq].n_mass;
-      while (i < idx.size() && pend[idx[i]].seq == seq && w.entry_count < E) {
-        w.entries[w.entry_count++] = pend[idx[i]].e;
-        ++i;
+      size_t e = i;
+      while (e < idx.size() && pend[idx[e]].seq == seq) ++e;
+      const int64_t ns = (int64_t)(e - i);
+      int64_t ws = (int64_t)std::llround((double)ns * (double)items / (double)std::max<int64_t>(N, 1));
+      ws = std::max<int64_t>(ws, std::max<int64_t>(1, (ns + E_max - 1) / E_max));
+      ws = std::min<int64_t>(ws, ns);
+      for (int64_t k = 0; k < ws; ++k) {
+        const int64_t cnt = ns / ws + (k < ns % ws ? 1 : 0);
+        WorkItem w = new_item(seq);
+        for (int64_t x = 0; x < cnt; ++x) w.entries[w.entry_count++] = pend[idx[i++]].e;
+        work_.push_back(w);
       }
-      work_.push_back(w);
+    }
+    if (L == 0) {
+      for (size_t q = 0; q < seqs_.size(); ++q)
+        if (seq_entries[q] == 0) work_.push_back(new_item((int)q));
     }
     launch_work_end_[L] = (int)work_.size();
   }
@@ -791,8 +824,6 @@ int PagedKV::begin_step(const int32_t* sids, int n, hipStream_t stream) {
   };
   const size_t o_seqs = carve(sizeof(SeqInfo) * S);
   const size_t o_work = carve(sizeof(WorkItem) * std::max<size_t>(work_.size(), 1));
-  const size_t o_aslot = carve(sizeof(int32_t) * S);
-  const size_t o_apos = carve(sizeof(int32_t) * S);
   const size_t o_srows = carve(sizeof(int32_t) * std::max(n, 1));
   const size_t o_sfirst = carve(sizeof(int32_t) * std::max(n, 1));
   const size_t plan_bytes = off;
@@ -819,8 +850,6 @@ int PagedKV::begin_step(const int32_t* sids, int n, hipStream_t stream) {
   char* h = static_cast<char*>(plan_host_);
   std::memcpy(h + o_seqs, seqs_.data(), sizeof(SeqInfo) * S);
   std::memcpy(h + o_work, work_.data(), sizeof(WorkItem) * work_.size());
-  std::memcpy(h + o_aslot, append_slot_.data(), sizeof(int32_t) * S);
-  std::memcpy(h + o_apos, append_pos_.data(), sizeof(int32_t) * S);
   std::memcpy(h + o_srows, sess_rows.data(), sizeof(int32_t) * n);
   std::memcpy(h + o_sfirst, sess_first.data(), sizeof(int32_t) * n);
   char* d = static_cast<char*>(ws_);
@@ -828,8 +857,6 @@ int PagedKV::begin_step(const int32_t* sids, int n, hipStream_t stream) {
   PGR_HIP(hipEventRecord(plan_uploaded_, stream));
   d_seqs_ = reinterpret_cast<SeqInfo*>(d + o_seqs);
   d_work_ = reinterpret_cast<WorkItem*>(d + o_work);
-  d_append_slot_ = reinterpret_cast<int32_t*>(d + o_aslot);
-  d_append_pos_ = reinterpret_cast<int32_t*>(d + o_apos);
   d_sess_rows_ = reinterpret_cast<int32_t*>(d + o_srows);
   d_sess_first_ = reinterpret_cast<int32_t*>(d + o_sfirst);
   d_pm_ = reinterpret_cast<float*>(d + o_pm);
@@ -847,14 +874,13 @@ int PagedKV::decode_layer(int layer, const void* q, const void* k_new, const voi
                           float* mass_accum, int64_t accum_stride, float scale, float softcap, hipStream_t stream) {
   if (!in_step_) return fail(kErrState, "decode_layer outside begin_step/end_step");
   if (layer < 0 || layer >= cfg_.num_layers) return fail(kErrInvalid, "layer out of range");
-  const int S = (int)seqs_.size();
   const int hq = cfg_.query_heads;
   const int T = cfg_.tokens_per_block;
   const size_t rec = rec_bytes();
-  PGR_HIP(launch_kv_append(k_new, v_new, pool_[layer], d_append_slot_, d_append_pos_, S, cfg_.kv_heads, T,
-                           cfg_.head_dim, stream));
   PagedLaunch pl{};
   pl.q = q;
+  pl.k_new = k_new;
+  pl.v_new = v_new;
   pl.pool = pool_[layer];
   pl.stage = stage_;
   pl.seqs = d_seqs_;
@@ -863,6 +889,9 @@ int PagedKV::decode_layer(int layer, const void* q, const void* k_new, const voi
   pl.pacc = d_pacc_;
   pl.mass_m = mass_accum ? d_mass_m_ : nullptr;
   pl.mass_s = mass_accum ? d_mass_s_ : nullptr;
+  pl.out = out;
+  pl.mf = d_mf_;
+  pl.lf = d_lf_;
   pl.hq = hq;
   pl.hkv = cfg_.kv_heads;
   pl.tokens_per_block = T;
@@ -905,8 +934,7 @@ int PagedKV::decode_layer(int layer, const void* q, const void* k_new, const voi
     }
     if (n_chunks_ > 0) PGR_HIP(hipEventRecord(buf_free_[buf], stream));
   }
-  PGR_HIP(launch_paged_merge(cfg_.dtype, d_seqs_, S, hq, cfg_.head_dim, d_pm_, d_pl_, d_pacc_, out, d_mf_, d_lf_,
-                             nullptr, stream));
+  PGR_HIP(launch_paged_merge(cfg_.dtype, cfg_.head_dim, pl, (int)seqs_.size(), stream));
   if (mass_accum) {
     PGR_HIP(launch_mass_reduce(d_seqs_, d_sess_rows_, d_sess_first_, d_mass_m_, d_mass_s_, d_mf_, d_lf_, mass_accum,
                                (int)accum_stride, hq, mass_stride_, (int)step_sids_.size(), mass_stride_, stream));

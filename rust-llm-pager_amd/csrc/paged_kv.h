@@ -39,7 +39,7 @@ struct PagedKVConfig {
   int64_t staging_slots = 0;     // records per staging buffer
   int staging_buffers = 2;       // ring depth
   int blocks_per_workgroup = 16; // most block entries folded by one workgroup (4 waves)
-  int target_workgroups = 768;   // workgroups a launch aims for: 3 resident per CU
+  int target_workgroups = 0;     // workgroups a launch aims for (0: a multiple of the CU count)
 };
 
 struct StoreStats {
@@ -173,6 +173,7 @@ class PagedKV {
   int64_t host_alloc(int64_t n);
   void host_free(int64_t off, int64_t n);
   int ensure_workspace(size_t bytes);
+  int default_workgroups() const;
   int ensure_block_capacity(Session& s, int64_t blocks);
   int move_block(Session& s, int64_t b, bool to_gpu, hipStream_t stream);
   int resolve_timing();
@@ -184,6 +185,7 @@ class PagedKV {
   void* stage_ = nullptr;
   void* ws_ = nullptr;
   size_t ws_bytes_ = 0;
+  int n_cu_ = 0;                  // compute units of the device
   void* plan_host_ = nullptr;  // pinned upload buffer for the step plan
   size_t plan_host_bytes_ = 0;
   float* mass_host_ = nullptr;  // pinned readback of the step's block mass
@@ -212,7 +214,6 @@ class PagedKV {
   std::vector<int> launch_work_begin_;  // per launch: first work item; launches = chunks or 1
   std::vector<int> launch_work_end_;
   std::vector<CopyCmd> copies_;
-  std::vector<int32_t> append_slot_, append_pos_;
   std::vector<std::vector<int64_t>> step_host_ids_;
   int n_chunks_ = 0;
   int n_partials_ = 0;
@@ -222,11 +223,9 @@ class PagedKV {
   // Device views into the workspace for the current step.
   SeqInfo* d_seqs_ = nullptr;
   WorkItem* d_work_ = nullptr;
-  int32_t* d_append_slot_ = nullptr;
-  int32_t* d_append_pos_ = nullptr;
   int32_t* d_sess_rows_ = nullptr;
   int32_t* d_sess_first_ = nullptr;
-  float *d_pm_ = nullptr, *d_pl_ = nullptr, *d_pacc_ = nullptr;
+  float *d_pm_ = nullptr, *d_pl_ = nullptr, *d_pacc_ = nullptr;  // split-K partials
   float *d_mass_m_ = nullptr, *d_mass_s_ = nullptr, *d_mf_ = nullptr, *d_lf_ = nullptr;
   StepStats step_stats_;
 

@@ -42,21 +42,22 @@ struct WorkItem {
   int32_t seq;          // sequence index: row of q / out
   int32_t partial;      // partial-result slot written by this workgroup
   int32_t entry_count;  // number of entries (blocks) it folds
-  int32_t lo;           // valid token range [lo, hi) of the sequence
+  int32_t lo;           // stored valid tokens [lo, hi) of the sequence
   int32_t hi;
   int32_t n_mass;       // blocks below this id get a mass entry
-  int32_t pad_[2];
+  int32_t append_slot;  // >= 0 (one work item per sequence): write the current token's K/V to
+  int32_t append_pos;   // position append_pos of pool record append_slot
   BlockEntry entries[kMaxWorkEntries];
 };
 
 // Per-sequence scalars of a paged decode step.
 struct SeqInfo {
   int32_t lo;            // first valid token position (left padding / sliding window)
-  int32_t hi;            // one past the last valid token (includes the current token)
+  int32_t hi;            // position of the current token: stored tokens [lo, hi) are read
   int32_t n_mass;        // blocks [0, n_mass) get a mass entry (the full blocks known before this step)
   int32_t mass_lo;       // first block id in scope for mass (blocks below were skipped: mass 0)
   int32_t partial_base;  // first partial slot of this sequence
-  int32_t partial_count; // number of partial slots of this sequence
+  int32_t partial_count; // number of partial slots (work items) of this sequence
   int32_t session;       // session index (rows of one session share placement and mass)
   int32_t pad_;
 };

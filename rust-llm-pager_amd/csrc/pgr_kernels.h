@@ -26,9 +26,15 @@ struct DenseLaunch {
   float scale, softcap;
 };
 
+// The paged decode kernels of one layer. launch_paged folds work items [work, work + n_work)
+// into partial slots (and the work item that carries an append target writes the current
+// token's K/V into the pool); launch_paged_merge then combines each sequence's partials
+// with the current token (k_new/v_new) into out and the final (mf, lf).
 struct PagedLaunch {
   const void* q;
-  const void* pool;
+  const void* k_new;
+  const void* v_new;
+  void* pool;
   const void* stage;
   const WorkItem* work;
   const SeqInfo* seqs;
@@ -37,6 +43,9 @@ struct PagedLaunch {
   float* pacc;
   float* mass_m;
   float* mass_s;
+  void* out;
+  float* mf;
+  float* lf;
   int n_work, hq, hkv, tokens_per_block, mass_stride;
   float scale, softcap;
 };
@@ -48,19 +57,13 @@ hipError_t launch_dense(int dtype, int mode, int d, const DenseLaunch& p, hipStr
 hipError_t launch_finalize(int dtype, const float* acc, const float* l, void* out, int rows, int d,
                            hipStream_t stream);
 hipError_t launch_paged(int dtype, int d, const PagedLaunch& p, hipStream_t stream);
-hipError_t launch_paged_merge(int dtype, const SeqInfo* seqs, int n_seq, int hq, int d, const float* pm,
-                              const float* pl, const float* pacc, void* out, float* mf, float* lf, float* acc_out,
-                              hipStream_t stream);
+hipError_t launch_paged_merge(int dtype, int d, const PagedLaunch& p, int n_seq, hipStream_t stream);
 hipError_t launch_mass_reduce(const SeqInfo* seqs, const int32_t* session_rows, const int32_t* session_first,
                               const float* mass_m, const float* mass_s, const float* mf, const float* lf,
                               float* mass_accum, int accum_stride, int hq, int mass_stride, int n_sessions,
                               int max_blocks, hipStream_t stream);
 
 // kv_kernels.hip
-// Write one new token's K/V per sequence into its open block record:
-// k_new, v_new [S, Hkv, D]; slot[S], pos[S] (token offset inside the block).
-hipError_t launch_kv_append(const void* k_new, const void* v_new, void* pool, const int32_t* slots,
-                            const int32_t* pos, int n_seq, int hkv, int tokens_per_block, int d, hipStream_t stream);
 // Reference block layout <-> pool records for one layer:
 // ref [B, T, Hkv, D] (a layer slice of the [L, B, T, Hkv, D] block) <-> records [B][2][Hkv][T][D].
 hipError_t launch_ref_to_records(const void* key, const void* value, void* pool, const int32_t* slots, int rows,
