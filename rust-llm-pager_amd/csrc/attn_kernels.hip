@@ -510,7 +510,7 @@ struct TileMeta {
 
 template <int D>
 struct PagedRing {
-  static constexpr int NB = D <= 64 ? 4 : 3;  // register tiles per wave
+  static constexpr int NB = D <= 64 ? 2 : 3;  // register tiles per wave
 };
 
 template <class Ty, int D, bool kMass>
@@ -673,145 +673,113 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(PagedArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------
-// Split-K merge: one workgroup per (sequence, KV head) combines the sequence's partial slots
-// for the group's n_rep query heads with the current token (score q.k_new, weight 2^(x - m),
-// P rounded like every other P), and writes the output and the final (m, l) for the mass
-// pass. Each phase keeps many independent loads in flight: the partials are a few KB per
-// slot and the kernel is latency-bound.
-constexpr int kSeqMergeChunk = 128;  // partial weights staged in LDS at a time
-
-__device__ __forceinline__ float sum16(float x) {
-  x += __shfl_xor(x, 8);
-  x += __shfl_xor(x, 4);
-  x += __shfl_xor(x, 2);
-  return x + __shfl_xor(x, 1);
-}
-__device__ __forceinline__ float max16(float x) {
-  x = fmaxf(x, __shfl_xor(x, 8));
-  x = fmaxf(x, __shfl_xor(x, 4));
-  x = fmaxf(x, __shfl_xor(x, 2));
-  return fmaxf(x, __shfl_xor(x, 1));
-}
+// Split-K merge: one workgroup per (sequence, query head). Thread (g, c) owns output dims
+// 2c, 2c+1 and merges the partial slots g, g+G, g+2G, ... online (running max, rescaled
+// sums), G = 512 / D thread groups; the groups are then combined through LDS together with
+// the current token (score q.k_new, weight 2^(x - m), P rounded like every other P), and the
+// output and the final (m, l) for the mass pass are written. The kernel is latency-bound:
+// each thread issues a whole batch of partial loads before using any of them (a load past
+// the last partial re-reads it and is weighted 0).
+constexpr int kMergeBatch = 8;
 
 template <class Ty, int D>
 __global__ __launch_bounds__(256) void paged_merge_kernel(PagedArgs a) {
-  constexpr int kC = (kMaxRep * D / 2 + 255) / 256;  // float2 chunks of the group's acc per thread
-  constexpr int kU = 32 / kC;                        // partials loaded per chunk per batch
-  __shared__ float w_s[kMaxRep][kSeqMergeChunk];
-  __shared__ float lf_s[kMaxRep], pc_s[kMaxRep];
-  const int seq = blockIdx.x, h = blockIdx.y;
+  constexpr int kLanes = D / 2;          // threads per partial group (two dims each)
+  constexpr int G = 256 / kLanes;        // partial groups
+  constexpr int kU = kMergeBatch;
+  __shared__ float m_s[G], l_s[G];
+  __shared__ float acc_s[G][D];
+  const int seq = blockIdx.x, qh = blockIdx.y;
   const int tid = threadIdx.x;
-  const int r = tid >> 4, j = tid & 15;  // 16 lanes per query head of the group
-  const bool rv = r < a.n_rep;
-  const int hq = a.hq;
-  const int qh = h * a.n_rep + (rv ? r : 0);
+  const int c = tid % kLanes, grp = tid / kLanes;
+  const int hq = a.hq, h = qh / a.n_rep;
   const SeqInfo* si = a.seqs + seq;
-  const int P = si->partial_count, base = si->partial_base;
+  const int P = si->partial_count, base = si->partial_base;  // P >= 1: every sequence has a work item
   const size_t kv_row = ((size_t)seq * a.hkv + h) * D;
 
-  // Current token: x = mult * s' (s' softcapped like every score); it is always valid.
-  float dot = 0.f;
-  if (rv) {
-    const uint16_t* qp = a.q + ((size_t)seq * hq + qh) * D;
-#pragma unroll
-    for (int d = j; d < D; d += 16) dot += Ty::to_f(qp[d]) * Ty::to_f(a.k_new[kv_row + d]);
+  // Group 0 also computes the current token's score (its loads overlap the partial loads).
+  uint32_t qd = 0, kd = 0, vd = 0;
+  if (grp == 0) {
+    qd = *reinterpret_cast<const uint32_t*>(a.q + ((size_t)seq * hq + qh) * D + 2 * c);
+    kd = *reinterpret_cast<const uint32_t*>(a.k_new + kv_row + 2 * c);
+    vd = *reinterpret_cast<const uint32_t*>(a.v_new + kv_row + 2 * c);
   }
-  dot = sum16(dot);
+
+  const float* pm = a.pm + (size_t)base * hq + qh;
+  const float* pl = a.pl + (size_t)base * hq + qh;
+  const float* pa = a.pacc + ((size_t)base * hq + qh) * D + 2 * c;
+  const size_t stride_a = (size_t)hq * D;
+  float m = kNegInf, l = 0.f;
+  float2 acc = float2{0.f, 0.f};
+  for (int p0 = grp; p0 < P; p0 += G * kU) {
+    float xm[kU], xl[kU];
+    float2 xa[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int p = min(p0 + G * u, P - 1);
+      xm[u] = pm[(size_t)p * hq];
+      xl[u] = pl[(size_t)p * hq];
+      xa[u] = *reinterpret_cast<const float2*>(pa + (size_t)p * stride_a);
+    }
+    float bmax = kNegInf;
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      if (p0 + G * u >= P) xm[u] = kNegInf;  // re-read past the end: weight 0
+      bmax = fmaxf(bmax, xm[u]);
+    }
+    const float m_new = fmaxf(m, bmax);
+    const float mm = m_new == kNegInf ? 0.f : m_new;  // nothing valid yet: every weight is 0
+    const float alpha = __builtin_amdgcn_exp2f(m - mm);
+    l *= alpha;
+    acc.x *= alpha;
+    acc.y *= alpha;
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const float w = __builtin_amdgcn_exp2f(xm[u] - mm);
+      l += xl[u] * w;
+      acc.x += xa[u].x * w;
+      acc.y += xa[u].y * w;
+    }
+    m = m_new;
+  }
+  if (c == 0) {
+    m_s[grp] = m;
+    l_s[grp] = l;
+  }
+  acc_s[grp][2 * c] = acc.x;
+  acc_s[grp][2 * c + 1] = acc.y;
+  __syncthreads();
+  if (grp != 0) return;
+
+  float dot = Ty::to_f((uint16_t)(qd & 0xffffu)) * Ty::to_f((uint16_t)(kd & 0xffffu)) +
+              Ty::to_f((uint16_t)(qd >> 16)) * Ty::to_f((uint16_t)(kd >> 16));
+#pragma unroll
+  for (int o = kLanes / 2; o > 0; o >>= 1) dot += __shfl_xor(dot, o);
   float x_cur;
   if (a.softcap > 0.f)
     x_cur = a.softcap * tanhf(dot * (a.scale / a.softcap)) * kLog2e;
   else
     x_cur = dot * (a.scale * kLog2e);
-
-  float mx = kNegInf;
-  if (rv) {
-    for (int p0 = 0; p0 < P; p0 += 128) {
-      float v[8];
+  float mf = x_cur;  // the current token is always valid: mf is finite
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int p = p0 + j + 16 * u;
-        v[u] = p < P ? a.pm[(size_t)(base + p) * hq + qh] : kNegInf;
-      }
-#pragma unroll
-      for (int u = 0; u < 8; ++u) mx = fmaxf(mx, v[u]);
-    }
-  }
-  const float mf = fmaxf(max16(mx), x_cur);
-
-  const int C = a.n_rep * D / 2;  // float2 chunks of the group's acc rows
-  float2 acc[kC];
-#pragma unroll
-  for (int k = 0; k < kC; ++k) acc[k] = float2{0.f, 0.f};
-  float ls = 0.f;
-  const size_t stride = (size_t)hq * D;  // floats between consecutive partial slots
-  const float* acc_base = a.pacc + ((size_t)base * hq + (size_t)h * a.n_rep) * D;
-  for (int p0 = 0; p0 < P; p0 += kSeqMergeChunk) {
-    const int cnt = min(kSeqMergeChunk, P - p0);
-    if (rv) {
-      float vm[8], vl[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int p = j + 16 * u;
-        const size_t pi = (size_t)(base + p0 + p) * hq + qh;
-        vm[u] = p < cnt ? a.pm[pi] : kNegInf;
-        vl[u] = p < cnt ? a.pl[pi] : 0.f;
-      }
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int p = j + 16 * u;
-        const float w = __builtin_amdgcn_exp2f(vm[u] - mf);  // empty partial: m = -inf, w = 0
-        if (p < cnt) w_s[r][p] = w;
-        ls += vl[u] * w;
-      }
-    }
-    __syncthreads();
-    for (int q0 = 0; q0 < cnt; q0 += kU) {
-      float2 v[kC][kU];
-#pragma unroll
-      for (int k = 0; k < kC; ++k) {
-        const int c = tid + 256 * k;
-#pragma unroll
-        for (int u = 0; u < kU; ++u) {
-          const int p = q0 + u;
-          v[k][u] = (c < C && p < cnt) ? *reinterpret_cast<const float2*>(acc_base + (size_t)(p0 + p) * stride + 2 * c)
-                                       : float2{0.f, 0.f};
-        }
-      }
-#pragma unroll
-      for (int k = 0; k < kC; ++k) {
-        const int c = tid + 256 * k;
-        const int ro = min(2 * c / D, kMaxRep - 1);
-#pragma unroll
-        for (int u = 0; u < kU; ++u) {
-          const float w = q0 + u < cnt ? w_s[ro][q0 + u] : 0.f;
-          acc[k].x += v[k][u].x * w;
-          acc[k].y += v[k][u].y * w;
-        }
-      }
-    }
-    __syncthreads();
-  }
-  ls = sum16(ls);
+  for (int g2 = 0; g2 < G; ++g2) mf = fmaxf(mf, m_s[g2]);
   const float pc = __builtin_amdgcn_exp2f(x_cur - mf);
-  if (rv && j == 0) {
-    lf_s[r] = ls + pc;
-    pc_s[r] = Ty::to_f(Ty::cvt(pc));  // P rounded to the K/V type before P.V
-    a.mf[(size_t)seq * hq + qh] = mf;
-    a.lf[(size_t)seq * hq + qh] = ls + pc;
-  }
-  __syncthreads();
+  const float pcr = Ty::to_f(Ty::cvt(pc));  // P rounded to the K/V type before P.V
+  float lf = pc;
+  float o0 = pcr * Ty::to_f((uint16_t)(vd & 0xffffu));
+  float o1 = pcr * Ty::to_f((uint16_t)(vd >> 16));
 #pragma unroll
-  for (int k = 0; k < kC; ++k) {
-    const int c = tid + 256 * k;
-    if (c < C) {
-      const int e = 2 * c, ro = e / D, d = e - ro * D;
-      const float pcr = pc_s[ro], lf = lf_s[ro];
-      const float v0 = acc[k].x + pcr * Ty::to_f(a.v_new[kv_row + d]);
-      const float v1 = acc[k].y + pcr * Ty::to_f(a.v_new[kv_row + d + 1]);
-      uint16_t* o = a.out + ((size_t)seq * hq + h * a.n_rep + ro) * D + d;
-      o[0] = Ty::cvt(v0 / lf);
-      o[1] = Ty::cvt(v1 / lf);
-    }
+  for (int g2 = 0; g2 < G; ++g2) {
+    const float w = __builtin_amdgcn_exp2f(m_s[g2] - mf);  // empty group: m = -inf, w = 0
+    lf += l_s[g2] * w;
+    o0 += acc_s[g2][2 * c] * w;
+    o1 += acc_s[g2][2 * c + 1] * w;
+  }
+  const uint32_t packed = (uint32_t)Ty::cvt(o0 / lf) | ((uint32_t)Ty::cvt(o1 / lf) << 16);
+  *reinterpret_cast<uint32_t*>(a.out + ((size_t)seq * hq + qh) * D + 2 * c) = packed;
+  if (c == 0) {
+    a.mf[(size_t)seq * hq + qh] = mf;
+    a.lf[(size_t)seq * hq + qh] = lf;
   }
 }
 
@@ -1024,7 +992,7 @@ hipError_t launch_paged_merge(int dtype, int d, const PagedLaunch& p, int n_seq,
   a.n_rep = p.hq / p.hkv;
   a.scale = p.scale;
   a.softcap = p.softcap;
-  dim3 grid(n_seq, p.hkv);
+  dim3 grid(n_seq, p.hq);
 #define PGR_MERGE(TY, DD) paged_merge_kernel<TY, DD><<<grid, 256, 0, stream>>>(a)
   if (dtype == kF16) {
     if (d == 32) PGR_MERGE(F16, 32);
