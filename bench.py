@@ -4,8 +4,15 @@ Workload (one "step" = one decode step of one layer over the whole batch): Qwen2
 attention geometry (14 query heads, 2 KV heads, head_dim 64, fp16, 32-token blocks), batch 8,
 contexts drawn uniform in [1024, 32768] from a seed, each sequence keeping its 64 most recent
 blocks in HBM and the rest in pinned host RAM (recent_only placement). Every step appends one
-token per sequence, streams the host blocks, attends, and evicts the block that leaves the
-resident window. Synthetic N(0,1)*0.5 data. Prints one JSON line.
+token per sequence, reads the host blocks over the host link (in place, or through a staging
+ring with --stream-mode staged), attends, and evicts the block that leaves the resident
+window. `value` is the (HBM + host) K/V bytes per step over the step time; `host_link` the
+host part against PCIe Gen5 x16.
+
+The HBM roofline is measured on the same batch with every block resident, over 24 layers
+(1.45 GB of K/V per step, beyond the 256 MB MALL): `roofline` is paged_attn_kernel's K/V
+bytes per launch over its HIP-event launch time there. Synthetic N(0,1)*0.5 data. Prints one
+JSON line.
 """
 from __future__ import annotations
 
@@ -34,7 +41,7 @@ def draw_contexts(seed, batch, lo, hi):
 
 
 def build(steps_total, staging_blocks=2048, staging_buffers=3, blocks_per_wg=16, resident_blocks=None,
-          target_wg=0):
+          target_wg=0, layers=1, stream_mode="direct"):
     import torch
 
     from pager_hf import PagedDecoder
@@ -44,20 +51,21 @@ def build(steps_total, staging_blocks=2048, staging_buffers=3, blocks_per_wg=16,
         c["resident_blocks"] = resident_blocks
     ctx = draw_contexts(c["seed"], c["batch"], c["ctx_lo"], c["ctx_hi"])
     dec = PagedDecoder(
-        num_layers=1, num_query_heads=c["hq"], num_kv_heads=c["hkv"], head_dim=c["d"], tokens_per_block=c["tpb"],
+        num_layers=layers, num_query_heads=c["hq"], num_kv_heads=c["hkv"], head_dim=c["d"], tokens_per_block=c["tpb"],
         dtype=torch.float16, device="cuda", pool_blocks=c["batch"] * (c["resident_blocks"] + 4),
         host_blocks=sum(n // c["tpb"] + steps_total // c["tpb"] + 8 for n in ctx), staging_blocks=staging_blocks,
         staging_buffers=staging_buffers, blocks_per_workgroup=blocks_per_wg, target_workgroups=target_wg,
+        stream_mode=stream_mode,
     )
     gen = torch.Generator(device="cuda").manual_seed(c["seed"])
     sids = []
     for n in ctx:
         sid = dec.add_session(capacity_tokens=n + steps_total + 64, vram_budget=c["resident_blocks"] * MIB16,
                               ram_budget=1 << 40, recent_window=c["resident_blocks"] - 1, policy="recent_only")
-        k = (torch.randn(1, c["hkv"], n, c["d"], device="cuda", generator=gen) * 0.5).half()
-        v = (torch.randn(1, c["hkv"], n, c["d"], device="cuda", generator=gen) * 0.5).half()
-        dec.prefill(sid, [k], [v], n)
-        del k, v
+        ks = [(torch.randn(1, c["hkv"], n, c["d"], device="cuda", generator=gen) * 0.5).half() for _ in range(layers)]
+        vs = [(torch.randn(1, c["hkv"], n, c["d"], device="cuda", generator=gen) * 0.5).half() for _ in range(layers)]
+        dec.prefill(sid, ks, vs, n)
+        del ks, vs
         sids.append(sid)
     S = c["batch"]
     q = (torch.randn(steps_total, S, c["hq"], c["d"], device="cuda", generator=gen) * 0.5).half()
@@ -76,8 +84,71 @@ def run_steps(dec, sids, q, kn, vn, out, first, count, stats):
         stats["host_tokens"] += st["host_tokens"]
         stats["copies"] += st["copies"]
         stats["launches"] += st["launches"]
-        dec.decode_layer(0, q[i], kn[i], vn[i], out)
+        for layer in range(dec.num_layers):
+            dec.decode_layer(layer, q[i], kn[i], vn[i], out)
         dec.end_step(collect=False)
+
+
+def hbm_all_resident(layers, steps, warmup):
+    """The same batch with every block resident in HBM, over `layers` layers (one launch pair
+    per layer, so the K/V read per step exceeds the 256 MB MALL and comes from HBM)."""
+    import torch
+
+    dec, sids, ctx, q, kn, vn, out = build(warmup + 2 * steps, resident_blocks=1100, layers=layers)
+    stats = {"resident_tokens": 0, "host_tokens": 0, "copies": 0, "launches": 0}
+    run_steps(dec, sids, q, kn, vn, out, 0, warmup, stats)
+    # Pass 1: step rate (no per-launch events).
+    stats = {"resident_tokens": 0, "host_tokens": 0, "copies": 0, "launches": 0}
+    torch.cuda.synchronize()
+    dec.pool.sync()
+    t0 = time.perf_counter()
+    run_steps(dec, sids, q, kn, vn, out, warmup, steps, stats)
+    torch.cuda.synchronize()
+    dec.pool.sync()
+    dt = time.perf_counter() - t0
+    # Pass 2: the attention kernel's own execution time, event-stamped per launch.
+    dec.pool.kernel_time()
+    dec.pool.set_timing(True)
+    run_steps(dec, sids, q, kn, vn, out, warmup + steps, steps, {"resident_tokens": 0, "host_tokens": 0,
+                                                                  "copies": 0, "launches": 0})
+    torch.cuda.synchronize()
+    dec.pool.sync()
+    k_ms, k_launches, k_bytes = dec.pool.kernel_time()
+    dec.pool.close()
+    c = CFG
+    tok_bytes = 2 * c["hkv"] * c["d"] * 2
+    layer_bytes = stats["resident_tokens"] * tok_bytes // steps  # K/V bytes one layer-step reads
+    kernel_gbs = k_bytes / (k_ms / 1e3) / 1e9
+    step_gbs = layer_bytes * layers * steps / dt / 1e9
+    return {
+        "workload": f"the same batch with every block resident in HBM, {layers} layers",
+        "layers": layers,
+        "steps": steps,
+        "kv_bytes_per_layer_step": layer_bytes,
+        "ms_per_step": round(dt / steps * 1e3, 4),
+        "tokens_per_s": round(c["batch"] * steps / dt, 2),
+        "kernel": {"name": "paged_attn_kernel", "launches": k_launches,
+                   "avg_launch_us": round(k_ms * 1e3 / max(k_launches, 1), 3),
+                   "bytes_per_launch": k_bytes // max(k_launches, 1),
+                   "achieved": round(kernel_gbs, 2), "frac": round(kernel_gbs / HBM_PEAK_GBS, 4)},
+        "step": {"achieved": round(step_gbs, 2), "frac": round(step_gbs / HBM_PEAK_GBS, 4),
+                 "note": "whole decode step per layer (planning, both kernels, host glue) over K/V bytes"},
+        "unit": "GB/s",
+        "peak": HBM_PEAK_GBS,
+    }
+
+
+def committed_traffic(workload_layers):
+    """HBM bytes per launch of the all-resident kernel from the committed counter summary
+    (FETCH_SIZE and WRITE_SIZE scaled by a plain copy's readings), or None."""
+    path = os.path.join(ROOT, "profiles", "paged_attn_all_resident_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        t = json.load(f)
+    if t.get("layers") != workload_layers or t.get("batch") != CFG["batch"]:
+        return None
+    return t.get("traffic_bytes_per_launch")
 
 
 def cpu_baseline(ctx, budget_s=15.0):
@@ -127,6 +198,10 @@ def main() -> int:
     ap.add_argument("--resident-blocks", type=int, default=CFG["resident_blocks"],
                     help="HBM-resident blocks per sequence (1100 keeps every block resident)")
     ap.add_argument("--target-wg", type=int, default=0, help="workgroups per attention launch (0 = library default)")
+    ap.add_argument("--stream-mode", choices=["direct", "staged"], default="direct",
+                    help="host blocks read in place over the host link, or copied into a staging ring")
+    ap.add_argument("--resident-layers", type=int, default=24,
+                    help="layers of the all-resident HBM measurement (0 skips it)")
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
                     help="after timing, run one device copy of this size (counter calibration)")
     args = ap.parse_args()
@@ -142,7 +217,7 @@ def main() -> int:
     c = CFG
     total = args.warmup + args.steps
     dec, sids, ctx, q, kn, vn, out = build(total, args.staging_blocks, args.staging_buffers, args.blocks_per_wg,
-                                          args.resident_blocks, args.target_wg)
+                                          args.resident_blocks, args.target_wg, 1, args.stream_mode)
     warm = {"resident_tokens": 0, "host_tokens": 0, "copies": 0, "launches": 0}
     run_steps(dec, sids, q, kn, vn, out, 0, args.warmup, warm)
     torch.cuda.synchronize()
@@ -184,6 +259,7 @@ def main() -> int:
                         "HBM and the rest in pinned host RAM, 1 token appended per sequence per step",
             "contexts": ctx,
             "batch": c["batch"],
+            "stream_mode": args.stream_mode,
             "staging": {"records_per_buffer": args.staging_blocks, "buffers": args.staging_buffers},
         },
         "tokens_per_s": round(c["batch"] * args.steps / dt, 2),
@@ -194,19 +270,17 @@ def main() -> int:
             "frac": round(link_gbs / LINK_PEAK_GBS, 4),
             "bytes_per_step": host_bytes // args.steps,
             "copies_per_step": stats["copies"] / args.steps,
+            "note": "host-resident K/V bytes per step over the step time; peak = PCIe Gen5 x16 nominal",
         },
         "hbm_resident": {"bytes_per_step": hbm_bytes // args.steps, "blocks_per_sequence": args.resident_blocks},
-        "roofline": {
-            "bound": "hbm",
-            "kernel": "paged_attn_kernel",
-            "achieved": round(kernel_gbs, 2),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(kernel_gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+        "kernel": {
+            "name": "paged_attn_kernel",
             "launches": k_launches,
             "avg_launch_us": round(k_ms * 1e3 / max(k_launches, 1), 3),
             "bytes_per_launch": k_bytes // max(k_launches, 1),
+            "achieved": round(kernel_gbs, 2),
+            "unit": "GB/s",
+            "note": "K/V bytes (HBM + host) per launch over the launch time in this workload",
         },
     }
     if args.calibration_copy_mib:
@@ -216,9 +290,28 @@ def main() -> int:
         dst.copy_(src)
         torch.cuda.synchronize()
         line["calibration_copy_bytes"] = n
+    dec.pool.close()
+    del dec
+    line["roofline"] = None
+    if args.resident_layers > 0:
+        res = hbm_all_resident(args.resident_layers, max(4, min(args.steps, 16)), 2)
+        line["hbm_all_resident"] = res
+        kern = res["kernel"]
+        line["roofline"] = {
+            "bound": "hbm",
+            "kernel": "paged_attn_kernel",
+            "workload": res["workload"],
+            "achieved": kern["achieved"],
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": kern["frac"],
+            "traffic": committed_traffic(args.resident_layers),
+            "launches": kern["launches"],
+            "avg_launch_us": kern["avg_launch_us"],
+            "bytes_per_launch": kern["bytes_per_launch"],
+        }
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(ctx, args.cpu_seconds)
-    dec.pool.close()
     print(json.dumps(line), flush=True)
     return 0
 

@@ -142,7 +142,15 @@ typedef struct pgr_kv_config_s {
   int32_t staging_buffers;  /* ring depth, >= 1 (2 = double buffering) */
   int32_t blocks_per_workgroup; /* most block entries per workgroup (4..16) */
   int32_t target_workgroups;    /* workgroups a launch aims for (0 = a multiple of the CU count) */
+  int32_t stream_mode;          /* PGR_STREAM_DIRECT (0) or PGR_STREAM_STAGED (1), see below */
 } pgr_kv_config_t;
+
+/* How decode reads host-resident blocks. DIRECT: the attention kernel reads them in place from
+ * the pinned host mirror (mapped into the device address space) over the host link, in the
+ * same launch as the HBM-resident blocks. STAGED: runs of host blocks are copied into an HBM
+ * staging ring with hipMemcpyAsync on a side stream, double-buffered against the kernel. */
+#define PGR_STREAM_DIRECT 0
+#define PGR_STREAM_STAGED 1
 
 typedef struct pgr_kv_stats_s {
   uint64_t gpu_to_cpu_bytes, cpu_to_gpu_bytes, gpu_to_cpu_copies, cpu_to_gpu_copies;

@@ -30,7 +30,10 @@ MODE_STATS = 1
 MODE_ACCUMULATE = 2
 MODE_FOLD_FIXED = 3
 
-ABI_VERSION = 1
+STREAM_DIRECT = 0
+STREAM_STAGED = 1
+
+ABI_VERSION = 2
 
 c_i32, c_i64, c_u8, c_u32, c_u64 = ctypes.c_int32, ctypes.c_int64, ctypes.c_uint8, ctypes.c_uint32, ctypes.c_uint64
 c_f32, c_f64, c_size, c_vp = ctypes.c_float, ctypes.c_double, ctypes.c_size_t, ctypes.c_void_p
@@ -63,6 +66,7 @@ class KVConfig(ctypes.Structure):
         ("staging_buffers", c_i32),
         ("blocks_per_workgroup", c_i32),
         ("target_workgroups", c_i32),
+        ("stream_mode", c_i32),
     ]
 
 

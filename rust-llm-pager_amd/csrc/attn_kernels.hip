@@ -26,6 +26,7 @@
 //
 // P is rounded to the K/V element type before the P.V product, as the reference does
 // (streaming_attention.py:178, :347, :428).
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include "pgr_common.h"
@@ -857,13 +858,22 @@ hipError_t launch_dense_ty(const DenseArgs& a, int mode, int batch, int d, float
   }
 }
 
+// With start/stop events, the launch itself timestamps the kernel's execution (the events
+// bracket the dispatch packet, not the queue ahead of it).
 template <class Ty, int D>
-hipError_t launch_paged_t(const PagedArgs& a, int n_work, bool mass, hipStream_t stream) {
+hipError_t launch_paged_t(const PagedArgs& a, int n_work, bool mass, hipEvent_t ev_start, hipEvent_t ev_stop,
+                          hipStream_t stream) {
   dim3 grid(n_work, a.hkv);
-  if (mass)
+  if (ev_start != nullptr) {
+    if (mass)
+      hipExtLaunchKernelGGL(paged_attn_kernel<Ty, D, true>, grid, dim3(256), 0, stream, ev_start, ev_stop, 0, a);
+    else
+      hipExtLaunchKernelGGL(paged_attn_kernel<Ty, D, false>, grid, dim3(256), 0, stream, ev_start, ev_stop, 0, a);
+  } else if (mass) {
     paged_attn_kernel<Ty, D, true><<<grid, 256, 0, stream>>>(a);
-  else
+  } else {
     paged_attn_kernel<Ty, D, false><<<grid, 256, 0, stream>>>(a);
+  }
   return hipGetLastError();
 }
 
@@ -957,20 +967,20 @@ hipError_t launch_paged(int dtype, int d, const PagedLaunch& p, hipStream_t stre
   if (dtype == kF16) {
     switch (d) {
       case 32:
-        return launch_paged_t<F16, 32>(a, p.n_work, mass, stream);
+        return launch_paged_t<F16, 32>(a, p.n_work, mass, p.ev_start, p.ev_stop, stream);
       case 64:
-        return launch_paged_t<F16, 64>(a, p.n_work, mass, stream);
+        return launch_paged_t<F16, 64>(a, p.n_work, mass, p.ev_start, p.ev_stop, stream);
       default:
-        return launch_paged_t<F16, 128>(a, p.n_work, mass, stream);
+        return launch_paged_t<F16, 128>(a, p.n_work, mass, p.ev_start, p.ev_stop, stream);
     }
   }
   switch (d) {
     case 32:
-      return launch_paged_t<BF16, 32>(a, p.n_work, mass, stream);
+      return launch_paged_t<BF16, 32>(a, p.n_work, mass, p.ev_start, p.ev_stop, stream);
     case 64:
-      return launch_paged_t<BF16, 64>(a, p.n_work, mass, stream);
+      return launch_paged_t<BF16, 64>(a, p.n_work, mass, p.ev_start, p.ev_stop, stream);
     default:
-      return launch_paged_t<BF16, 128>(a, p.n_work, mass, stream);
+      return launch_paged_t<BF16, 128>(a, p.n_work, mass, p.ev_start, p.ev_stop, stream);
   }
 }
 

@@ -125,7 +125,7 @@ int kv_rc(pgr::PagedKV* kv, int rc) {
 
 extern "C" {
 
-int pgr_abi_version(void) { return 1; }
+int pgr_abi_version(void) { return 2; }
 
 const char* pgr_last_error(void) { return g_last_error.c_str(); }
 
@@ -262,6 +262,7 @@ void* pgr_kv_create(const pgr_kv_config_t* c) {
   cfg.staging_buffers = c->staging_buffers;
   cfg.blocks_per_workgroup = c->blocks_per_workgroup > 0 ? c->blocks_per_workgroup : 16;
   cfg.target_workgroups = c->target_workgroups > 0 ? c->target_workgroups : 0;
+  cfg.stream_mode = c->stream_mode;
   auto* kv = new (std::nothrow) pgr::PagedKV(cfg);
   if (!kv) {
     set_err(pgr::kErrCapacity, "out of host memory");

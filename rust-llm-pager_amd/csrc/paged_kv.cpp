@@ -4,8 +4,9 @@
 // a Python loop gathering every block with a blocking .to(device) + permute + torch.cat,
 // then one Triton launch per 64-block group (two passes for attention-scoring policies).
 // Here one plan per step covers all layers: resident blocks are read in place from the HBM
-// pool, host blocks are streamed in contiguous runs into a staging ring on a side stream,
-// and one split-K kernel per staged chunk folds them, with a merge kernel at the end.
+// pool; host blocks are read in place from the pinned host mirror by the same kernel over
+// the host link (direct mode), or streamed in contiguous runs into a staging ring on a side
+// stream with one kernel launch per staged chunk (staged mode); a merge kernel follows.
 #include "paged_kv.h"
 
 #include <algorithm>
@@ -127,6 +128,8 @@ int PagedKV::init() {
   if (cfg_.dtype != kF16 && cfg_.dtype != kBF16) return fail(kErrInvalid, "dtype must be fp16 or bf16");
   if (cfg_.pool_slots <= 0 || cfg_.host_records < 0 || cfg_.staging_slots <= 0 || cfg_.staging_buffers < 1)
     return fail(kErrInvalid, "pool_slots, staging_slots > 0 and staging_buffers >= 1 required");
+  if (cfg_.stream_mode != 0 && cfg_.stream_mode != 1) return fail(kErrInvalid, "stream_mode must be 0 or 1");
+  if (cfg_.host_records > INT32_MAX / 2) return fail(kErrInvalid, "host_records too large for 32-bit record indices");
   if (cfg_.pool_slots > INT32_MAX / 2 || cfg_.staging_slots * cfg_.staging_buffers > INT32_MAX / 2)
     return fail(kErrInvalid, "pool or staging too large for 32-bit record indices");
   if (cfg_.blocks_per_workgroup < kWaves) cfg_.blocks_per_workgroup = kWaves;
@@ -136,9 +139,13 @@ int PagedKV::init() {
   const size_t rec = rec_bytes();
   pool_.assign(cfg_.num_layers, nullptr);
   host_.assign(cfg_.num_layers, nullptr);
+  host_dev_.assign(cfg_.num_layers, nullptr);
   for (int l = 0; l < cfg_.num_layers; ++l) {
     PGR_HIP(hipMalloc(&pool_[l], rec * (size_t)cfg_.pool_slots));
-    if (cfg_.host_records > 0) PGR_HIP(hipHostMalloc(&host_[l], rec * (size_t)cfg_.host_records, hipHostMallocDefault));
+    if (cfg_.host_records > 0) {
+      PGR_HIP(hipHostMalloc(&host_[l], rec * (size_t)cfg_.host_records, hipHostMallocDefault));
+      PGR_HIP(hipHostGetDevicePointer(&host_dev_[l], host_[l], 0));
+    }
   }
   PGR_HIP(hipMalloc(&stage_, rec * (size_t)cfg_.staging_slots * cfg_.staging_buffers));
   PGR_HIP(hipStreamCreateWithFlags(&copy_stream_, hipStreamNonBlocking));
@@ -710,6 +717,14 @@ int PagedKV::begin_step(const int32_t* sids, int n, hipStream_t stream) {
           if (!s.host_valid[x * s.rows + r]) return fail(kErrState, "host block without data (not imported)");
           host_ids.push_back(x);
         }
+        if (cfg_.stream_mode == 0) {  // direct: the kernel reads the host records in place
+          for (int64_t x = b; x < e; ++x)
+            pend.push_back({seq, BlockEntry{(int32_t)(-(s.row[r].host_off + x) - 1), (int32_t)x}, 0});
+          step_stats_.host_blocks += e - b;
+          step_stats_.host_tokens += (e - b) * T;
+          b = e;
+          continue;
+        }
         int64_t cur = b;
         while (cur < e) {
           if (used_in_chunk == chunk_cap) {
@@ -882,7 +897,7 @@ int PagedKV::decode_layer(int layer, const void* q, const void* k_new, const voi
   pl.k_new = k_new;
   pl.v_new = v_new;
   pl.pool = pool_[layer];
-  pl.stage = stage_;
+  pl.stage = cfg_.stream_mode == 0 ? host_dev_[layer] : stage_;
   pl.seqs = d_seqs_;
   pl.pm = d_pm_;
   pl.pl = d_pl_;
@@ -899,6 +914,7 @@ int PagedKV::decode_layer(int layer, const void* q, const void* k_new, const voi
   pl.scale = scale;
   pl.softcap = softcap;
   const int n_launch = (int)launch_work_begin_.size();
+  if (cfg_.stream_mode == 0) stats_.stream_bytes += (uint64_t)step_stats_.host_blocks * rec;
   size_t ci = 0;
   for (int L = 0; L < n_launch; ++L) {
     const int buf = (step_stage_base_ + L) % cfg_.staging_buffers;
@@ -919,14 +935,15 @@ int PagedKV::decode_layer(int layer, const void* q, const void* k_new, const voi
     pl.work = d_work_ + launch_work_begin_[L];
     pl.n_work = launch_work_end_[L] - launch_work_begin_[L];
     PendingTiming t{nullptr, nullptr, 0};
+    pl.ev_start = pl.ev_stop = nullptr;
     if (timing_) {
       PGR_HIP(hipEventCreate(&t.start));
       PGR_HIP(hipEventCreate(&t.stop));
-      PGR_HIP(hipEventRecord(t.start, stream));
+      pl.ev_start = t.start;
+      pl.ev_stop = t.stop;
     }
     PGR_HIP(launch_paged(cfg_.dtype, cfg_.head_dim, pl, stream));
     if (timing_) {
-      PGR_HIP(hipEventRecord(t.stop, stream));
       int64_t ent = 0;
       for (int w = launch_work_begin_[L]; w < launch_work_end_[L]; ++w) ent += work_[w].entry_count;
       t.bytes = ent * (int64_t)T * 2 * cfg_.head_dim * 2 * cfg_.kv_heads;  // K+V bytes read, whole blocks

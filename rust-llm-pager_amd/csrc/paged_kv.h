@@ -9,8 +9,10 @@
 //     row owning a contiguous range [host_off, host_off + capacity_blocks). Host-resident
 //     blocks with consecutive ids are therefore one contiguous run, and are streamed to the
 //     GPU with one multi-MiB copy per run.
-//   * Staging ring in HBM: `staging_buffers` buffers of `staging_slots` records, filled by
-//     host-to-device copies on a side stream and read by the attention kernel in place.
+//   * Staging ring in HBM: `staging_buffers` buffers of `staging_slots` records. In the staged
+//     stream mode, filled by host-to-device copies on a side stream and read by the attention
+//     kernel in place; in the direct mode (default) the kernel reads host blocks straight from
+//     the mirror over the host link and the ring only bounces imports/exports.
 // Blocks are immutable once full, so a host copy stays valid after the block is loaded back
 // to HBM and a later eviction of it needs no copy.
 #pragma once
@@ -40,6 +42,7 @@ struct PagedKVConfig {
   int staging_buffers = 2;       // ring depth
   int blocks_per_workgroup = 16; // most block entries folded by one workgroup (4 waves)
   int target_workgroups = 0;     // workgroups a launch aims for (0: a multiple of the CU count)
+  int stream_mode = 0;           // 0: kernels read host blocks in place; 1: staged copies
 };
 
 struct StoreStats {
@@ -182,6 +185,7 @@ class PagedKV {
   std::string err_;
   std::vector<void*> pool_;   // per layer
   std::vector<void*> host_;   // per layer (pinned)
+  std::vector<void*> host_dev_;  // per layer: device address of the pinned arena
   void* stage_ = nullptr;
   void* ws_ = nullptr;
   size_t ws_bytes_ = 0;

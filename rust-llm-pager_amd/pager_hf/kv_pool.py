@@ -1,7 +1,9 @@
 """Python handle of the native paged KV store (``pgr_kv_*`` in include/pgr.h).
 
 One NativeKVPool owns, for every layer, an HBM slot pool, a pinned host mirror and an HBM
-staging ring, plus the per-session block tables. Sessions are groups of rows that share one
+staging ring, plus the per-session block tables. ``stream_mode="direct"`` (default) has the
+decode kernel read host-resident blocks in place over the host link; ``"staged"`` copies
+them into the staging ring first. Sessions are groups of rows that share one
 placement (the reference's one-PagedModel-per-session model, kv_block_store.py:36-56).
 """
 from __future__ import annotations
@@ -51,6 +53,7 @@ class NativeKVPool:
         staging_buffers: int = 2,
         blocks_per_workgroup: int = 16,
         target_workgroups: int = 0,
+        stream_mode: str = "direct",
     ):
         self.device = torch.device(device)
         if self.device.type != "cuda":
@@ -64,6 +67,10 @@ class NativeKVPool:
         self.tokens_per_block = tokens_per_block
         self.dtype = dtype
         self.lib = N.lib()
+        modes = {"direct": nat.STREAM_DIRECT, "staged": nat.STREAM_STAGED}
+        if stream_mode not in modes:
+            raise ValueError(f"stream_mode must be one of {sorted(modes)}, got {stream_mode!r}")
+        self.stream_mode = stream_mode
         cfg = nat.KVConfig(
             num_layers=num_layers,
             kv_heads=num_kv_heads,
@@ -77,6 +84,7 @@ class NativeKVPool:
             staging_buffers=staging_buffers,
             blocks_per_workgroup=blocks_per_workgroup,
             target_workgroups=target_workgroups,
+            stream_mode=modes[stream_mode],
         )
         with torch.cuda.device(self.device):
             handle = self.lib.pgr_kv_create(ctypes.byref(cfg))

@@ -67,6 +67,7 @@ class PagedDecoder:
         target_workgroups: int = 0,
         scale: float | None = None,
         softcap: float | None = None,
+        stream_mode: str = "direct",
     ):
         self.pool = NativeKVPool(
             num_layers=num_layers,
@@ -82,6 +83,7 @@ class PagedDecoder:
             staging_buffers=staging_buffers,
             blocks_per_workgroup=blocks_per_workgroup,
             target_workgroups=target_workgroups,
+            stream_mode=stream_mode,
         )
         self.pool.set_ram_budget(ram_budget_bytes)
         self.device = self.pool.device
@@ -159,9 +161,10 @@ class PagedDecoder:
             if rc != 0:
                 raise RuntimeError(f"ram_budget exceeded while placing block {fail_block}")
             moves = {"to_gpu": to_gpu, "to_cpu": to_cpu}
-        for layer in range(self.num_layers):
-            for row in range(s.rows):
-                self.pool.import_tokens(sid, row, layer, keys[layer][row], values[layer][row], n_tokens)
+        if n_tokens:
+            for layer in range(self.num_layers):
+                for row in range(s.rows):
+                    self.pool.import_tokens(sid, row, layer, keys[layer][row], values[layer][row], n_tokens)
         return moves
 
     def num_blocks(self, sid: int) -> int:

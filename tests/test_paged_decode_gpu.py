@@ -31,12 +31,12 @@ class Pair:
     """A PagedDecoder and the oracle driven with the same inputs."""
 
     def __init__(self, *, layers, hq, hkv, d, tpb, dtype, pool_blocks, host_blocks, staging_blocks=1024,
-                 blocks_per_workgroup=16):
+                 blocks_per_workgroup=16, stream_mode="direct"):
         self.dtype = dtype
         self.dec = PagedDecoder(num_layers=layers, num_query_heads=hq, num_kv_heads=hkv, head_dim=d,
                                 tokens_per_block=tpb, dtype=dtype, device="cuda", pool_blocks=pool_blocks,
                                 host_blocks=host_blocks, staging_blocks=staging_blocks,
-                                blocks_per_workgroup=blocks_per_workgroup)
+                                blocks_per_workgroup=blocks_per_workgroup, stream_mode=stream_mode)
         self.ora = PagedDecodeOracle(num_layers=layers, num_query_heads=hq, num_kv_heads=hkv, head_dim=d,
                                      tokens_per_block=tpb)
         self.layers, self.hq, self.hkv, self.d, self.tpb = layers, hq, hkv, d, tpb
@@ -91,9 +91,11 @@ class Pair:
         return res, ref, err
 
 
-def test_config1_single_layer_4096_ctx_8_resident():
+@pytest.mark.parametrize("mode", ["direct", "staged"])
+def test_config1_single_layer_4096_ctx_8_resident(mode):
     g = torch.Generator().manual_seed(1)
-    p = Pair(layers=1, hq=14, hkv=2, d=64, tpb=32, dtype=torch.float16, pool_blocks=32, host_blocks=256)
+    p = Pair(layers=1, hq=14, hkv=2, d=64, tpb=32, dtype=torch.float16, pool_blocks=32, host_blocks=256,
+             stream_mode=mode)
     sid = p.add(ctx=4096, capacity=4096 + 128, gen=g, vram_budget=8 * MIB16, ram_budget=1024 * MIB16,
                 recent_window=7, policy="recent_only")
     assert p.dec.pool.block_ids(sid, True) == list(range(120, 128))
@@ -106,11 +108,13 @@ def test_config1_single_layer_4096_ctx_8_resident():
     assert p.dec.pool.block_ids(sid, True) == list(range(121, 129))
 
 
-def test_config2_batch8_ragged_contexts_128_steps():
+@pytest.mark.parametrize("mode", ["direct", "staged"])
+def test_config2_batch8_ragged_contexts_128_steps(mode):
     g = torch.Generator().manual_seed(2)
     ctx = torch.randint(1024, 32769, (8,), generator=g).tolist()
     host_blocks = sum(c // 32 + 8 for c in ctx)
-    p = Pair(layers=1, hq=14, hkv=2, d=64, tpb=32, dtype=torch.float16, pool_blocks=8 * 70, host_blocks=host_blocks)
+    p = Pair(layers=1, hq=14, hkv=2, d=64, tpb=32, dtype=torch.float16, pool_blocks=8 * 70, host_blocks=host_blocks,
+             stream_mode=mode)
     for c in ctx:
         p.add(ctx=c, capacity=c + 160, gen=g, vram_budget=64 * MIB16, ram_budget=4096 * MIB16, recent_window=63,
               policy="recent_only")
@@ -126,13 +130,13 @@ def test_config2_batch8_ragged_contexts_128_steps():
         assert p.dec.pool.block_ids(sid, True) == list(range(n_full - 64, n_full))
 
 
-@pytest.mark.parametrize("staging_blocks", [96, 4096])
-def test_config4_mistral_layer_window_bf16(staging_blocks):
+@pytest.mark.parametrize("mode,staging_blocks", [("direct", 96), ("staged", 96), ("staged", 4096)])
+def test_config4_mistral_layer_window_bf16(mode, staging_blocks):
     """131072 tokens, window 4096: valid iff position > current - 4096 (paged_model.py:981)."""
     g = torch.Generator().manual_seed(4)
     ctx, window = 131072, 4096
     p = Pair(layers=1, hq=32, hkv=8, d=128, tpb=32, dtype=torch.bfloat16, pool_blocks=4 * 40,
-             host_blocks=4 * (ctx // 32 + 8), staging_blocks=staging_blocks)
+             host_blocks=4 * (ctx // 32 + 8), staging_blocks=staging_blocks, stream_mode=mode)
     for _ in range(4):
         p.add(ctx=ctx, capacity=ctx + 64, gen=g, zero_before=ctx - 2 * window, vram_budget=32 * MIB16,
               ram_budget=8192 * MIB16, recent_window=31, policy="recent_only")
@@ -147,11 +151,13 @@ def test_config4_mistral_layer_window_bf16(staging_blocks):
     assert p.ora.host_ids(p.sids[0], 0)[0] == (ctx + 3 - window) // 32
 
 
-def test_scoring_policy_mass_drives_placement():
+@pytest.mark.parametrize("mode", ["direct", "staged"])
+def test_scoring_policy_mass_drives_placement(mode):
     """sinks_heavy_hitter over two layers: the per-block mass handed to the pager matches the
     oracle's within float tolerance and, where score gaps are clear, placement is identical."""
     g = torch.Generator().manual_seed(5)
-    p = Pair(layers=2, hq=32, hkv=4, d=64, tpb=32, dtype=torch.float16, pool_blocks=64, host_blocks=256)
+    p = Pair(layers=2, hq=32, hkv=4, d=64, tpb=32, dtype=torch.float16, pool_blocks=64, host_blocks=256,
+             stream_mode=mode)
     sid = p.add(ctx=1500, capacity=1500 + 128, gen=g, scale=1.0, vram_budget=12 * MIB16, ram_budget=512 * MIB16,
                 recent_window=4, rebalance_interval=4, policy="sinks_heavy_hitter")
     for _ in range(40):
@@ -183,3 +189,14 @@ def test_short_prompt_below_one_block():
     for _ in range(60):
         p.step(g)
     assert p.dec.num_tokens(sid) == 65 and p.dec.num_blocks(sid) == 2
+
+
+def test_first_token_of_an_empty_session():
+    """No stored tokens: the step attends to the current token alone (output = v_new)."""
+    g = torch.Generator().manual_seed(8)
+    p = Pair(layers=1, hq=14, hkv=2, d=64, tpb=32, dtype=torch.float16, pool_blocks=16, host_blocks=64)
+    sid = p.add(ctx=0, capacity=200, gen=g, vram_budget=2 * MIB16, ram_budget=64 * MIB16, recent_window=1,
+                policy="recent_only")
+    for _ in range(40):
+        p.step(g)
+    assert p.dec.num_tokens(sid) == 40 and p.dec.num_blocks(sid) == 1
