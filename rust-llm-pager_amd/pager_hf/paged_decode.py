@@ -10,11 +10,11 @@ Per decode step::
     step_stats = dec.end_step()                  # new blocks -> pager.on_step -> apply_tiers
 
 ``q`` is [S, Hq, D] (post-RoPE), ``k_new``/``v_new`` [S, Hkv, D], where the S sequences are
-the rows of the stepped sessions in order. The append writes the new token into the
-session's open block in HBM before attention, so the current token attends to itself
-exactly as in the reference (tail + current token, paged_model.py:955, :984-987). Blocks
-outside the valid range [lo, position] are neither read nor streamed (the reference reads
-and masks them, paged_model.py:961).
+the rows of the stepped sessions in order. The current token attends to itself exactly as in
+the reference (tail + current token, paged_model.py:955, :984-987): the merge kernel folds it
+in from k_new/v_new, and the attention kernel writes it into the session's open block for
+later steps. Blocks outside the valid range [lo, position] are neither read nor streamed
+(the reference reads and masks them, paged_model.py:961).
 
 Placement glue follows paged_model.py:768-812: with N full blocks after the step,
 ``on_step(N - 1, 0, scores)`` then ``force_rebalance(N - 1)`` if a block completed, then
@@ -191,7 +191,10 @@ class PagedDecoder:
         return sum(self.sessions[sid].rows for sid in (self._step or []))
 
     def decode_layer(self, layer: int, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor,
-                     out: torch.Tensor | None = None) -> torch.Tensor:
+                     out: torch.Tensor | None = None, *, scale: float | None = None,
+                     softcap: float | None = None) -> torch.Tensor:
+        """Append k_new/v_new, attend q over every valid stored token plus the new one, and
+        accumulate this layer's block mass. scale/softcap override the decoder's defaults."""
         if self._step is None:
             raise RuntimeError("decode_layer outside begin_step/end_step")
         S = self.num_sequences()
@@ -205,7 +208,8 @@ class PagedDecoder:
         q, k_new, v_new = q.contiguous(), k_new.contiguous(), v_new.contiguous()
         if out is None:
             out = torch.empty(exp_q, dtype=self.dtype, device=self.device)
-        self.pool.decode_layer(layer, q, k_new, v_new, out, self._mass, self.scale, self.softcap)
+        self.pool.decode_layer(layer, q, k_new, v_new, out, self._mass, self.scale if scale is None else scale,
+                               self.softcap if softcap is None else softcap)
         return out
 
     def step_host_blocks(self, seq: int) -> list[int]:

@@ -1,0 +1,413 @@
+"""PagedModel: a HuggingFace causal LM whose KV cache is paged between HBM and host RAM.
+
+Same public surface as the reference's ``pager_hf.PagedModel`` (paged_model.py:179-409):
+the constructor arguments and defaults, ``generate(input_ids, attention_mask,
+max_new_tokens, *, do_sample, temperature, top_k, top_p, generator)``, ``reset()``, the
+session that persists across generate() calls, ``last_run_stats`` (GenerationStats) and the
+one-call-at-a-time lock. What runs underneath is the native path:
+
+* prefill: the model's own attention over the prompt (minus its last token) in chunks of
+  ``prefill_chunk_tokens`` (paged_model.py:1121-1161); the resulting K/V is imported into the
+  native store with every full block resident in HBM, as the reference's initial store is
+  (paged_model.py:1183-1192);
+* decode: one token per step. The model runs with the attention implementation registered
+  here, which hands each layer's post-RoPE q / k_new / v_new to PagedDecoder.decode_layer:
+  append, attention over HBM and host blocks, block mass -- in place of the reference's
+  patched layer forward (paged_model.py:926-1086). After the step the native placement glue
+  runs on_step / force_rebalance / apply_tiers (paged_model.py:768-812).
+
+Differences: ``use_streaming_attention=False`` (the reference's reload-everything mode) and
+``generate_beam_search`` raise NotImplementedError; supported model types are the ones
+whose attention is the plain q/k/v + RoPE + o_proj layout in transformers 5.x (llama,
+mistral, qwen2, qwen3). Mistral's sliding window is applied per step through the
+sequences' first valid position.
+"""
+from __future__ import annotations
+
+import logging
+import threading
+from contextlib import contextmanager
+from dataclasses import dataclass
+
+import torch
+from transformers import AttentionInterface
+from transformers.cache_utils import DynamicCache
+
+from .paged_decode import PagedDecoder
+
+logger = logging.getLogger(__name__)
+
+_ATTN_IMPL = "pgr_paged_decode"
+_POLICIES_WITHOUT_ATTENTION_SIGNAL = frozenset({"recent_only", "sinks_recent"})  # paged_model.py:40
+_SUPPORTED_MODEL_TYPES = frozenset({"llama", "mistral", "qwen2", "qwen3"})
+
+
+def _paged_attention(module, query, key, value, attention_mask, scaling=None, dropout=0.0, **kwargs):
+    """Attention interface of a decode step: query [B, Hq, 1, D], key/value [B, Hkv, 1, D]
+    (post-RoPE, the current token only). Returns ([B, 1, Hq, D], None)."""
+    ctx = getattr(module, "_pgr_ctx", None)
+    if ctx is None:
+        raise RuntimeError(f"attention implementation {_ATTN_IMPL!r} is only usable inside PagedModel.generate()")
+    if query.shape[2] != 1:
+        raise RuntimeError("paged decode attention takes exactly one new token per sequence")
+    q = query[:, :, 0, :]
+    k = key[:, :, 0, :]
+    v = value[:, :, 0, :]
+    out = ctx.decoder.decode_layer(module.layer_idx, q, k, v, scale=scaling, softcap=ctx.softcap)
+    return out.unsqueeze(1), None
+
+
+AttentionInterface.register(_ATTN_IMPL, _paged_attention)
+
+
+class _LayerContext:
+    def __init__(self, decoder: PagedDecoder, softcap: float | None):
+        self.decoder = decoder
+        self.softcap = softcap
+
+
+@dataclass
+class GenerationStats:
+    """paged_model.py:179-189."""
+
+    total_new_blocks: int = 0
+    final_num_blocks: int = 0
+    total_gpu_to_cpu_mb: float = 0.0
+    total_cpu_to_gpu_mb: float = 0.0
+    total_gpu_to_cpu_copies: int = 0
+    total_cpu_to_gpu_copies: int = 0
+    mean_attention_in_gpu: float = 0.0
+    min_attention_in_gpu: float = 0.0
+    max_attention_in_gpu: float = 0.0
+
+
+class PagedModel:
+    def __init__(
+        self,
+        model,
+        *,
+        vram_budget: int,
+        ram_budget: int,
+        recent_window: int = 64,
+        rebalance_interval: int = 4,
+        promote_margin: float = 0.05,
+        ram_promote_margin: float = 0.20,
+        policy: str = "sinks_heavy_hitter",
+        tokens_per_block: int = 16,
+        prefill_chunk_tokens: int = 512,
+        use_streaming_attention: bool = True,
+        streaming_group_size_blocks: int = 64,
+        max_context_tokens: int | None = None,
+        stream_mode: str = "direct",
+    ):
+        """Arguments and defaults of paged_model.py:200-215. Added: ``max_context_tokens``
+        (tokens per row the native store is sized for; default: the first session's prompt
+        plus max_new_tokens) and ``stream_mode`` ("direct" or "staged"). The group size has
+        no effect: the native kernel covers every block in one launch."""
+        if not use_streaming_attention:
+            raise NotImplementedError(
+                "use_streaming_attention=False (reload every block into one HBM cache per step) is not built: "
+                "the native decode path reads HBM and host blocks in place."
+            )
+        if tokens_per_block <= 0 or tokens_per_block % 16:
+            raise ValueError("tokens_per_block must be a positive multiple of 16 for the native kernels")
+        self.model = model
+        self.tokens_per_block = tokens_per_block
+        self.prefill_chunk_tokens = prefill_chunk_tokens
+        self.use_streaming_attention = use_streaming_attention
+        self.streaming_group_size_blocks = streaming_group_size_blocks
+        self.max_context_tokens = max_context_tokens
+        self.stream_mode = stream_mode
+        self._needs_attention = policy not in _POLICIES_WITHOUT_ATTENTION_SIGNAL
+        self._ram_budget = ram_budget
+        self._pager_kwargs = dict(
+            vram_budget=vram_budget,
+            ram_budget=ram_budget,
+            recent_window=recent_window,
+            rebalance_interval=rebalance_interval,
+            promote_margin=promote_margin,
+            ram_promote_margin=ram_promote_margin,
+            policy=policy,
+        )
+        self.last_run_stats: GenerationStats | None = None
+        self._decoder: PagedDecoder | None = None
+        self._sid: int | None = None
+        self._rows = 0
+        self._capacity = 0
+        self._num_layers: int | None = None
+        self._primed_tokens = 0
+        self._primed_prefix: torch.Tensor | None = None
+        self._lock = threading.Lock()
+
+    # -- lifetime ------------------------------------------------------------------------
+    def _acquire_or_raise(self) -> None:
+        """paged_model.py:270-282."""
+        if not self._lock.acquire(blocking=False):
+            raise RuntimeError(
+                "Another generate() or reset() call is already running on this PagedModel instance. It holds one "
+                "mutable session, so concurrent calls from another thread would corrupt its state rather than run "
+                "as independent requests. Use a separate PagedModel per concurrent session, or synchronize calls "
+                "to this one yourself."
+            )
+
+    def reset(self) -> None:
+        """Drop the current session; the next generate() call starts fresh (paged_model.py:284-299)."""
+        self._acquire_or_raise()
+        try:
+            self._close()
+        finally:
+            self._lock.release()
+
+    def _close(self) -> None:
+        if self._decoder is not None:
+            self._decoder.pool.close()
+        self._decoder = None
+        self._sid = None
+        self._num_layers = None
+        self._primed_tokens = 0
+        self._primed_prefix = None
+
+    @property
+    def decoder(self) -> PagedDecoder | None:
+        return self._decoder
+
+    # -- generation ------------------------------------------------------------------------
+    @torch.inference_mode()
+    def generate(
+        self,
+        input_ids: torch.Tensor,
+        attention_mask: torch.Tensor,
+        max_new_tokens: int,
+        *,
+        do_sample: bool = False,
+        temperature: float = 1.0,
+        top_k: int | None = None,
+        top_p: float | None = None,
+        generator: torch.Generator | None = None,
+    ) -> list[int] | list[list[int]]:
+        """paged_model.py:300-407: generate up to max_new_tokens, continuing any previous session."""
+        self._acquire_or_raise()
+        try:
+            batch_size = input_ids.shape[0]
+            self._validate_left_padded(attention_mask)
+            if do_sample:
+                if temperature <= 0:
+                    raise ValueError(f"temperature must be > 0 for sampling, got {temperature}.")
+                if top_k is not None and top_k < 1:
+                    raise ValueError(f"top_k must be >= 1, got {top_k}.")
+                if top_p is not None and not (0.0 < top_p <= 1.0):
+                    raise ValueError(f"top_p must be in (0, 1], got {top_p}.")
+            if self._decoder is None:
+                self._start_session(input_ids, attention_mask, max_new_tokens)
+            else:
+                self._extend_session(input_ids, attention_mask, max_new_tokens)
+
+            next_input_id = input_ids[:, -1:]
+            current_attention_mask = attention_mask
+            generated_per_row: list[list[int]] = [[] for _ in range(batch_size)]
+            stats = GenerationStats()
+            in_gpu: list[float] = []
+            for _ in range(max_new_tokens):
+                logits, step = self._forward_step(next_input_id, current_attention_mask)
+                if do_sample:
+                    next_token_id = self._sample_next_token(logits, temperature=temperature, top_k=top_k, top_p=top_p,
+                                                            generator=generator)
+                else:
+                    next_token_id = torch.argmax(logits, dim=-1, keepdim=True)
+                for row_tokens, token_id in zip(generated_per_row, next_token_id[:, 0].tolist()):
+                    row_tokens.append(token_id)
+                stats.total_new_blocks += step["new_blocks"]
+                stats.total_gpu_to_cpu_mb += step["gpu_to_cpu_mb"]
+                stats.total_cpu_to_gpu_mb += step["cpu_to_gpu_mb"]
+                stats.total_gpu_to_cpu_copies += step["gpu_to_cpu_copies"]
+                stats.total_cpu_to_gpu_copies += step["cpu_to_gpu_copies"]
+                in_gpu.append(step["attention_in_gpu"])
+                next_input_id = next_token_id
+                current_attention_mask = torch.cat(
+                    [current_attention_mask, current_attention_mask.new_ones((batch_size, 1))], dim=1
+                )
+            full_sequence = torch.cat(
+                [input_ids, torch.tensor(generated_per_row, dtype=input_ids.dtype, device=input_ids.device)], dim=1
+            )
+            self._primed_prefix = full_sequence[:, :-1].detach().clone()
+            self._primed_tokens = full_sequence.shape[-1] - 1
+            stats.final_num_blocks = self._decoder.num_blocks(self._sid)
+            if in_gpu:
+                stats.mean_attention_in_gpu = sum(in_gpu) / len(in_gpu)
+                stats.min_attention_in_gpu = min(in_gpu)
+                stats.max_attention_in_gpu = max(in_gpu)
+            self.last_run_stats = stats
+            return generated_per_row[0] if batch_size == 1 else generated_per_row
+        finally:
+            self._lock.release()
+
+    def generate_beam_search(self, *args, **kwargs):
+        raise NotImplementedError("beam search (row reordering of the paged store) is not built")
+
+    @staticmethod
+    def _sample_next_token(logits, *, temperature, top_k, top_p, generator):
+        """paged_model.py:643-670."""
+        logits = logits / temperature
+        if top_k is not None:
+            kth_value = torch.topk(logits, min(top_k, logits.shape[-1]), dim=-1).values[:, -1, None]
+            logits = logits.masked_fill(logits < kth_value, float("-inf"))
+        if top_p is not None:
+            sorted_logits, sorted_indices = torch.sort(logits, descending=True, dim=-1)
+            sorted_probs = torch.softmax(sorted_logits, dim=-1)
+            cumulative_probs = torch.cumsum(sorted_probs, dim=-1)
+            sorted_logits = sorted_logits.masked_fill(cumulative_probs - sorted_probs > top_p, float("-inf"))
+            logits = torch.full_like(logits, float("-inf")).scatter(-1, sorted_indices, sorted_logits)
+        probs = torch.softmax(logits, dim=-1)
+        return torch.multinomial(probs, num_samples=1, generator=generator)
+
+    # -- session ---------------------------------------------------------------------------
+    def _model_geometry(self):
+        cfg = self.model.config
+        model_type = getattr(cfg, "model_type", None)
+        if model_type not in _SUPPORTED_MODEL_TYPES:
+            raise NotImplementedError(
+                f"PagedModel doesn't recognize model_type={model_type!r}; supported: {sorted(_SUPPORTED_MODEL_TYPES)}"
+            )
+        num_heads = cfg.num_attention_heads
+        num_kv = getattr(cfg, "num_key_value_heads", None) or num_heads
+        head_dim = getattr(cfg, "head_dim", None) or cfg.hidden_size // num_heads
+        window = getattr(cfg, "sliding_window", None) if model_type == "mistral" else None
+        return cfg.num_hidden_layers, num_heads, num_kv, head_dim, window
+
+    def _start_session(self, input_ids: torch.Tensor, attention_mask: torch.Tensor, max_new_tokens: int) -> None:
+        """paged_model.py:672-689: prefill all but the last token, store every full block in HBM."""
+        layers, hq, hkv, d, _ = self._model_geometry()
+        rows, total = input_ids.shape
+        T = self.tokens_per_block
+        n_prefix = total - 1
+        capacity = max(self.max_context_tokens or 0, total + max_new_tokens + T)
+        blocks = -(-capacity // T) + 2
+        dtype = next(self.model.parameters()).dtype
+        device = input_ids.device
+        dec = PagedDecoder(
+            num_layers=layers, num_query_heads=hq, num_kv_heads=hkv, head_dim=d, tokens_per_block=T, dtype=dtype,
+            device=device, pool_blocks=rows * blocks, host_blocks=rows * blocks, staging_blocks=64,
+            staging_buffers=2, ram_budget_bytes=self._ram_budget, stream_mode=self.stream_mode,
+        )
+        pads = (attention_mask.shape[1] - attention_mask.long().sum(dim=1)).tolist()
+        sid = dec.add_session(capacity_tokens=capacity, rows=rows, lo=pads, **self._pager_kwargs)
+        if n_prefix > 0:
+            past = self._chunked_prefill(input_ids[:, :-1], attention_mask[:, :-1])
+            keys = [past.layers[i].keys for i in range(layers)]
+            values = [past.layers[i].values for i in range(layers)]
+            dec.prefill(sid, keys, values, n_prefix, place=False)
+            del past, keys, values
+        self._decoder, self._sid, self._rows, self._capacity, self._num_layers = dec, sid, rows, capacity, layers
+        logger.info("Started PagedModel session: batch_size=%d prompt_tokens=%d layers=%d blocks=%d policy=%r",
+                    rows, total, layers, dec.num_blocks(sid), self._pager_kwargs["policy"])
+
+    def _extend_session(self, input_ids: torch.Tensor, attention_mask: torch.Tensor, max_new_tokens: int) -> None:
+        """paged_model.py:691-713: feed the tokens not yet primed before decoding new ones."""
+        total_len = input_ids.shape[-1]
+        if input_ids.shape[0] != self._rows:
+            raise ValueError("batch size differs from the primed session; call reset() first")
+        if total_len - 1 < self._primed_tokens:
+            raise ValueError(
+                "input_ids is shorter than the already-primed session "
+                f"({total_len - 1} < {self._primed_tokens} tokens). "
+                "Call reset() to start a new session instead of rewinding one."
+            )
+        if not torch.equal(input_ids[:, : self._primed_tokens].cpu(), self._primed_prefix.cpu()):
+            raise ValueError(
+                "input_ids diverges from the already-primed session prefix. generate() expects each call to extend "
+                "the same growing sequence (previous input + previously generated tokens + any new tokens). Call "
+                "reset() to start a different session."
+            )
+        if total_len + max_new_tokens > self._capacity:
+            raise ValueError(
+                f"the session would grow past the {self._capacity} tokens its store was sized for; pass a larger "
+                "max_context_tokens to PagedModel"
+            )
+        pending = input_ids[:, self._primed_tokens : total_len - 1]
+        for i in range(pending.shape[-1]):
+            self._forward_step(pending[:, i : i + 1], attention_mask[:, : self._primed_tokens + i + 1])
+
+    def _chunked_prefill(self, prefix_input_ids: torch.Tensor, prefix_attention_mask: torch.Tensor) -> DynamicCache:
+        """paged_model.py:1121-1161 (absolute cache_position per chunk)."""
+        seq_len = prefix_input_ids.shape[-1]
+        position_ids = self._position_ids_from_mask(prefix_attention_mask)
+        past = DynamicCache()
+        for start in range(0, seq_len, self.prefill_chunk_tokens):
+            end = min(start + self.prefill_chunk_tokens, seq_len)
+            out = self.model(
+                input_ids=prefix_input_ids[:, start:end],
+                attention_mask=prefix_attention_mask[:, :end],
+                position_ids=position_ids[:, start:end],
+                cache_position=torch.arange(start, end, device=prefix_input_ids.device),
+                past_key_values=past,
+                use_cache=True,
+                logits_to_keep=1,
+            )
+            past = out.past_key_values
+        return past
+
+    @contextmanager
+    def _paged_attention(self):
+        cfg = self.model.config
+        previous = cfg._attn_implementation
+        ctx = _LayerContext(self._decoder, None)
+        modules = [layer.self_attn for layer in self.model.model.layers]
+        for m in modules:
+            m._pgr_ctx = ctx
+        cfg._attn_implementation = _ATTN_IMPL
+        try:
+            yield
+        finally:
+            cfg._attn_implementation = previous
+            for m in modules:
+                m._pgr_ctx = None
+
+    def _forward_step(self, input_id_tensor: torch.Tensor, current_attention_mask: torch.Tensor):
+        """One token per row through the model over the paged store, then the placement glue
+        (paged_model.py:715-823). Returns (last-position logits [B, V], step stats)."""
+        dec, sid = self._decoder, self._sid
+        _, _, _, _, window = self._model_geometry()
+        position_ids = self._position_ids_from_mask(current_attention_mask)[:, -1:]
+        if window is not None:
+            # Valid columns c > current_column - window (the causal mask's sliding-window rule).
+            col = current_attention_mask.shape[1] - 1
+            pads = (current_attention_mask.shape[1] - current_attention_mask.long().sum(dim=1)).tolist()
+            dec.set_lo(sid, [max(p, col - window + 1) for p in pads])
+        dec.begin_step([sid])
+        host_blocks = dec.pool.step_stats()["host_blocks"]
+        try:
+            with self._paged_attention():
+                out = self.model(input_ids=input_id_tensor, position_ids=position_ids, use_cache=False,
+                                 logits_to_keep=1)
+        except BaseException:
+            dec.end_step(collect=False)
+            raise
+        st = dec.end_step()[sid]
+        block_bytes_layer = dec.pool.block_bytes(sid) // max(self._num_layers, 1) // max(self._rows, 1)
+        step = {
+            "new_blocks": st["new_blocks"],
+            "gpu_to_cpu_mb": st["gpu_to_cpu_mb"],
+            "gpu_to_cpu_copies": st["gpu_to_cpu_copies"],
+            "cpu_to_gpu_mb": host_blocks * block_bytes_layer * self._num_layers / 1_000_000,
+            "cpu_to_gpu_copies": host_blocks * self._num_layers,
+            "attention_in_gpu": st["attention_in_gpu"],
+        }
+        return out.logits[:, -1, :], step
+
+    @staticmethod
+    def _position_ids_from_mask(attention_mask: torch.Tensor) -> torch.Tensor:
+        """paged_model.py:1163-1167."""
+        position_ids = attention_mask.long().cumsum(-1) - 1
+        return position_ids.masked_fill(attention_mask == 0, 0)
+
+    @staticmethod
+    def _validate_left_padded(attention_mask: torch.Tensor) -> None:
+        """paged_model.py:1169-1181."""
+        mask = attention_mask.bool()
+        if not mask.any(dim=1).all():
+            raise NotImplementedError("attention_mask has a row with no real (non-padding) tokens.")
+        if not torch.all(mask[:, :-1] <= mask[:, 1:]):
+            raise NotImplementedError(
+                "PagedModel only supports left-padding (zero or more leading zeros, then all ones, per row); "
+                "right-padding or interleaved masking is not supported."
+            )
