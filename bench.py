@@ -151,6 +151,93 @@ def committed_traffic(workload_layers):
     return t.get("traffic_bytes_per_launch")
 
 
+def continuous(args):
+    """Continuous-batching decode: Qwen2.5-1.5B architecture (28 layers, hidden 1536, 12 query
+    heads, 2 KV heads, head_dim 128, bf16, random init), 64 concurrent requests, prompts
+    lognormal(median 4096, sigma 1) clipped to [256, 65536], outputs U[64, 512], a new request
+    admitted whenever one finishes; 4 GB of HBM K/V budget (68 logical blocks per session) and
+    the rest in pinned host RAM. Times `rounds` scheduler rounds after the first (which opens
+    the first 64 requests); returns one JSON-able dict."""
+    import numpy as np
+    import torch
+    from transformers import Qwen2Config, Qwen2ForCausalLM
+
+    from pager_hf.serving.scheduler import ContinuousBatchingScheduler
+
+    conc, T = 64, 32
+    cfg = Qwen2Config(hidden_size=1536, intermediate_size=8960, num_hidden_layers=28, num_attention_heads=12,
+                      num_key_value_heads=2, vocab_size=151936, max_position_embeddings=131072, rope_theta=1e6,
+                      tie_word_embeddings=True)
+    torch.manual_seed(0)
+    with torch.device("cuda"):
+        model = Qwen2ForCausalLM(cfg)
+    model = model.to(torch.bfloat16).eval()
+    rng = np.random.default_rng(5)
+    n_req = conc + args.cb_extra_requests
+    lens = np.clip(np.exp(rng.normal(np.log(4096), 1.0, n_req)), 256, 65536).astype(int).tolist()
+    outs = rng.integers(64, 513, n_req).tolist()
+    per_session_blocks = int(4e9 // (conc * (2 * 2 * 128 * 2 * T * 28)))  # 68: real bytes -> logical blocks
+    sched = ContinuousBatchingScheduler(
+        model, SimpleTokenizer(), max_concurrent_sessions=conc,
+        total_vram_budget=conc * per_session_blocks * MIB16, total_ram_budget=1 << 42, policy=args.cb_policy,
+        tokens_per_block=T, max_context_tokens=65536 + 1024, host_token_capacity=args.cb_host_tokens,
+        max_queue_depth=n_req, device="cuda",
+    )
+    g = torch.Generator().manual_seed(6)
+    reqs = [sched.submit(torch.randint(0, cfg.vocab_size, (1, n), generator=g), torch.ones(1, n, dtype=torch.long),
+                         max_new_tokens=m) for n, m in zip(lens, outs)]
+    eng = sched.engine()
+    host_bytes = [0]
+    orig_step = eng.step
+
+    def step(sessions, tokens):
+        out = orig_step(sessions, tokens)
+        if len(sessions) > 1:
+            host_bytes[0] += eng.host_bytes_per_step()
+        return out
+
+    eng.step = step
+    t_open = time.perf_counter()
+    sched._admit_new_requests()
+    sched._run_once()  # opens and first-steps the first 64 requests
+    torch.cuda.synchronize()
+    t_open = time.perf_counter() - t_open
+    tokens0 = sum(len(r.generated_tokens) for r in reqs)
+    host_bytes[0] = 0
+    live = sum(r.input_ids.shape[1] for r in sched._active)
+    t0 = time.perf_counter()
+    for _ in range(args.cb_rounds):
+        sched._admit_new_requests()
+        sched._run_once()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    tokens = sum(len(r.generated_tokens) for r in reqs) - tokens0
+    sched.stop(timeout=0)
+    link = host_bytes[0] / dt / 1e9
+    return {
+        "metric": "continuous-batching decode tokens/s (64 concurrent, Qwen2.5-1.5B arch, 4 GB HBM K/V budget)",
+        "value": round(tokens / dt, 2),
+        "unit": "tokens/s",
+        "rounds": args.cb_rounds,
+        "ms_per_round": round(dt / args.cb_rounds * 1e3, 2),
+        "tokens": tokens,
+        "live_tokens_at_start": live,
+        "first_round_s": round(t_open, 2),
+        "host_link": {"achieved": round(link, 3), "peak": LINK_PEAK_GBS, "unit": "GB/s",
+                      "frac": round(link / LINK_PEAK_GBS, 4)},
+        "dtype": "bf16",
+        "data": "synthetic: random-init weights, random token ids",
+        "config": {"workload": "continuous batching, Qwen2.5-1.5B architecture, 64 concurrent, prompts lognormal("
+                               "median 4096, sigma 1) clipped [256, 65536], outputs U[64, 512], admit on finish",
+                   "policy": args.cb_policy, "per_session_hbm_blocks": per_session_blocks, "tokens_per_block": T,
+                   "requests": n_req},
+    }
+
+
+class SimpleTokenizer:
+    eos_token_id = None
+
+
 def cpu_baseline(ctx, budget_s=15.0):
     """Times the oracle's fp32 dense attention on the host over a bounded sample of the same
     workload (whole steps of the batch, upcast included); returns KV GB/s and tokens/s."""
@@ -202,6 +289,12 @@ def main() -> int:
                     help="host blocks read in place over the host link, or copied into a staging ring")
     ap.add_argument("--resident-layers", type=int, default=24,
                     help="layers of the all-resident HBM measurement (0 skips it)")
+    ap.add_argument("--workload", choices=["batch8", "continuous"], default="batch8",
+                    help="batch8: the headline line; continuous: the 64-request continuous-batching run")
+    ap.add_argument("--cb-rounds", type=int, default=24)
+    ap.add_argument("--cb-extra-requests", type=int, default=64)
+    ap.add_argument("--cb-policy", default="recent_only")
+    ap.add_argument("--cb-host-tokens", type=int, default=800_000)
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
                     help="after timing, run one device copy of this size (counter calibration)")
     args = ap.parse_args()
@@ -214,6 +307,12 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a HIP device", file=sys.stderr)
         return 2
+    if args.workload == "continuous":
+        line = continuous(args)
+        line.update({"n_gpus": 1, "steps": args.cb_rounds, "warmup": 1, "higher_is_better": True, "scaling": "weak",
+                     "vs_baseline": None})
+        print(json.dumps(line), flush=True)
+        return 0
     c = CFG
     total = args.warmup + args.steps
     dec, sids, ctx, q, kn, vn, out = build(total, args.staging_blocks, args.staging_buffers, args.blocks_per_wg,
