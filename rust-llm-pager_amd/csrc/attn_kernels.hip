@@ -436,13 +436,15 @@ __global__ void finalize_f32_kernel(const float* acc, const float* l, float* out
 
 // ---------------------------------------------------------------------------------------
 // Paged kernel: the fused decode path. Blocks are read in place from the layer's HBM
-// pool or from a staging buffer filled by host-to-device copies; record layout per
-// (block, sequence): K [Hkv][T][D] then V [Hkv][T][D]. Grid (n_work, Hkv).
+// pool, from the mapped pinned host mirror, or from a staging buffer filled by
+// host-to-device copies; record layout per (block, sequence): K [Hkv][T][D] then
+// V [Hkv][T][D]. Grid (n_work, Hkv).
 //
 // Each wave streams the blocks w, w+4, ... of its work item through a ring of NB register
 // tiles (NB-1 tiles of loads in flight while one is folded). Everything that selects a
 // tile (entry, slot, block id, tile index) is wave-uniform and lives in SGPRs; a lane's
-// part of a tile is a fixed byte offset, so every load is one `global_load saddr + voffset`.
+// part of a tile is a fixed byte offset, so every load is one `buffer_load` with the
+// tile's offsets in SGPRs.
 //
 // Scores are kept in log2 units (x = s * scale * log2 e, p = 2^(x - m)). The running max m
 // is refreshed lazily: a tile rescales (m, l, acc) only when one of its scores exceeds m
@@ -473,28 +475,29 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLazyRescale = 8.0f;
 constexpr float kMInit = -1.0e30f;  // running max before any valid score (finite: 2^(-inf - kMInit) = 0)
 
-template <class T>
-__device__ __forceinline__ T load_at(const uint16_t* base, uint32_t byte_off) {
-  return *reinterpret_cast<const T*>(reinterpret_cast<const char*>(base) + byte_off);
-}
 
-// K row n (bytes k_lane from the tile base) and V rows 4g..4g+3 (v_lane, then +D elements).
+// One 16-token tile through a buffer resource: K row n (bytes k_lane from the K tile) and V
+// rows 4g..4g+3 (v_lane, then +D elements). `r` covers one KV head of one record, `sk` / `sv` are
+// the tile's K and V byte offsets (wave-uniform, in SGPRs). A resource with no records makes
+// every load of the tile return zeros without a memory access.
+constexpr int kBufferFlags = 0x00020000;  // dword 3 of a raw buffer resource on gfx9
+
 template <int D>
-__device__ __forceinline__ void load_tile(Tile<D>& t, const uint16_t* kb, const uint16_t* vb, uint32_t k_lane,
-                                          uint32_t v_lane) {
+__device__ __forceinline__ void load_tile_rs(Tile<D>& t, __amdgpu_buffer_rsrc_t r, uint32_t sk, uint32_t sv,
+                                             uint32_t k_lane, uint32_t v_lane) {
 #pragma unroll
-  for (int i = 0; i < Tile<D>::KV4; ++i) t.k[i] = load_at<u32x4>(kb, k_lane + 16u * i);
+  for (int i = 0; i < Tile<D>::KV4; ++i) t.k[i] = __builtin_amdgcn_raw_buffer_load_b128(r, k_lane + 16u * i, sk, 0);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const uint32_t off = v_lane + (uint32_t)(i * D * 2);
     if constexpr (D == 32) {
-      t.v[i][0] = load_at<uint32_t>(vb, off);
+      t.v[i][0] = __builtin_amdgcn_raw_buffer_load_b32(r, off, sv, 0);
     } else if constexpr (D == 64) {
-      const u32x2 x = load_at<u32x2>(vb, off);
+      const u32x2 x = __builtin_amdgcn_raw_buffer_load_b64(r, off, sv, 0);
       t.v[i][0] = x.x;
       t.v[i][1] = x.y;
     } else {
-      const u32x4 x = load_at<u32x4>(vb, off);
+      const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(r, off, sv, 0);
       t.v[i][0] = x.x;
       t.v[i][1] = x.y;
       t.v[i][2] = x.z;
@@ -511,7 +514,7 @@ struct TileMeta {
 
 template <int D>
 struct PagedRing {
-  static constexpr int NB = D <= 64 ? 2 : 3;  // register tiles per wave
+  static constexpr int NB = 3;  // register tiles per wave
 };
 
 template <class Ty, int D, bool kMass>
@@ -544,8 +547,7 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(PagedArgs a) {
   const BlockEntry en0 = wi->entries[wave], en1 = wi->entries[wave + kWaves];
   const BlockEntry en2 = wi->entries[wave + 2 * kWaves], en3 = wi->entries[wave + 3 * kWaves];
 
-  u32x4 q[D / 32];
-  load_q<D>(q, a.q + ((size_t)seq * a.hq + qh) * D, real, g);
+  u32x4 q[D / 32];  // loaded behind the first tile (below)
 
   // Score transform: x = mult * s' with s' = s (no softcap) or cap * tanh(s * scale / cap).
   const bool capped = a.softcap > 0.f;
@@ -560,25 +562,25 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(PagedArgs a) {
   const int my_blocks = count > wave ? (count - wave + kWaves - 1) / kWaves : 0;
   const int tiles = my_blocks * tpb;
 
-  // Next tile to fetch: flat index nf, entry fe, tile ftb within the block. A fetch past the
-  // wave's last tile reloads the last tile (an L2 hit) so that every fetch in the loop is
-  // unconditional and the load counter stays in order.
+  // Next tile to fetch: flat index nf, entry fe, tile ftb within the block. Every fetch in
+  // the loop is unconditional, so the load counter stays in order; a fetch past the wave's
+  // last tile goes through an empty buffer resource and returns at once with zeros.
   int nf = 0, fe = 0, ftb = 0;
   auto fetch = [&](Tile<D>& t, TileMeta& mt) {
     const int slot = fe == 0 ? en0.slot : fe == 1 ? en1.slot : fe == 2 ? en2.slot : en3.slot;
     const int bid = fe == 0 ? en0.block_id : fe == 1 ? en1.block_id : fe == 2 ? en2.block_id : en3.block_id;
     const uint16_t* rb = slot >= 0 ? a.pool + (size_t)slot * rec : a.stage + (size_t)(-slot - 1) * rec;
-    const uint16_t* kb = rb + head_off + (size_t)ftb * 16 * D;
-    load_tile<D>(t, kb, kb + v_off, k_lane, v_lane);
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(rb + head_off), (short)0, nf < tiles ? 0x7fffffff : 0, kBufferFlags);
+    const uint32_t sk = (uint32_t)(ftb * 16 * D * 2);
+    load_tile_rs<D>(t, r, sk, sk + (uint32_t)(v_off * 2), k_lane, v_lane);
     mt.t0 = bid * T + ftb * 16;
     mt.block_id = bid;
     mt.last = (ftb == tpb - 1) ? fe : -1;
-    if (nf + 1 < tiles) {
-      ++nf;
-      if (++ftb == tpb) {
-        ftb = 0;
-        ++fe;
-      }
+    ++nf;
+    if (++ftb == tpb) {
+      ftb = 0;
+      ++fe;
     }
   };
 
@@ -631,10 +633,13 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(PagedArgs a) {
   if (tiles > 0) {
     Tile<D> buf[NB];
     TileMeta meta[NB];
+    // Tile 0, then q, then the rest of the prologue: q is needed by the first fold, and
+    // waiting for it here (which also waits for tile 0, as loads return in order) keeps
+    // the loop's wait counts independent of it while tiles 1 .. NB-2 stay in flight.
+    fetch(buf[0], meta[0]);
+    load_q<D>(q, a.q + ((size_t)seq * a.hq + qh) * D, real, g);
 #pragma unroll
-    for (int j = 0; j < NB - 1; ++j) fetch(buf[j], meta[j]);
-    // q is needed by the first fold; waiting for it here (behind the prologue loads) keeps
-    // the loop's wait counts independent of it.
+    for (int j = 1; j < NB - 1; ++j) fetch(buf[j], meta[j]);
 #pragma unroll
     for (int i = 0; i < D / 32; ++i) asm volatile("" ::"v"(q[i]));
     for (int ti = 0; ti < tiles; ti += NB) {
