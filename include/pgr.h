@@ -173,6 +173,12 @@ int pgr_kv_remove_session(void* kv, int32_t sid);
 /* Sliding window / padding: first valid token per row. Replaces the padding and window mask
  * fold of paged_model.py:964-982 (valid iff col > pos - window). */
 int pgr_kv_set_lo(void* kv, int32_t sid, const int32_t* lo_per_row);
+/* Beam-search row reordering: new row r takes old row src_rows[r]'s whole K/V history on
+ * either tier (open block included) and its first valid token; a source row listed twice
+ * is duplicated, one never listed is dropped. n_rows must equal the session's row count.
+ * Replaces KVBlockStore.reorder_batch_rows, kv_block_store.py:229-254 (and the tail
+ * index_select of PagedModel._reorder_batch, paged_model.py:636-644). Synchronous. */
+int pgr_kv_reorder_rows(void* kv, int32_t sid, const int32_t* src_rows, int32_t n_rows, void* stream);
 /* Declares the length of an empty session (prefill); full blocks start host-side. */
 int pgr_kv_set_length(void* kv, int32_t sid, int64_t n_tokens);
 /* Writes tokens [0, n_tokens) of (sid, row, layer) from k, v [Hkv, n_src, D] (device).

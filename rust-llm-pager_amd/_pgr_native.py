@@ -136,6 +136,7 @@ SIGNATURES: dict[str, tuple] = {
     "pgr_kv_add_session": (ctypes.c_int, [c_vp, c_i32, c_i64, P(c_i32)]),
     "pgr_kv_remove_session": (ctypes.c_int, [c_vp, c_i32]),
     "pgr_kv_set_lo": (ctypes.c_int, [c_vp, c_i32, P(c_i32)]),
+    "pgr_kv_reorder_rows": (ctypes.c_int, [c_vp, c_i32, P(c_i32), c_i32, c_vp]),
     "pgr_kv_set_length": (ctypes.c_int, [c_vp, c_i32, c_i64]),
     "pgr_kv_import": (ctypes.c_int, [c_vp, c_i32, c_i32, c_i32, c_vp, c_vp, c_i64, c_i64, c_vp]),
     "pgr_kv_export": (ctypes.c_int, [c_vp, c_i32, c_i32, c_i32, c_vp, c_vp, c_i64, c_vp]),

@@ -294,6 +294,11 @@ int pgr_kv_set_lo(void* kv, int32_t sid, const int32_t* lo_per_row) {
   return kv_rc(kv_of(kv), kv_of(kv)->set_lo(sid, lo_per_row));
 }
 
+int pgr_kv_reorder_rows(void* kv, int32_t sid, const int32_t* src_rows, int32_t n_rows, void* stream) {
+  if (!kv || !src_rows) return set_err(pgr::kErrInvalid, "null pointer");
+  return kv_rc(kv_of(kv), kv_of(kv)->reorder_rows(sid, src_rows, n_rows, as_stream(stream)));
+}
+
 int pgr_kv_set_length(void* kv, int32_t sid, int64_t n_tokens) {
   if (!kv) return set_err(pgr::kErrInvalid, "null store");
   return kv_rc(kv_of(kv), kv_of(kv)->set_length(sid, n_tokens));

@@ -67,6 +67,15 @@ __global__ void records_to_hf_kernel(const uint16_t* src, const int32_t* src_slo
   }
 }
 
+// Copies whole records within one layer's pool: workgroup i copies record pairs[2i] to
+// record pairs[2i + 1] with 16-byte loads and stores.
+__global__ void copy_records_kernel(uint16_t* pool, const int32_t* pairs, int64_t rec_vec) {
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4* src = reinterpret_cast<const u32x4*>(pool) + (size_t)pairs[2 * blockIdx.x] * rec_vec;
+  u32x4* dst = reinterpret_cast<u32x4*>(pool) + (size_t)pairs[2 * blockIdx.x + 1] * rec_vec;
+  for (int64_t i = threadIdx.x; i < rec_vec; i += blockDim.x) dst[i] = src[i];
+}
+
 }  // namespace
 
 PagedKV::PagedKV(const PagedKVConfig& cfg) : cfg_(cfg) {}
@@ -80,6 +89,7 @@ PagedKV::~PagedKV() {
     if (p) hipHostFree(p);
   if (stage_) hipFree(stage_);
   if (ws_) hipFree(ws_);
+  if (pairs_dev_) hipFree(pairs_dev_);
   if (plan_host_) hipHostFree(plan_host_);
   if (mass_host_) hipHostFree(mass_host_);
   for (hipEvent_t e : buf_free_) hipEventDestroy(e);
@@ -261,6 +271,91 @@ int PagedKV::set_lo(int sid, const int32_t* lo_per_row) {
   if (sid < 0 || sid >= (int)sessions_.size() || !sessions_[sid].live) return fail(kErrKey, "unknown session");
   Session& s = sessions_[sid];
   for (int r = 0; r < s.rows; ++r) s.row[r].lo = lo_per_row[r];
+  return kOk;
+}
+
+int PagedKV::ensure_pairs(size_t n) {
+  if (n <= pairs_cap_) return kOk;
+  if (pairs_dev_) PGR_HIP(hipFree(pairs_dev_));
+  pairs_dev_ = nullptr;
+  pairs_cap_ = 0;
+  const size_t want = std::max<size_t>(n, 256);
+  PGR_HIP(hipMalloc(&pairs_dev_, want * 2 * sizeof(int32_t)));
+  pairs_cap_ = want;
+  return kOk;
+}
+
+int PagedKV::reorder_rows(int sid, const int32_t* src, int n, hipStream_t stream) {
+  if (sid < 0 || sid >= (int)sessions_.size() || !sessions_[sid].live) return fail(kErrKey, "unknown session");
+  if (in_step_) return fail(kErrState, "reorder_rows during a decode step");
+  Session& s = sessions_[sid];
+  const int rows = s.rows;
+  if (n != rows) return fail(kErrInvalid, "reorder_rows takes one source row per row of the session");
+  for (int r = 0; r < rows; ++r)
+    if (src[r] < 0 || src[r] >= rows) return fail(kErrInvalid, "source row out of range");
+  // The first new row that takes an old row inherits its records (HBM slots and host
+  // range). Every later taker reuses the records of an old row that no new row takes --
+  // there are exactly as many of those, and every row of a session holds records for the
+  // same blocks -- and gets a copy of its source's data there. So nothing is allocated and
+  // copies only ever read inherited records and write dropped ones.
+  std::vector<int> heir(rows, -1);
+  for (int r = 0; r < rows; ++r)
+    if (heir[src[r]] < 0) heir[src[r]] = r;
+  std::vector<int> dropped;
+  for (int o = 0; o < rows; ++o)
+    if (heir[o] < 0) dropped.push_back(o);
+  std::vector<int> holder(rows);  // old row whose records new row r takes over
+  size_t next_dropped = 0;
+  for (int r = 0; r < rows; ++r) holder[r] = heir[src[r]] == r ? src[r] : dropped[next_dropped++];
+  const int64_t nb = s.capacity_blocks;
+  for (int64_t b = 0; b < nb; ++b)
+    for (int r = 1; r < rows; ++r)
+      if ((s.slot[b * rows + r] < 0) != (s.slot[b * rows] < 0))
+        return fail(kErrState, "rows of a session differ in residency");
+  // Queued kernels and copies may still read or write this session's records.
+  PGR_HIP(hipDeviceSynchronize());
+  const size_t rec = rec_bytes();
+  std::vector<int32_t> slot(s.slot.size(), -1);
+  std::vector<uint8_t> hv(s.host_valid.size(), 0);
+  std::vector<int32_t> pairs;  // HBM copies (from slot, to slot)
+  for (int r = 0; r < rows; ++r) {
+    const int o = src[r], h = holder[r];
+    for (int64_t b = 0; b < nb; ++b) {
+      const int32_t from = s.slot[b * rows + o], to = s.slot[b * rows + h];
+      slot[b * rows + r] = to;
+      if (from >= 0 && h != o) {
+        pairs.push_back(from);
+        pairs.push_back(to);
+      }
+      const uint8_t v = s.host_valid[b * rows + o];
+      hv[b * rows + r] = v;
+      if (v && h != o)
+        for (int l = 0; l < cfg_.num_layers; ++l) {
+          char* base = static_cast<char*>(host_[l]);
+          std::memcpy(base + (size_t)(s.row[h].host_off + b) * rec, base + (size_t)(s.row[o].host_off + b) * rec, rec);
+        }
+    }
+  }
+  if (!pairs.empty()) {
+    int rc = ensure_pairs(pairs.size() / 2);
+    if (rc != kOk) return rc;
+    PGR_HIP(hipMemcpy(pairs_dev_, pairs.data(), pairs.size() * sizeof(int32_t), hipMemcpyHostToDevice));
+    const int64_t rec_vec = (int64_t)(rec / 16);
+    for (int l = 0; l < cfg_.num_layers; ++l) {
+      copy_records_kernel<<<(unsigned)(pairs.size() / 2), 256, 0, stream>>>(static_cast<uint16_t*>(pool_[l]), pairs_dev_,
+                                                                           rec_vec);
+      PGR_HIP(hipGetLastError());
+    }
+    PGR_HIP(hipStreamSynchronize(stream));
+  }
+  std::vector<Row> row(rows);
+  for (int r = 0; r < rows; ++r) {
+    row[r].host_off = s.row[holder[r]].host_off;
+    row[r].lo = s.row[src[r]].lo;
+  }
+  s.row = std::move(row);
+  s.slot = std::move(slot);
+  s.host_valid = std::move(hv);
   return kOk;
 }
 

@@ -78,6 +78,10 @@ class PagedKV {
   int add_session(int rows, int64_t capacity_tokens, const int32_t* lo_per_row);
   int remove_session(int sid);
   int set_lo(int sid, const int32_t* lo_per_row);
+  // Beam-search row reordering (kv_block_store.py:229-254): new row r takes old row
+  // src[r]'s whole history (every block on either tier, the open block included) and its lo;
+  // n must equal the session's row count. Synchronous.
+  int reorder_rows(int sid, const int32_t* src, int n, hipStream_t stream);
 
   // Setup: write the first n_tokens of one (session, row, layer) from k, v [Hkv, n_src, D]
   // (device memory, row stride n_src) and set the session length. Blocks go to the pool when
@@ -180,6 +184,7 @@ class PagedKV {
   int ensure_block_capacity(Session& s, int64_t blocks);
   int move_block(Session& s, int64_t b, bool to_gpu, hipStream_t stream);
   int resolve_timing();
+  int ensure_pairs(size_t n);
 
   PagedKVConfig cfg_;
   std::string err_;
@@ -190,6 +195,8 @@ class PagedKV {
   void* ws_ = nullptr;
   size_t ws_bytes_ = 0;
   int n_cu_ = 0;                  // compute units of the device
+  int32_t* pairs_dev_ = nullptr;  // (from slot, to slot) pairs of a record copy
+  size_t pairs_cap_ = 0;
   void* plan_host_ = nullptr;  // pinned upload buffer for the step plan
   size_t plan_host_bytes_ = 0;
   float* mass_host_ = nullptr;  // pinned readback of the step's block mass

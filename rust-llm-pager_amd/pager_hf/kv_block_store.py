@@ -289,7 +289,18 @@ class KVBlockStore:
         return self._apply([int(t) for t in tiers])
 
     def reorder_batch_rows(self, new_row_indices: list[int]) -> None:
-        raise NotImplementedError("reorder_batch_rows (beam search) is not part of this store")
+        """kv_block_store.py:229-254: new row i takes old row new_row_indices[i]'s data in
+        every block, on whichever tier the block lives, without changing the tier. An index
+        listed twice duplicates that row; one never listed drops it. The native store keeps
+        the batch size, so exactly one index per row is required."""
+        if self._sid is None:
+            return
+        idx = [int(i) for i in new_row_indices]
+        if len(idx) != self._rows:
+            raise ValueError(f"reorder_batch_rows needs one index per row ({self._rows}), got {len(idx)}")
+        if any(i < 0 or i >= self._rows for i in idx):
+            raise IndexError(f"row index out of range for a batch of {self._rows}: {idx}")
+        self._pool.reorder_rows(self._sid, idx)
 
     def get_gpu(self, block_id: int) -> tuple[torch.Tensor, torch.Tensor]:
         if not self.has_gpu(block_id):

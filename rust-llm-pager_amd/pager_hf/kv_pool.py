@@ -128,6 +128,11 @@ class NativeKVPool:
         arr = (ctypes.c_int32 * len(lo))(*[int(x) for x in lo])
         self._call("set_lo", self.lib.pgr_kv_set_lo, sid, arr)
 
+    def reorder_rows(self, sid: int, src_rows) -> None:
+        """New row r of session `sid` takes old row src_rows[r]'s K/V history (beam search)."""
+        arr = (ctypes.c_int32 * len(src_rows))(*[int(x) for x in src_rows])
+        self._call("reorder_rows", self.lib.pgr_kv_reorder_rows, sid, arr, len(src_rows), self._stream())
+
     def set_length(self, sid: int, n_tokens: int) -> None:
         self._call("set_length", self.lib.pgr_kv_set_length, sid, n_tokens)
 

@@ -137,6 +137,15 @@ class PagedDecoder:
         self.pool.set_lo(sid, lo)
         self.sessions[sid].lo = list(lo)
 
+    def reorder_rows(self, sid: int, src_rows: list[int]) -> None:
+        """Beam search (kv_block_store.py:229-254): new row r takes old row src_rows[r]'s
+        K/V history on either tier and its first valid position; one source per row."""
+        sess = self.sessions[sid]
+        if len(src_rows) != sess.rows:
+            raise ValueError(f"reorder_rows needs {sess.rows} source rows, got {len(src_rows)}")
+        self.pool.reorder_rows(sid, src_rows)
+        sess.lo = [sess.lo[i] for i in src_rows]
+
     def prefill(self, sid: int, keys, values, n_tokens: int, *, place: bool = True) -> dict[str, list[int]]:
         """Install a prompt's KV: keys[layer], values[layer] are [rows, Hkv, n_src, D] on this device.
 

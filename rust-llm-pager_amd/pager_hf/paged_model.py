@@ -16,8 +16,10 @@ one-call-at-a-time lock. What runs underneath is the native path:
   patched layer forward (paged_model.py:926-1086). After the step the native placement glue
   runs on_step / force_rebalance / apply_tiers (paged_model.py:768-812).
 
-Differences: ``use_streaming_attention=False`` (the reference's reload-everything mode) and
-``generate_beam_search`` raise NotImplementedError; supported model types are the ones
+``generate_beam_search`` (paged_model.py:409-634) moves beam rows inside the native store.
+
+Differences: ``use_streaming_attention=False`` (the reference's reload-everything mode)
+raises NotImplementedError; supported model types are the ones
 whose attention is the plain q/k/v + RoPE + o_proj layout in transformers 5.x (llama,
 mistral, qwen2, qwen3). Mistral's sliding window is applied per step through the
 sequences' first valid position.
@@ -241,8 +243,129 @@ class PagedModel:
         finally:
             self._lock.release()
 
-    def generate_beam_search(self, *args, **kwargs):
-        raise NotImplementedError("beam search (row reordering of the paged store) is not built")
+    @torch.inference_mode()
+    def generate_beam_search(
+        self,
+        input_ids: torch.Tensor,
+        attention_mask: torch.Tensor,
+        num_beams: int,
+        max_new_tokens: int,
+        *,
+        eos_token_id: int | None = None,
+        length_penalty: float = 1.0,
+        num_return_sequences: int = 1,
+        do_sample: bool = False,
+        temperature: float = 1.0,
+        top_k: int | None = None,
+        top_p: float | None = None,
+        generator: torch.Generator | None = None,
+    ):
+        """Beam search with the semantics of paged_model.py:409-634.
+
+        Each prompt keeps num_beams rows; every step the num_beams best (or, with do_sample,
+        sampled without replacement) continuations over all beams of the same prompt are
+        kept, so one beam's history can go to several rows or to none. The rows are moved
+        inside the native store (reorder_rows: the first child inherits its parent's
+        records, further children get copies), so no K/V leaves the device. Beams start
+        as copies of the prompt with only the first one live (score 0, the rest -inf); a
+        beam that emitted eos_token_id only continues with eos at no score change. The
+        final candidates are ranked by score / len**length_penalty. Every call starts a
+        fresh session and closes it at the end (no continuation by generate()).
+
+        Returns list[int] (one prompt, one sequence), list[list[int]] (one prompt and
+        several sequences, or several prompts and one), or list[list[list[int]]]."""
+        self._acquire_or_raise()
+        try:
+            batch_size = input_ids.shape[0]
+            if num_beams < 1:
+                raise ValueError(f"num_beams must be >= 1, got {num_beams}")
+            if not 1 <= num_return_sequences <= num_beams:
+                raise ValueError(
+                    f"num_return_sequences must be between 1 and num_beams ({num_beams}), got {num_return_sequences}"
+                )
+            if do_sample:
+                if temperature <= 0:
+                    raise ValueError(f"temperature must be > 0 for sampling, got {temperature}.")
+                if top_k is not None and top_k < 1:
+                    raise ValueError(f"top_k must be >= 1, got {top_k}.")
+                if top_p is not None and not (0.0 < top_p <= 1.0):
+                    raise ValueError(f"top_p must be in (0, 1], got {top_p}.")
+            self._validate_left_padded(attention_mask)
+            device = input_ids.device
+            rows = batch_size * num_beams
+            ids = input_ids.repeat_interleave(num_beams, dim=0)
+            mask = attention_mask.repeat_interleave(num_beams, dim=0)
+            self._close()
+            self._start_session(ids, mask, max_new_tokens)
+            try:
+                scores = torch.full((rows,), float("-inf"), dtype=torch.float32, device=device)
+                scores[0::num_beams] = 0.0
+                tokens: list[list[int]] = [[] for _ in range(rows)]
+                finished = torch.zeros(rows, dtype=torch.bool, device=device)
+                group_base = (torch.arange(batch_size, device=device) * num_beams).unsqueeze(1)
+                nxt = ids[:, -1:]
+                for _ in range(max_new_tokens):
+                    logits, _ = self._forward_step(nxt, mask)
+                    logp = torch.log_softmax(logits.float(), dim=-1)  # [rows, V]
+                    vocab = logp.shape[-1]
+                    if eos_token_id is not None and bool(finished.any()):
+                        frozen = torch.full((vocab,), float("-inf"), device=device)
+                        frozen[eos_token_id] = 0.0
+                        logp[finished] = frozen
+                    cand = self._filter_for_sampling(logp, temperature, top_k, top_p) if do_sample else logp
+                    joint = (scores.unsqueeze(1) + cand).view(batch_size, num_beams * vocab)
+                    if do_sample:
+                        pick = torch.multinomial(torch.softmax(joint, dim=-1), num_beams, replacement=False,
+                                                 generator=generator)
+                        top = torch.gather(joint, 1, pick)
+                    else:
+                        top, pick = torch.topk(joint, num_beams, dim=-1)
+                    parents = (pick // vocab + group_base).flatten()
+                    chosen = (pick % vocab).flatten()
+                    parent_list, chosen_list = parents.tolist(), chosen.tolist()
+                    tokens = [tokens[p] + [t] for p, t in zip(parent_list, chosen_list)]
+                    finished = finished[parents]
+                    if eos_token_id is not None:
+                        finished = finished | (chosen == eos_token_id)
+                    scores = top.flatten()
+                    self._decoder.reorder_rows(self._sid, parent_list)
+                    nxt = chosen.to(ids.dtype).unsqueeze(1)
+                    mask = torch.cat([mask[parents], mask.new_ones((rows, 1))], dim=1)
+                    if bool(finished.all()):
+                        break
+                final_scores = scores.tolist()
+            finally:
+                self._close()
+            results: list[list[list[int]]] = []
+            for g in range(batch_size):
+                ranked = []
+                for r in range(g * num_beams, (g + 1) * num_beams):
+                    seq = tokens[r]
+                    if eos_token_id is not None and eos_token_id in seq:
+                        seq = seq[: seq.index(eos_token_id) + 1]
+                    ranked.append((final_scores[r] / (max(len(seq), 1) ** length_penalty), seq))
+                ranked.sort(key=lambda x: x[0], reverse=True)
+                results.append([seq for _, seq in ranked[:num_return_sequences]])
+            if batch_size == 1:
+                return results[0][0] if num_return_sequences == 1 else results[0]
+            return [grp[0] for grp in results] if num_return_sequences == 1 else results
+        finally:
+            self._lock.release()
+
+    @staticmethod
+    def _filter_for_sampling(logp, temperature, top_k, top_p):
+        """paged_model.py:530-546: temperature, top-k and nucleus filtering of log-probs,
+        renormalized."""
+        scaled = logp / temperature
+        if top_k is not None:
+            kth = torch.topk(scaled, min(top_k, scaled.shape[-1]), dim=-1).values[:, -1, None]
+            scaled = scaled.masked_fill(scaled < kth, float("-inf"))
+        if top_p is not None:
+            srt, order = torch.sort(scaled, descending=True, dim=-1)
+            probs = torch.softmax(srt, dim=-1)
+            srt = srt.masked_fill(torch.cumsum(probs, dim=-1) - probs > top_p, float("-inf"))
+            scaled = torch.full_like(scaled, float("-inf")).scatter(-1, order, srt)
+        return torch.log_softmax(scaled, dim=-1)
 
     @staticmethod
     def _sample_next_token(logits, *, temperature, top_k, top_p, generator):
