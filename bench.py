@@ -234,6 +234,66 @@ def continuous(args):
     }
 
 
+def register(args):
+    """Prompt registration at Qwen2.5-0.5B geometry (24 layers, 2 KV heads, head_dim 64, fp16,
+    32-token blocks, 64 resident blocks, recent_only): for prompts of 8k, 32k and 64k tokens,
+    (a) prefill with placement: every block written straight to its tier, host blocks into
+    the pinned mirror over the host link; (b) prefill in HBM, then the first step's placement
+    burst that evicts all but the recent blocks. Reports the time and the host-link rate of
+    each (K/V bytes that crossed the link / time)."""
+    import torch
+
+    from pager_hf import PagedDecoder
+
+    L, HQ, HKV, D, T = 24, 14, 2, 64, 32
+    rows = []
+    for n in (8192, 32768, 65536):
+        g = torch.Generator(device="cuda").manual_seed(n)
+        ks = [(torch.randn(1, HKV, n, D, device="cuda", generator=g) * 0.5).half() for _ in range(L)]
+        vs = [(torch.randn(1, HKV, n, D, device="cuda", generator=g) * 0.5).half() for _ in range(L)]
+        line = {"prompt_tokens": n}
+        for place in (True, False):
+            best = None
+            for _ in range(args.register_reps):
+                dec = PagedDecoder(num_layers=L, num_query_heads=HQ, num_kv_heads=HKV, head_dim=D, tokens_per_block=T,
+                                   dtype=torch.float16, device="cuda", pool_blocks=n // T + 16,
+                                   host_blocks=n // T + 16, staging_blocks=256, staging_buffers=2)
+                sid = dec.add_session(capacity_tokens=n + 64, vram_budget=64 * MIB16, ram_budget=1 << 40,
+                                      recent_window=63, policy="recent_only")
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                moves = dec.prefill(sid, ks, vs, n - 1, place=place)
+                if not place:  # the first step's placement (no attention: the tiers the pager picks)
+                    s = dec.sessions[sid]
+                    nb = (n - 1) // T
+                    s.pager.on_step(nb - 1, 0, [1.0 / nb] * nb)
+                    s.pager.force_rebalance(nb - 1)
+                    _, to_cpu, _, _ = dec.pool.apply_tiers(sid, s.pager.tiers())
+                    moves = {"to_cpu": to_cpu}
+                torch.cuda.synchronize()
+                dec.pool.sync()
+                dt = time.perf_counter() - t0
+                host_blocks = len(moves["to_cpu"]) if not place else sum(1 for _ in dec.pool.block_ids(sid, False))
+                best = dt if best is None or dt < best else best
+                dec.pool.close()
+            link = host_blocks * T * 2 * HKV * D * 2 * L
+            key = "prefill_placed" if place else "prefill_then_evict"
+            line[key] = {"ms": round(best * 1e3, 2), "host_bytes": link, "host_link_GBs": round(link / best / 1e9, 2)}
+        rows.append(line)
+        del ks, vs
+    return {
+        "metric": "prompt registration time and host-link GB/s (Qwen2.5-0.5B geometry, 24 layers)",
+        "value": rows[1]["prefill_then_evict"]["host_link_GBs"],
+        "unit": "GB/s",
+        "higher_is_better": True,
+        "sizes": rows,
+        "dtype": "fp16",
+        "data": "synthetic K/V",
+        "config": {"workload": "prompt registration, 8k/32k/64k tokens, 64 resident blocks of 32 tokens, recent_only",
+                   "value_is": "32k prompt, HBM prefill then the first placement burst"},
+    }
+
+
 class SimpleTokenizer:
     eos_token_id = None
 
@@ -289,8 +349,10 @@ def main() -> int:
                     help="host blocks read in place over the host link, or copied into a staging ring")
     ap.add_argument("--resident-layers", type=int, default=24,
                     help="layers of the all-resident HBM measurement (0 skips it)")
-    ap.add_argument("--workload", choices=["batch8", "continuous"], default="batch8",
-                    help="batch8: the headline line; continuous: the 64-request continuous-batching run")
+    ap.add_argument("--workload", choices=["batch8", "continuous", "register"], default="batch8",
+                    help="batch8: the headline line; continuous: the 64-request continuous-batching run; "
+                         "register: prompt registration at 8k-64k tokens")
+    ap.add_argument("--register-reps", type=int, default=3)
     ap.add_argument("--cb-rounds", type=int, default=24)
     ap.add_argument("--cb-extra-requests", type=int, default=64)
     ap.add_argument("--cb-policy", default="recent_only")
@@ -307,6 +369,11 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a HIP device", file=sys.stderr)
         return 2
+    if args.workload == "register":
+        line = register(args)
+        line.update({"n_gpus": 1, "steps": args.register_reps, "warmup": 0, "scaling": "weak", "vs_baseline": None})
+        print(json.dumps(line), flush=True)
+        return 0
     if args.workload == "continuous":
         line = continuous(args)
         line.update({"n_gpus": 1, "steps": args.cb_rounds, "warmup": 1, "higher_is_better": True, "scaling": "weak",

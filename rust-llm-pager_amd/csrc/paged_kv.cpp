@@ -22,27 +22,32 @@ namespace {
 // One workgroup per block of records: converts tokens of one (row, layer) from the
 // [Hkv, n_src, D] layout into records at dst + slot[i] * rec (zero past n_tokens), or back.
 __global__ void hf_to_records_kernel(const uint16_t* k, const uint16_t* v, int64_t n_src, int64_t n_tokens,
-                                     int64_t first_block, const int32_t* dst_slot, uint16_t* dst, int hkv, int tpb,
-                                     int d) {
-  const int i = blockIdx.x;
-  const int64_t b = first_block + i;
+                                     const int64_t* dst, uint16_t* pool, uint16_t* host, int hkv, int tpb, int d) {
+  // Block i of a [Hkv, n_src, D] tensor pair into its record: dst[i] >= 0 is an HBM pool
+  // slot, dst[i] < 0 the host mirror record -dst[i] - 1 (written in place over the host
+  // link). 16 bytes per load and store; tokens past n_tokens are zero.
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  const int64_t b = blockIdx.x;
+  const int64_t di = dst[b];
   const size_t rec = (size_t)2 * hkv * tpb * d;
-  uint16_t* kr = dst + (size_t)dst_slot[i] * rec;
+  uint16_t* kr = di >= 0 ? pool + (size_t)di * rec : host + (size_t)(-di - 1) * rec;
   uint16_t* vr = kr + (size_t)hkv * tpb * d;
-  const int per = hkv * tpb * d;
-  for (int e = threadIdx.x; e < per; e += blockDim.x) {
-    const int h = e / (tpb * d);
-    const int r = e - h * tpb * d;
-    const int t = r / d, dd = r - t * d;
+  const int cpr = d / 8;  // 16-byte chunks per token row
+  const int per = hkv * tpb * cpr;
+  for (int c = threadIdx.x; c < per; c += blockDim.x) {
+    const int h = c / (tpb * cpr);
+    const int r = c - h * tpb * cpr;
+    const int t = r / cpr, cc = r - t * cpr;
     const int64_t tok = b * tpb + t;
-    uint16_t kv = 0, vv = 0;
+    u32x4 kx = {0u, 0u, 0u, 0u}, vx = {0u, 0u, 0u, 0u};
     if (tok < n_tokens) {
-      const size_t src = ((size_t)h * n_src + tok) * d + dd;
-      kv = k[src];
-      vv = v[src];
+      const size_t src = ((size_t)h * n_src + tok) * d + (size_t)cc * 8;
+      kx = *reinterpret_cast<const u32x4*>(k + src);
+      vx = *reinterpret_cast<const u32x4*>(v + src);
     }
-    kr[e] = kv;
-    vr[e] = vv;
+    const size_t o = (size_t)(h * tpb + t) * d + (size_t)cc * 8;
+    *reinterpret_cast<u32x4*>(kr + o) = kx;
+    *reinterpret_cast<u32x4*>(vr + o) = vx;
   }
 }
 
@@ -67,12 +72,16 @@ __global__ void records_to_hf_kernel(const uint16_t* src, const int32_t* src_slo
   }
 }
 
-// Copies whole records within one layer's pool: workgroup i copies record pairs[2i] to
-// record pairs[2i + 1] with 16-byte loads and stores.
-__global__ void copy_records_kernel(uint16_t* pool, const int32_t* pairs, int64_t rec_vec) {
+// Copies whole records for every layer: workgroup (i, layer) copies record pairs[2i] of
+// bases[src_tbl + layer] to record pairs[2i + 1] of bases[dst_tbl + layer], 16 bytes per
+// load and store. A base is a layer's HBM pool or the device address of its pinned host
+// mirror, so one launch serves evictions, loads and row copies.
+__global__ void copy_records_kernel(void* const* bases, int src_tbl, int dst_tbl, const int64_t* pairs,
+                                    int64_t rec_vec) {
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-  const u32x4* src = reinterpret_cast<const u32x4*>(pool) + (size_t)pairs[2 * blockIdx.x] * rec_vec;
-  u32x4* dst = reinterpret_cast<u32x4*>(pool) + (size_t)pairs[2 * blockIdx.x + 1] * rec_vec;
+  const int layer = blockIdx.y;
+  const u32x4* src = static_cast<const u32x4*>(bases[src_tbl + layer]) + (size_t)pairs[2 * blockIdx.x] * rec_vec;
+  u32x4* dst = static_cast<u32x4*>(bases[dst_tbl + layer]) + (size_t)pairs[2 * blockIdx.x + 1] * rec_vec;
   for (int64_t i = threadIdx.x; i < rec_vec; i += blockDim.x) dst[i] = src[i];
 }
 
@@ -89,7 +98,11 @@ PagedKV::~PagedKV() {
     if (p) hipHostFree(p);
   if (stage_) hipFree(stage_);
   if (ws_) hipFree(ws_);
-  if (pairs_dev_) hipFree(pairs_dev_);
+  if (bases_dev_) hipFree(bases_dev_);
+  for (IndexBuf& b : index_bufs_) {
+    if (b.host) hipHostFree(b.host);
+    if (b.done) hipEventDestroy(b.done);
+  }
   if (plan_host_) hipHostFree(plan_host_);
   if (mass_host_) hipHostFree(mass_host_);
   for (hipEvent_t e : buf_free_) hipEventDestroy(e);
@@ -168,6 +181,13 @@ int PagedKV::init() {
   PGR_HIP(hipEventCreateWithFlags(&plan_uploaded_, hipEventDisableTiming));
   PGR_HIP(hipEventCreateWithFlags(&compute_mark_, hipEventDisableTiming));
   PGR_HIP(hipEventCreateWithFlags(&copy_mark_, hipEventDisableTiming));
+  for (IndexBuf& b : index_bufs_) PGR_HIP(hipEventCreateWithFlags(&b.done, hipEventDisableTiming));
+  {
+    std::vector<void*> bases(pool_);
+    bases.insert(bases.end(), host_dev_.begin(), host_dev_.end());
+    PGR_HIP(hipMalloc(&bases_dev_, sizeof(void*) * bases.size()));
+    PGR_HIP(hipMemcpy(bases_dev_, bases.data(), sizeof(void*) * bases.size(), hipMemcpyHostToDevice));
+  }
   free_slots_.resize(cfg_.pool_slots);
   for (int64_t i = 0; i < cfg_.pool_slots; ++i) free_slots_[i] = (int32_t)(cfg_.pool_slots - 1 - i);
   host_free_.clear();
@@ -274,14 +294,39 @@ int PagedKV::set_lo(int sid, const int32_t* lo_per_row) {
   return kOk;
 }
 
-int PagedKV::ensure_pairs(size_t n) {
-  if (n <= pairs_cap_) return kOk;
-  if (pairs_dev_) PGR_HIP(hipFree(pairs_dev_));
-  pairs_dev_ = nullptr;
-  pairs_cap_ = 0;
-  const size_t want = std::max<size_t>(n, 256);
-  PGR_HIP(hipMalloc(&pairs_dev_, want * 2 * sizeof(int32_t)));
-  pairs_cap_ = want;
+int PagedKV::acquire_index_buf(size_t n, IndexBuf** out) {
+  IndexBuf& b = index_bufs_[next_index_buf_];
+  next_index_buf_ = (next_index_buf_ + 1) % kIndexBufs;
+  if (b.pending) {
+    PGR_HIP(hipEventSynchronize(b.done));
+    b.pending = false;
+  }
+  if (n > b.cap) {
+    if (b.host) PGR_HIP(hipHostFree(b.host));
+    b.host = nullptr;
+    b.dev = nullptr;
+    b.cap = 0;
+    const size_t want = std::max<size_t>(n, 4096);
+    PGR_HIP(hipHostMalloc(reinterpret_cast<void**>(&b.host), want * sizeof(int64_t), hipHostMallocDefault));
+    PGR_HIP(hipHostGetDevicePointer(reinterpret_cast<void**>(&b.dev), b.host, 0));
+    b.cap = want;
+  }
+  *out = &b;
+  return kOk;
+}
+
+int PagedKV::launch_copies(std::vector<int64_t>& pairs, int src_tbl, int dst_tbl, hipStream_t stream) {
+  if (pairs.empty()) return kOk;
+  IndexBuf* ib = nullptr;
+  int rc = acquire_index_buf(pairs.size(), &ib);
+  if (rc != kOk) return rc;
+  std::memcpy(ib->host, pairs.data(), pairs.size() * sizeof(int64_t));
+  const dim3 grid((unsigned)(pairs.size() / 2), (unsigned)cfg_.num_layers);
+  copy_records_kernel<<<grid, 256, 0, stream>>>(bases_dev_, src_tbl, dst_tbl, ib->dev, (int64_t)(rec_bytes() / 16));
+  PGR_HIP(hipGetLastError());
+  PGR_HIP(hipEventRecord(ib->done, stream));
+  ib->pending = true;
+  pairs.clear();
   return kOk;
 }
 
@@ -314,10 +359,9 @@ int PagedKV::reorder_rows(int sid, const int32_t* src, int n, hipStream_t stream
         return fail(kErrState, "rows of a session differ in residency");
   // Queued kernels and copies may still read or write this session's records.
   PGR_HIP(hipDeviceSynchronize());
-  const size_t rec = rec_bytes();
   std::vector<int32_t> slot(s.slot.size(), -1);
   std::vector<uint8_t> hv(s.host_valid.size(), 0);
-  std::vector<int32_t> pairs;  // HBM copies (from slot, to slot)
+  std::vector<int64_t> pairs, host_pairs;  // (from record, to record) in the pool / host mirror
   for (int r = 0; r < rows; ++r) {
     const int o = src[r], h = holder[r];
     for (int64_t b = 0; b < nb; ++b) {
@@ -329,23 +373,16 @@ int PagedKV::reorder_rows(int sid, const int32_t* src, int n, hipStream_t stream
       }
       const uint8_t v = s.host_valid[b * rows + o];
       hv[b * rows + r] = v;
-      if (v && h != o)
-        for (int l = 0; l < cfg_.num_layers; ++l) {
-          char* base = static_cast<char*>(host_[l]);
-          std::memcpy(base + (size_t)(s.row[h].host_off + b) * rec, base + (size_t)(s.row[o].host_off + b) * rec, rec);
-        }
+      if (v && h != o) {
+        host_pairs.push_back(s.row[o].host_off + b);
+        host_pairs.push_back(s.row[h].host_off + b);
+      }
     }
   }
-  if (!pairs.empty()) {
-    int rc = ensure_pairs(pairs.size() / 2);
+  if (!pairs.empty() || !host_pairs.empty()) {
+    int rc = launch_copies(pairs, 0, 0, stream);
+    if (rc == kOk) rc = launch_copies(host_pairs, cfg_.num_layers, cfg_.num_layers, stream);
     if (rc != kOk) return rc;
-    PGR_HIP(hipMemcpy(pairs_dev_, pairs.data(), pairs.size() * sizeof(int32_t), hipMemcpyHostToDevice));
-    const int64_t rec_vec = (int64_t)(rec / 16);
-    for (int l = 0; l < cfg_.num_layers; ++l) {
-      copy_records_kernel<<<(unsigned)(pairs.size() / 2), 256, 0, stream>>>(static_cast<uint16_t*>(pool_[l]), pairs_dev_,
-                                                                           rec_vec);
-      PGR_HIP(hipGetLastError());
-    }
     PGR_HIP(hipStreamSynchronize(stream));
   }
   std::vector<Row> row(rows);
@@ -395,81 +432,29 @@ int PagedKV::import_tokens(int sid, int row, int layer, const void* k, const voi
   if (row < 0 || row >= s.rows || layer < 0 || layer >= cfg_.num_layers) return fail(kErrInvalid, "row/layer out of range");
   if (n_tokens != s.n_tokens || n_src < n_tokens) return fail(kErrInvalid, "n_tokens must equal the session length");
   if (in_step_) return fail(kErrState, "import during a decode step");
+  if (((uintptr_t)k | (uintptr_t)v) % 16 != 0) return fail(kErrInvalid, "k and v must be 16-byte aligned");
   const int64_t T = cfg_.tokens_per_block;
   const int64_t nb = (n_tokens + T - 1) / T;
-  const size_t rec = rec_bytes();
-  const int64_t cap = cfg_.staging_slots * cfg_.staging_buffers;
-  // Earlier streamed work may still read the staging ring.
-  PGR_HIP(hipStreamSynchronize(stream));
-  PGR_HIP(hipStreamSynchronize(copy_stream_));
-  std::vector<int32_t> slots;
-  int32_t* d_slots = nullptr;
-  PGR_HIP(hipMalloc(&d_slots, sizeof(int32_t) * (size_t)std::max<int64_t>(cap, 1)));
-  int rc = kOk;
-  for (int64_t b0 = 0; b0 < nb && rc == kOk; b0 += cap) {
-    const int64_t cnt = std::min(cap, nb - b0);
-    // Pass 1: resident blocks straight into the pool; pass 2: host blocks via staging.
-    for (int pass = 0; pass < 2 && rc == kOk; ++pass) {
-      slots.clear();
-      std::vector<int64_t> ids;
-      for (int64_t i = 0; i < cnt; ++i) {
-        const int64_t b = b0 + i;
-        const int32_t sl = s.slot[b * s.rows + row];
-        if (pass == 0 && sl >= 0) {
-          slots.push_back(sl);
-          ids.push_back(b);
-        }
-        if (pass == 1 && sl < 0) {
-          slots.push_back((int32_t)ids.size());
-          ids.push_back(b);
-        }
-      }
-      if (ids.empty()) continue;
-      // Consecutive ids are processed as runs so each kernel launch covers a contiguous id range.
-      size_t i = 0;
-      while (i < ids.size() && rc == kOk) {
-        size_t j = i + 1;
-        while (j < ids.size() && ids[j] == ids[j - 1] + 1) ++j;
-        const int64_t first = ids[i];
-        const int run = (int)(j - i);
-        std::vector<int32_t> run_slots(slots.begin() + i, slots.begin() + j);
-        if (pass == 1)
-          for (int q = 0; q < run; ++q) run_slots[q] = q;
-        hipError_t e = hipMemcpyAsync(d_slots, run_slots.data(), sizeof(int32_t) * run, hipMemcpyHostToDevice, stream);
-        if (e != hipSuccess) {
-          rc = hip_fail(e, "hipMemcpyAsync(slots)");
-          break;
-        }
-        uint16_t* dst = static_cast<uint16_t*>(pass == 0 ? pool_[layer] : stage_);
-        hf_to_records_kernel<<<run, 256, 0, stream>>>(static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
-                                                      n_src, n_tokens, first, d_slots, dst, cfg_.kv_heads, (int)T,
-                                                      cfg_.head_dim);
-        e = hipGetLastError();
-        if (e != hipSuccess) {
-          rc = hip_fail(e, "hf_to_records_kernel");
-          break;
-        }
-        if (pass == 1) {
-          char* hdst = static_cast<char*>(host_[layer]) + (size_t)(s.row[row].host_off + first) * rec;
-          e = hipMemcpyAsync(hdst, stage_, rec * run, hipMemcpyDeviceToHost, stream);
-          if (e != hipSuccess) {
-            rc = hip_fail(e, "hipMemcpyAsync(D2H import)");
-            break;
-          }
-          for (int q = 0; q < run; ++q) s.host_valid[(first + q) * s.rows + row] = 1;
-        }
-        // The slot list buffer is reused by the next launch.
-        e = hipStreamSynchronize(stream);
-        if (e != hipSuccess) {
-          rc = hip_fail(e, "hipStreamSynchronize(import)");
-          break;
-        }
-        i = j;
-      }
-    }
+  if (nb == 0) return kOk;
+  // One launch: resident blocks into their pool slots, host blocks straight into the
+  // pinned mirror through its device mapping.
+  IndexBuf* ib = nullptr;
+  int rc = acquire_index_buf((size_t)nb, &ib);
+  if (rc != kOk) return rc;
+  for (int64_t b = 0; b < nb; ++b) {
+    const int32_t sl = s.slot[b * s.rows + row];
+    ib->host[b] = sl >= 0 ? (int64_t)sl : -(s.row[row].host_off + b) - 1;
   }
-  hipFree(d_slots);
-  return rc;
+  hf_to_records_kernel<<<(unsigned)nb, 256, 0, stream>>>(
+      static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v), n_src, n_tokens, ib->dev,
+      static_cast<uint16_t*>(pool_[layer]), static_cast<uint16_t*>(host_dev_[layer]), cfg_.kv_heads, (int)T,
+      cfg_.head_dim);
+  PGR_HIP(hipGetLastError());
+  PGR_HIP(hipEventRecord(ib->done, stream));
+  ib->pending = true;
+  for (int64_t b = 0; b < nb; ++b)
+    if (s.slot[b * s.rows + row] < 0) s.host_valid[b * s.rows + row] = 1;
+  return kOk;
 }
 
 int PagedKV::export_tokens(int sid, int row, int layer, void* k, void* v, int64_t n_tokens, hipStream_t stream) {
@@ -600,6 +585,7 @@ double PagedKV::ram_usage_ratio() const {
 }
 
 int PagedKV::move_block(Session& s, int64_t b, bool to_gpu, hipStream_t) {
+  // Record copies are collected here and issued by apply_tiers in one launch per direction.
   const size_t rec = rec_bytes();
   for (int r = 0; r < s.rows; ++r) {
     const size_t k = (size_t)b * s.rows + r;
@@ -608,26 +594,21 @@ int PagedKV::move_block(Session& s, int64_t b, bool to_gpu, hipStream_t) {
       if (sl < 0) return fail(kErrCapacity, "HBM pool exhausted while loading a block");
       s.slot[k] = sl;
       if (s.host_valid[k]) {
-        for (int l = 0; l < cfg_.num_layers; ++l) {
-          const char* src = static_cast<const char*>(host_[l]) + (size_t)(s.row[r].host_off + b) * rec;
-          char* dst = static_cast<char*>(pool_[l]) + (size_t)sl * rec;
-          PGR_HIP(hipMemcpyAsync(dst, src, rec, hipMemcpyHostToDevice, copy_stream_));
-          stats_.load_bytes_copied += rec;
-        }
+        load_pairs_.push_back(s.row[r].host_off + b);
+        load_pairs_.push_back(sl);
+        stats_.load_bytes_copied += rec * cfg_.num_layers;
       }
     } else {
       const int32_t sl = s.slot[k];
       if (sl >= 0) {
         if (!s.host_valid[k]) {
-          for (int l = 0; l < cfg_.num_layers; ++l) {
-            const char* src = static_cast<const char*>(pool_[l]) + (size_t)sl * rec;
-            char* dst = static_cast<char*>(host_[l]) + (size_t)(s.row[r].host_off + b) * rec;
-            PGR_HIP(hipMemcpyAsync(dst, src, rec, hipMemcpyDeviceToHost, copy_stream_));
-            stats_.evict_bytes_copied += rec;
-          }
+          evict_pairs_.push_back(sl);
+          evict_pairs_.push_back(s.row[r].host_off + b);
+          stats_.evict_bytes_copied += rec * cfg_.num_layers;
           s.host_valid[k] = 1;
         }
-        // Recycled only by later work ordered after copy_mark_ (see apply_tiers).
+        // Recycled only by later work ordered after copy_mark_ (see apply_tiers); a load of
+        // this same call that takes the slot is copied after the evictions.
         free_slot(sl);
         s.slot[k] = -1;
       }
@@ -659,17 +640,13 @@ int PagedKV::apply_tiers(int sid, const uint8_t* tiers, int64_t n_tiers, int64_t
     PGR_HIP(hipStreamWaitEvent(copy_stream_, compute_mark_, 0));
     return kOk;
   };
-  PendingTiming t_cpu{nullptr, nullptr, 0}, t_gpu{nullptr, nullptr, 0};
+  evict_pairs_.clear();
+  load_pairs_.clear();
   int rc = kOk;
   for (int64_t b = 0; b < n_full; ++b) {
     const int desired = b < n_tiers ? tiers[b] : 2;
     if (desired == 0 && !s.on_gpu[b]) {
       if ((rc = order_streams()) != kOk) break;
-      if (!t_gpu.start) {
-        hipEventCreate(&t_gpu.start);
-        hipEventCreate(&t_gpu.stop);
-        hipEventRecord(t_gpu.start, copy_stream_);
-      }
       rc = move_block(s, b, true, stream);
       if (rc != kOk) break;
       cpu_bytes_ -= bb;
@@ -684,11 +661,6 @@ int PagedKV::apply_tiers(int sid, const uint8_t* tiers, int64_t n_tiers, int64_t
         break;
       }
       if ((rc = order_streams()) != kOk) break;
-      if (!t_cpu.start) {
-        hipEventCreate(&t_cpu.start);
-        hipEventCreate(&t_cpu.stop);
-        hipEventRecord(t_cpu.start, copy_stream_);
-      }
       rc = move_block(s, b, false, stream);
       if (rc != kOk) break;
       cpu_bytes_ += bb;
@@ -698,15 +670,19 @@ int PagedKV::apply_tiers(int sid, const uint8_t* tiers, int64_t n_tiers, int64_t
       to_cpu[(*n_cpu)++] = b;
     }
   }
-  if (t_gpu.start) {
-    hipEventRecord(t_gpu.stop, copy_stream_);
-    t_gpu.bytes = 1;  // direction tag: to GPU
-    move_timing_.push_back(t_gpu);
-  }
-  if (t_cpu.start) {
-    hipEventRecord(t_cpu.stop, copy_stream_);
-    t_cpu.bytes = 0;
-    move_timing_.push_back(t_cpu);
+  // Evictions first: a load may reuse a slot an eviction of this call freed.
+  for (int dir = 0; dir < 2; ++dir) {
+    std::vector<int64_t>& pairs = dir == 0 ? evict_pairs_ : load_pairs_;
+    if (pairs.empty()) continue;
+    PendingTiming t{nullptr, nullptr, dir};  // bytes field tags the direction: 0 to host, 1 to GPU
+    hipEventCreate(&t.start);
+    hipEventCreate(&t.stop);
+    hipEventRecord(t.start, copy_stream_);
+    const int l = cfg_.num_layers;
+    const int crc = dir == 0 ? launch_copies(pairs, 0, l, copy_stream_) : launch_copies(pairs, l, 0, copy_stream_);
+    hipEventRecord(t.stop, copy_stream_);
+    move_timing_.push_back(t);
+    if (crc != kOk && rc == kOk) rc = crc;
   }
   if (ordered) {
     PGR_HIP(hipEventRecord(copy_mark_, copy_stream_));

@@ -184,7 +184,21 @@ class PagedKV {
   int ensure_block_capacity(Session& s, int64_t blocks);
   int move_block(Session& s, int64_t b, bool to_gpu, hipStream_t stream);
   int resolve_timing();
-  int ensure_pairs(size_t n);
+  // Record index lists for the copy kernels live in pinned host memory that the kernels read
+  // in place, in a small ring so a list is not overwritten while a queued kernel still
+  // needs it.
+  struct IndexBuf {
+    int64_t* host = nullptr;  // pinned
+    int64_t* dev = nullptr;   // device address of `host`
+    size_t cap = 0;           // entries
+    hipEvent_t done = nullptr;
+    bool pending = false;
+  };
+  static constexpr int kIndexBufs = 4;
+  int acquire_index_buf(size_t n, IndexBuf** out);
+  // Copies records (from, to) pairs for every layer in one launch; tables 0 (HBM pool) or
+  // num_layers (host mirror) select source and destination. Clears `pairs`.
+  int launch_copies(std::vector<int64_t>& pairs, int src_tbl, int dst_tbl, hipStream_t stream);
 
   PagedKVConfig cfg_;
   std::string err_;
@@ -195,8 +209,10 @@ class PagedKV {
   void* ws_ = nullptr;
   size_t ws_bytes_ = 0;
   int n_cu_ = 0;                  // compute units of the device
-  int32_t* pairs_dev_ = nullptr;  // (from slot, to slot) pairs of a record copy
-  size_t pairs_cap_ = 0;
+  void** bases_dev_ = nullptr;  // [pool_0 .. pool_{L-1}, host_dev_0 .. host_dev_{L-1}] on the device
+  IndexBuf index_bufs_[kIndexBufs];
+  int next_index_buf_ = 0;
+  std::vector<int64_t> evict_pairs_, load_pairs_;  // moves of the current apply_tiers call
   void* plan_host_ = nullptr;  // pinned upload buffer for the step plan
   size_t plan_host_bytes_ = 0;
   float* mass_host_ = nullptr;  // pinned readback of the step's block mass
