@@ -59,11 +59,14 @@ class BatchedPagedEngine:
         host_token_capacity: int | None = None,
         prefill_chunk_tokens: int = 512,
         stream_mode: str = "direct",
+        staging_blocks: int = 64,
+        staging_buffers: int = 2,
         collect_stats: bool = False,
     ):
         """``max_context_tokens``: most tokens one session may hold (prompt + generated);
         ``host_token_capacity``: tokens the pinned host mirror holds over all sessions
-        (default max_sessions * max_context_tokens)."""
+        (default max_sessions * max_context_tokens); ``staging_blocks`` / ``staging_buffers``:
+        the HBM staging ring of the staged stream mode (records per buffer, buffers)."""
         if max_sessions < 1:
             raise ValueError("max_sessions must be >= 1")
         self.model = model
@@ -86,8 +89,8 @@ class BatchedPagedEngine:
         host = -(-host_tokens // T) + max_sessions * 2
         self.decoder = PagedDecoder(
             num_layers=layers, num_query_heads=hq, num_kv_heads=hkv, head_dim=d, tokens_per_block=T, dtype=dtype,
-            device=device, pool_blocks=pool, host_blocks=host, staging_blocks=64, staging_buffers=2,
-            stream_mode=stream_mode,
+            device=device, pool_blocks=pool, host_blocks=host, staging_blocks=staging_blocks,
+            staging_buffers=staging_buffers, stream_mode=stream_mode,
         )
         self._pager_kwargs = dict(vram_budget=vram_budget_per_session, ram_budget=ram_budget_per_session,
                                   recent_window=recent_window, rebalance_interval=rebalance_interval,

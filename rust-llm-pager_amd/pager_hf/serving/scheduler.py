@@ -108,11 +108,14 @@ class ContinuousBatchingScheduler:
         max_context_tokens: int = 8192,
         host_token_capacity: int | None = None,
         stream_mode: str = "direct",
+        staging_blocks: int = 64,
+        staging_buffers: int = 2,
         engine: BatchedPagedEngine | None = None,
     ):
         """Arguments of scheduler.py:118-133. Added: ``max_context_tokens`` (most tokens one
         request or session holds), ``host_token_capacity`` (pinned host tokens over all
-        sessions), ``stream_mode`` and ``engine`` (an existing BatchedPagedEngine to serve
+        sessions), ``stream_mode`` / ``staging_blocks`` / ``staging_buffers`` (host block
+        streaming of the engine) and ``engine`` (an existing BatchedPagedEngine to serve
         from). ``use_streaming_attention=False`` is not built; the group size has no effect."""
         if max_concurrent_sessions < 1:
             raise ValueError(f"max_concurrent_sessions must be >= 1, got {max_concurrent_sessions}")
@@ -136,6 +139,8 @@ class ContinuousBatchingScheduler:
             max_context_tokens=max_context_tokens,
             host_token_capacity=host_token_capacity,
             stream_mode=stream_mode,
+            staging_blocks=staging_blocks,
+            staging_buffers=staging_buffers,
         )
         self._engine = engine
         self._device = torch.device(device)
