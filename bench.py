@@ -301,36 +301,50 @@ class SimpleTokenizer:
 
 
 def cpu_baseline(ctx, budget_s=15.0):
-    """Times the oracle's fp32 dense attention on the host over a bounded sample of the same
-    workload (whole steps of the batch, upcast included); returns KV GB/s and tokens/s."""
-    import numpy as np
+    """The reference's CPU path timed on the host: dense fp32 GQA attention plus the per-block
+    attention mass (the math of tests/test_streaming_attention.py:20-40, as the reference's
+    torch prototype runs it on CPU), over a bounded sample of whole steps of the same batch
+    (fp16 K/V upcast included), with torch on the host threads this job may use.
+    Returns KV GB/s and tokens/s."""
+    import os
 
-    from oracle.attention import dense_reference
+    import torch
 
     c = CFG
-    rng = np.random.default_rng(0)
-    kv = [((rng.standard_normal((1, c["hkv"], n + 1, c["d"])) * 0.5).astype(np.float16),
-           (rng.standard_normal((1, c["hkv"], n + 1, c["d"])) * 0.5).astype(np.float16)) for n in ctx]
-    q = (rng.standard_normal((1, c["hq"], c["d"])) * 0.5).astype(np.float16)
-    bytes_per_step = sum((n + 1) * 2 * c["hkv"] * c["d"] * 2 for n in ctx)
-    steps = 0
-    t0 = time.perf_counter()
-    while True:
-        for k, v in kv:
-            dense_reference(q.astype(np.float32), k.astype(np.float32), v.astype(np.float32),
-                            n_rep=c["hq"] // c["hkv"], tokens_per_block=c["tpb"])
-        steps += 1
-        if time.perf_counter() - t0 > budget_s or steps >= 50:
-            break
-    dt = time.perf_counter() - t0
+    threads = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
+    previous = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        g = torch.Generator().manual_seed(0)
+        n_rep, d, T = c["hq"] // c["hkv"], c["d"], c["tpb"]
+        kv = [((torch.randn(c["hkv"], n + 1, d, generator=g) * 0.5).half(),
+               (torch.randn(c["hkv"], n + 1, d, generator=g) * 0.5).half()) for n in ctx]
+        q = (torch.randn(c["hkv"], n_rep, d, generator=g) * 0.5).half()
+        scale = 1.0 / d ** 0.5
+        bytes_per_step = sum((n + 1) * 2 * c["hkv"] * d * 2 for n in ctx)
+        steps = 0
+        t0 = time.perf_counter()
+        while True:
+            for k, v in kv:
+                n = k.shape[1]
+                w = torch.softmax((q.float() @ k.float().transpose(1, 2)) * scale, dim=-1)  # [Hkv, n_rep, n]
+                _ = w @ v.float()
+                nb = -(-n // T)
+                _ = torch.nn.functional.pad(w, (0, nb * T - n)).view(c["hkv"], n_rep, nb, T).sum(-1)
+            steps += 1
+            if time.perf_counter() - t0 > budget_s or steps >= 2000:
+                break
+        dt = time.perf_counter() - t0
+    finally:
+        torch.set_num_threads(previous)
     return {
         "value": round(bytes_per_step * steps / dt / 1e9, 3),
         "unit": "GB/s",
         "tokens_per_s": round(c["batch"] * steps / dt, 2),
-        "cores": 1,
+        "cores": threads,
         "kind": "port",
-        "sample": f"{steps} full decode steps of the batch-8 workload (dense fp32 numpy oracle, fp16->fp32 upcast "
-                  f"included), {dt:.1f} s",
+        "sample": f"{steps} full decode steps of the batch-8 workload: dense fp32 attention and block mass in torch "
+                  f"on {threads} host threads (fp16 K/V upcast included), {dt:.1f} s",
     }
 
 
