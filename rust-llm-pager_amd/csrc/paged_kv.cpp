@@ -51,23 +51,28 @@ __global__ void hf_to_records_kernel(const uint16_t* k, const uint16_t* v, int64
   }
 }
 
-__global__ void records_to_hf_kernel(const uint16_t* src, const int32_t* src_slot, int64_t first_block,
+__global__ void records_to_hf_kernel(const int64_t* src, const uint16_t* pool, const uint16_t* host,
                                      int64_t n_tokens, uint16_t* k, uint16_t* v, int hkv, int tpb, int d) {
-  const int i = blockIdx.x;
-  const int64_t b = first_block + i;
+  // Record of block i (src[i] >= 0: pool slot; < 0: host mirror record -src[i] - 1, read in
+  // place over the host link) into k, v [Hkv, n_tokens, D]. 16 bytes per load and store.
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  const int64_t b = blockIdx.x;
+  const int64_t si = src[b];
   const size_t rec = (size_t)2 * hkv * tpb * d;
-  const uint16_t* kr = src + (size_t)src_slot[i] * rec;
+  const uint16_t* kr = si >= 0 ? pool + (size_t)si * rec : host + (size_t)(-si - 1) * rec;
   const uint16_t* vr = kr + (size_t)hkv * tpb * d;
-  const int per = hkv * tpb * d;
-  for (int e = threadIdx.x; e < per; e += blockDim.x) {
-    const int h = e / (tpb * d);
-    const int r = e - h * tpb * d;
-    const int t = r / d, dd = r - t * d;
+  const int cpr = d / 8;
+  const int per = hkv * tpb * cpr;
+  for (int c = threadIdx.x; c < per; c += blockDim.x) {
+    const int h = c / (tpb * cpr);
+    const int r = c - h * tpb * cpr;
+    const int t = r / cpr, cc = r - t * cpr;
     const int64_t tok = b * tpb + t;
     if (tok < n_tokens) {
-      const size_t dst = ((size_t)h * n_tokens + tok) * d + dd;
-      k[dst] = kr[e];
-      v[dst] = vr[e];
+      const size_t o = (size_t)(h * tpb + t) * d + (size_t)cc * 8;
+      const size_t dst = ((size_t)h * n_tokens + tok) * d + (size_t)cc * 8;
+      *reinterpret_cast<u32x4*>(k + dst) = *reinterpret_cast<const u32x4*>(kr + o);
+      *reinterpret_cast<u32x4*>(v + dst) = *reinterpret_cast<const u32x4*>(vr + o);
     }
   }
 }
@@ -170,7 +175,9 @@ int PagedKV::init() {
       PGR_HIP(hipHostGetDevicePointer(&host_dev_[l], host_[l], 0));
     }
   }
-  PGR_HIP(hipMalloc(&stage_, rec * (size_t)cfg_.staging_slots * cfg_.staging_buffers));
+  // The staging ring exists for the staged stream mode only: in the direct mode the kernels
+  // and the copy kernels read and write the host mirror in place.
+  if (cfg_.stream_mode == 1) PGR_HIP(hipMalloc(&stage_, rec * (size_t)cfg_.staging_slots * cfg_.staging_buffers));
   PGR_HIP(hipStreamCreateWithFlags(&copy_stream_, hipStreamNonBlocking));
   buf_free_.resize(cfg_.staging_buffers);
   chunk_ready_.resize(cfg_.staging_buffers);
@@ -463,38 +470,27 @@ int PagedKV::export_tokens(int sid, int row, int layer, void* k, void* v, int64_
   if (row < 0 || row >= s.rows || layer < 0 || layer >= cfg_.num_layers) return fail(kErrInvalid, "row/layer out of range");
   if (n_tokens > s.n_tokens) return fail(kErrInvalid, "n_tokens exceeds the session length");
   if (in_step_) return fail(kErrState, "export during a decode step");
+  if (((uintptr_t)k | (uintptr_t)v) % 16 != 0) return fail(kErrInvalid, "k and v must be 16-byte aligned");
   const int64_t T = cfg_.tokens_per_block;
   const int64_t nb = (n_tokens + T - 1) / T;
-  const size_t rec = rec_bytes();
-  PGR_HIP(hipStreamSynchronize(stream));
+  if (nb == 0) return kOk;
+  // Evictions and loads queued on the copy stream may still be writing these records.
   PGR_HIP(hipStreamSynchronize(copy_stream_));
-  int32_t* d_slot = nullptr;
-  PGR_HIP(hipMalloc(&d_slot, sizeof(int32_t)));
-  int rc = kOk;
-  for (int64_t b = 0; b < nb && rc == kOk; ++b) {
-    int32_t sl = s.slot[b * s.rows + row];
-    const uint16_t* src = static_cast<const uint16_t*>(pool_[layer]);
-    if (sl < 0) {
-      const char* hsrc = static_cast<const char*>(host_[layer]) + (size_t)(s.row[row].host_off + b) * rec;
-      hipError_t e = hipMemcpyAsync(stage_, hsrc, rec, hipMemcpyHostToDevice, stream);
-      if (e != hipSuccess) {
-        rc = hip_fail(e, "hipMemcpyAsync(H2D export)");
-        break;
-      }
-      sl = 0;
-      src = static_cast<const uint16_t*>(stage_);
-    }
-    hipError_t e = hipMemcpyAsync(d_slot, &sl, sizeof(int32_t), hipMemcpyHostToDevice, stream);
-    if (e == hipSuccess) {
-      records_to_hf_kernel<<<1, 256, 0, stream>>>(src, d_slot, b, n_tokens, static_cast<uint16_t*>(k),
-                                                 static_cast<uint16_t*>(v), cfg_.kv_heads, (int)T, cfg_.head_dim);
-      e = hipGetLastError();
-    }
-    if (e == hipSuccess) e = hipStreamSynchronize(stream);
-    if (e != hipSuccess) rc = hip_fail(e, "export");
+  IndexBuf* ib = nullptr;
+  int rc = acquire_index_buf((size_t)nb, &ib);
+  if (rc != kOk) return rc;
+  for (int64_t b = 0; b < nb; ++b) {
+    const int32_t sl = s.slot[b * s.rows + row];
+    ib->host[b] = sl >= 0 ? (int64_t)sl : -(s.row[row].host_off + b) - 1;
   }
-  hipFree(d_slot);
-  return rc;
+  records_to_hf_kernel<<<(unsigned)nb, 256, 0, stream>>>(
+      ib->dev, static_cast<const uint16_t*>(pool_[layer]), static_cast<const uint16_t*>(host_dev_[layer]), n_tokens,
+      static_cast<uint16_t*>(k), static_cast<uint16_t*>(v), cfg_.kv_heads, (int)T, cfg_.head_dim);
+  PGR_HIP(hipGetLastError());
+  PGR_HIP(hipEventRecord(ib->done, stream));
+  ib->pending = true;
+  PGR_HIP(hipStreamSynchronize(stream));
+  return kOk;
 }
 
 int PagedKV::put_block(int sid, int64_t block_id, const void* key, const void* value, hipStream_t stream) {
@@ -544,37 +540,26 @@ int PagedKV::get_block(int sid, int64_t block_id, void* key, void* value, hipStr
   Session& s = sessions_[sid];
   const int64_t T = cfg_.tokens_per_block;
   if (block_id < 0 || block_id >= s.n_tokens / T) return fail(kErrKey, "block is not a registered full block");
-  const size_t rec = rec_bytes();
-  PGR_HIP(hipStreamSynchronize(stream));
+  // Evictions and loads queued on the copy stream may still be writing this block.
   PGR_HIP(hipStreamSynchronize(copy_stream_));
-  std::vector<int32_t> slots(s.rows);
   const bool on_gpu = s.on_gpu[block_id] != 0;
-  int32_t* d_slots = nullptr;
-  PGR_HIP(hipMalloc(&d_slots, sizeof(int32_t) * s.rows));
+  // Record index per row: pool slots, or host mirror records read in place.
+  IndexBuf* ib = nullptr;
+  int rc = acquire_index_buf((size_t)s.rows, &ib);
+  if (rc != kOk) return rc;
+  int32_t* slots = reinterpret_cast<int32_t*>(ib->host);
+  for (int r = 0; r < s.rows; ++r)
+    slots[r] = on_gpu ? s.slot[block_id * s.rows + r] : (int32_t)(s.row[r].host_off + block_id);
+  const int32_t* d_slots = reinterpret_cast<const int32_t*>(ib->dev);
   hipError_t e = hipSuccess;
   const size_t layer_elems = (size_t)s.rows * T * cfg_.kv_heads * cfg_.head_dim;
-  for (int l = 0; l < cfg_.num_layers && e == hipSuccess; ++l) {
-    const void* src = pool_[l];
-    for (int r = 0; r < s.rows; ++r) {
-      if (on_gpu) {
-        slots[r] = s.slot[block_id * s.rows + r];
-      } else {
-        slots[r] = r;
-        const char* h = static_cast<const char*>(host_[l]) + (size_t)(s.row[r].host_off + block_id) * rec;
-        if (e == hipSuccess)
-          e = hipMemcpyAsync(static_cast<char*>(stage_) + (size_t)r * rec, h, rec, hipMemcpyHostToDevice, stream);
-        src = stage_;
-      }
-    }
-    if (e == hipSuccess)
-      e = hipMemcpyAsync(d_slots, slots.data(), sizeof(int32_t) * s.rows, hipMemcpyHostToDevice, stream);
-    if (e == hipSuccess)
-      e = launch_records_to_ref(src, d_slots, static_cast<uint16_t*>(key) + l * layer_elems,
-                                static_cast<uint16_t*>(value) + l * layer_elems, s.rows, cfg_.kv_heads, (int)T,
-                                cfg_.head_dim, stream);
-    if (e == hipSuccess) e = hipStreamSynchronize(stream);
-  }
-  hipFree(d_slots);
+  for (int l = 0; l < cfg_.num_layers && e == hipSuccess; ++l)
+    e = launch_records_to_ref(on_gpu ? pool_[l] : host_dev_[l], d_slots, static_cast<uint16_t*>(key) + l * layer_elems,
+                              static_cast<uint16_t*>(value) + l * layer_elems, s.rows, cfg_.kv_heads, (int)T,
+                              cfg_.head_dim, stream);
+  if (e == hipSuccess) e = hipEventRecord(ib->done, stream);
+  ib->pending = true;
+  if (e == hipSuccess) e = hipStreamSynchronize(stream);
   if (e != hipSuccess) return hip_fail(e, "get_block");
   return kOk;
 }

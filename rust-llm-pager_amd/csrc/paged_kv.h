@@ -9,10 +9,11 @@
 //     row owning a contiguous range [host_off, host_off + capacity_blocks). Host-resident
 //     blocks with consecutive ids are therefore one contiguous run, and are streamed to the
 //     GPU with one multi-MiB copy per run.
-//   * Staging ring in HBM: `staging_buffers` buffers of `staging_slots` records. In the staged
-//     stream mode, filled by host-to-device copies on a side stream and read by the attention
-//     kernel in place; in the direct mode (default) the kernel reads host blocks straight from
-//     the mirror over the host link and the ring only bounces imports/exports.
+//   * Staging ring in HBM (staged stream mode only): `staging_buffers` buffers of
+//     `staging_slots` records, filled by host-to-device copies on a side stream and read by
+//     the attention kernel in place. In the direct mode (default) the attention kernel reads
+//     host blocks straight from the mirror over the host link, and imports, exports and tier
+//     moves read and write the mirror in place through its device mapping.
 // Blocks are immutable once full, so a host copy stays valid after the block is loaded back
 // to HBM and a later eviction of it needs no copy.
 #pragma once
