@@ -660,8 +660,9 @@ int PagedKV::apply_tiers(int sid, const uint8_t* tiers, int64_t n_tiers, int64_t
     std::vector<int64_t>& pairs = dir == 0 ? evict_pairs_ : load_pairs_;
     if (pairs.empty()) continue;
     PendingTiming t{nullptr, nullptr, dir};  // bytes field tags the direction: 0 to host, 1 to GPU
-    hipEventCreate(&t.start);
-    hipEventCreate(&t.stop);
+    // Timing-only events: no system-scope fence (cache writeback and invalidate) at record.
+    hipEventCreateWithFlags(&t.start, hipEventDisableSystemFence);
+    hipEventCreateWithFlags(&t.stop, hipEventDisableSystemFence);
     hipEventRecord(t.start, copy_stream_);
     const int l = cfg_.num_layers;
     const int crc = dir == 0 ? launch_copies(pairs, 0, l, copy_stream_) : launch_copies(pairs, l, 0, copy_stream_);
@@ -993,8 +994,10 @@ int PagedKV::decode_layer(int layer, const void* q, const void* k_new, const voi
     PendingTiming t{nullptr, nullptr, 0};
     pl.ev_start = pl.ev_stop = nullptr;
     if (timing_) {
-      PGR_HIP(hipEventCreate(&t.start));
-      PGR_HIP(hipEventCreate(&t.stop));
+      // Timing-only events: without a system-scope fence at record time they do not write
+      // back and invalidate the caches around the launch they stamp.
+      PGR_HIP(hipEventCreateWithFlags(&t.start, hipEventDisableSystemFence));
+      PGR_HIP(hipEventCreateWithFlags(&t.stop, hipEventDisableSystemFence));
       pl.ev_start = t.start;
       pl.ev_stop = t.stop;
     }
