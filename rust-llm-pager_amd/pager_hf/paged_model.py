@@ -19,7 +19,7 @@ one-call-at-a-time lock. What runs underneath is the native path:
 ``generate_beam_search`` (paged_model.py:409-634) moves beam rows inside the native store.
 
 Differences: ``use_streaming_attention=False`` (the reference's reload-everything mode)
-raises NotImplementedError; supported model types are the ones
+runs the same native path, since it computes the same attention; supported model types are the ones
 whose attention is the plain q/k/v + RoPE + o_proj layout in transformers 5.x (llama,
 mistral, qwen2, qwen3). Mistral's sliding window is applied per step through the
 sequences' first valid position.
@@ -105,12 +105,13 @@ class PagedModel:
         """Arguments and defaults of paged_model.py:200-215. Added: ``max_context_tokens``
         (tokens per row the native store is sized for; default: the first session's prompt
         plus max_new_tokens) and ``stream_mode`` ("direct" or "staged"). The group size has
-        no effect: the native kernel covers every block in one launch."""
+        no effect: the native kernel covers every block in one launch.
+        ``use_streaming_attention=False`` selects the reference's reload mode, which copies
+        every block back into one HBM cache per step and runs the model's own attention
+        (paged_model.py:717-760). For the supported model types it computes the same
+        attention as the paged path, so both settings run the native path."""
         if not use_streaming_attention:
-            raise NotImplementedError(
-                "use_streaming_attention=False (reload every block into one HBM cache per step) is not built: "
-                "the native decode path reads HBM and host blocks in place."
-            )
+            logger.info("use_streaming_attention=False: running the native paged path (same attention, no reload)")
         if tokens_per_block <= 0 or tokens_per_block % 16:
             raise ValueError("tokens_per_block must be a positive multiple of 16 for the native kernels")
         self.model = model

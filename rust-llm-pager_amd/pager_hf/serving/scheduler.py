@@ -116,13 +116,12 @@ class ContinuousBatchingScheduler:
         request or session holds), ``host_token_capacity`` (pinned host tokens over all
         sessions), ``stream_mode`` / ``staging_blocks`` / ``staging_buffers`` (host block
         streaming of the engine) and ``engine`` (an existing BatchedPagedEngine to serve
-        from). ``use_streaming_attention=False`` is not built; the group size has no effect."""
+        from). ``use_streaming_attention=False`` runs the same native path (see PagedModel);
+        the group size has no effect."""
         if max_concurrent_sessions < 1:
             raise ValueError(f"max_concurrent_sessions must be >= 1, got {max_concurrent_sessions}")
         if max_queue_depth < 0:
             raise ValueError(f"max_queue_depth must be >= 0, got {max_queue_depth}")
-        if not use_streaming_attention:
-            raise NotImplementedError("use_streaming_attention=False is not built (see PagedModel)")
         self._model = model
         self._tokenizer = tokenizer
         self._max_concurrent_sessions = max_concurrent_sessions

@@ -91,6 +91,16 @@ def test_rejects_invalid_arguments():
                                     max_queue_depth=-1)
 
 
+def test_reload_mode_flag_is_accepted():
+    eng = FakeEngine([[5]])
+    sched = ContinuousBatchingScheduler(object(), SimpleNamespace(eos_token_id=EOS), max_concurrent_sessions=1,
+                                        total_vram_budget=1, total_ram_budget=1, use_streaming_attention=False,
+                                        engine=eng)
+    req = sched.submit(*prompt(), max_new_tokens=1)
+    drive(sched, 2)
+    assert req.generated_tokens == [5]
+
+
 def test_admission_respects_max_concurrent_sessions():
     sched, eng = make([[5, 6, 7]] * 3, max_concurrent=2)
     reqs = [sched.submit(*prompt(), max_new_tokens=3) for _ in range(3)]
