@@ -21,8 +21,9 @@ one-call-at-a-time lock. What runs underneath is the native path:
 Differences: ``use_streaming_attention=False`` (the reference's reload-everything mode)
 runs the same native path, since it computes the same attention; supported model types are the ones
 whose attention is the plain q/k/v + RoPE + o_proj layout in transformers 5.x (llama,
-mistral, qwen2, qwen3). Mistral's sliding window is applied per step through the
-sequences' first valid position.
+mistral, qwen2, qwen2_moe, qwen3, starcoder2). Mistral's and Starcoder2's sliding window
+is applied per step through the sequences' first valid position. The Gemma family is not
+supported (head_dim 256, and Gemma2's per-layer windows).
 """
 from __future__ import annotations
 
@@ -41,7 +42,9 @@ logger = logging.getLogger(__name__)
 
 _ATTN_IMPL = "pgr_paged_decode"
 _POLICIES_WITHOUT_ATTENTION_SIGNAL = frozenset({"recent_only", "sinks_recent"})  # paged_model.py:40
-_SUPPORTED_MODEL_TYPES = frozenset({"llama", "mistral", "qwen2", "qwen3"})
+_SUPPORTED_MODEL_TYPES = frozenset({"llama", "mistral", "qwen2", "qwen2_moe", "qwen3", "starcoder2"})
+# Model types whose every layer attends within config.sliding_window (when set).
+_WINDOWED_MODEL_TYPES = frozenset({"mistral", "starcoder2"})
 
 
 def _paged_attention(module, query, key, value, attention_mask, scaling=None, dropout=0.0, **kwargs):
@@ -395,7 +398,7 @@ class PagedModel:
         num_heads = cfg.num_attention_heads
         num_kv = getattr(cfg, "num_key_value_heads", None) or num_heads
         head_dim = getattr(cfg, "head_dim", None) or cfg.hidden_size // num_heads
-        window = getattr(cfg, "sliding_window", None) if model_type == "mistral" else None
+        window = getattr(cfg, "sliding_window", None) if model_type in _WINDOWED_MODEL_TYPES else None
         return cfg.num_hidden_layers, num_heads, num_kv, head_dim, window
 
     def _start_session(self, input_ids: torch.Tensor, attention_mask: torch.Tensor, max_new_tokens: int) -> None:

@@ -165,3 +165,52 @@ def test_config3_tinyllama_8192_prompt_256_tokens():
     st = pm.last_run_stats
     assert st.final_num_blocks == (8192 + 256 - 1) // 32
     assert st.total_cpu_to_gpu_mb > 0
+
+
+def _family_model(family):
+    import transformers as tr
+
+    common = dict(hidden_size=512, intermediate_size=1024, num_hidden_layers=3, num_attention_heads=8,
+                  num_key_value_heads=2, vocab_size=2048, max_position_embeddings=4096, initializer_range=0.05,
+                  bos_token_id=1, eos_token_id=2)
+    if family == "qwen2_moe":
+        cfg = tr.Qwen2MoeConfig(moe_intermediate_size=256, shared_expert_intermediate_size=512, num_experts=4,
+                                num_experts_per_tok=2, **common)
+        cls = tr.Qwen2MoeForCausalLM
+    else:
+        cfg = tr.Starcoder2Config(sliding_window=96, **common)  # every layer windowed
+        cls = tr.Starcoder2ForCausalLM
+    torch.manual_seed(41)
+    return cls(cfg).to(dtype=torch.float16, device="cuda").eval()
+
+
+@pytest.mark.parametrize("family", ["qwen2_moe", "starcoder2"])
+def test_other_model_families_greedy_match_unpaged(family):
+    """Qwen2-MoE and Starcoder2 (sliding window 96) through the same attention entry."""
+    from pager_hf import PagedModel
+
+    model = _family_model(family)
+    g = torch.Generator().manual_seed(42)
+    ids = torch.randint(3, 2048, (1, 400), generator=g).cuda()
+    mask = torch.ones_like(ids)
+    want, logits, gaps = _baseline(model, ids, mask, 32)
+    pm = PagedModel(model, vram_budget=4 * MIB16, ram_budget=1 << 40, recent_window=2, policy="sinks_heavy_hitter",
+                    tokens_per_block=16)
+    assert _teacher_forced(pm, ids, mask, want, logits, gaps) < LOGIT_TOL
+    got = pm.generate(ids, mask, 32)
+    _check_free_running([got], want, gaps)
+    assert pm.last_run_stats.total_cpu_to_gpu_mb > 0
+
+
+def test_reload_mode_flag_gives_the_same_tokens():
+    """use_streaming_attention=False (the reference's reload mode) computes the same attention."""
+    from pager_hf import PagedModel
+
+    model = _model(SMALL, seed=15, init_std=0.05)
+    g = torch.Generator().manual_seed(16)
+    ids = torch.randint(0, SMALL["vocab_size"], (1, 250), generator=g).cuda()
+    mask = torch.ones_like(ids)
+    kw = dict(vram_budget=3 * MIB16, ram_budget=1 << 40, recent_window=2, tokens_per_block=16)
+    a = PagedModel(model, **kw).generate(ids, mask, 16)
+    b = PagedModel(model, use_streaming_attention=False, **kw).generate(ids, mask, 16)
+    assert a == b
