@@ -35,7 +35,7 @@ extern "C" {
 
 /* ---- library ------------------------------------------------------------------------- */
 
-/* ABI version of this header (increments on incompatible change). */
+/* ABI version of this header (increments when an entry point is added or changed); 3. */
 int pgr_abi_version(void);
 /* Message of the last failing call on this thread ("" if none). */
 const char* pgr_last_error(void);

@@ -33,7 +33,7 @@ MODE_FOLD_FIXED = 3
 STREAM_DIRECT = 0
 STREAM_STAGED = 1
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 c_i32, c_i64, c_u8, c_u32, c_u64 = ctypes.c_int32, ctypes.c_int64, ctypes.c_uint8, ctypes.c_uint32, ctypes.c_uint64
 c_f32, c_f64, c_size, c_vp = ctypes.c_float, ctypes.c_double, ctypes.c_size_t, ctypes.c_void_p
@@ -186,12 +186,15 @@ def load() -> ctypes.CDLL:
                 "(or __graft_entry__.build())"
             )
         lib = ctypes.CDLL(LIB_PATH)
+        lib.pgr_abi_version.restype = ctypes.c_int
+        lib.pgr_abi_version.argtypes = []
+        if lib.pgr_abi_version() != ABI_VERSION:  # before any other symbol: a stale build fails here
+            raise ImportError(f"libpgr.so ABI {lib.pgr_abi_version()} does not match the bindings ({ABI_VERSION}); "
+                              "rebuild it")
         for name, (restype, argtypes) in SIGNATURES.items():
             fn = getattr(lib, name)
             fn.restype = restype
             fn.argtypes = argtypes
-        if lib.pgr_abi_version() != ABI_VERSION:
-            raise ImportError(f"libpgr.so ABI {lib.pgr_abi_version()} does not match the bindings ({ABI_VERSION})")
         _lib = lib
         return lib
 

@@ -125,7 +125,7 @@ int kv_rc(pgr::PagedKV* kv, int rc) {
 
 extern "C" {
 
-int pgr_abi_version(void) { return 2; }
+int pgr_abi_version(void) { return 3; }
 
 const char* pgr_last_error(void) { return g_last_error.c_str(); }
 
