@@ -296,6 +296,175 @@ def register(args):
     }
 
 
+def _cpu_attention_rate(groups, n_rep, d, budget_s):
+    """Dense fp32 attention plus block mass in torch on the host threads over (k, v) groups
+    ([Hkv, n, D] fp16/bf16 each, upcast included); returns (seconds per pass, threads)."""
+    import os
+
+    import torch
+
+    threads = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
+    previous = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        gen = torch.Generator().manual_seed(1)
+        qs = [(torch.randn(k.shape[0], n_rep, d, generator=gen) * 0.5).to(k.dtype) for k, _ in groups]
+        passes = 0
+        t0 = time.perf_counter()
+        while True:
+            for q, (k, v) in zip(qs, groups):
+                n = k.shape[1]
+                w = torch.softmax((q.float() @ k.float().transpose(1, 2)) / d ** 0.5, dim=-1)
+                _ = w @ v.float()
+                nb = -(-n // 32)
+                _ = torch.nn.functional.pad(w, (0, nb * 32 - n)).view(k.shape[0], n_rep, nb, 32).sum(-1)
+            passes += 1
+            if time.perf_counter() - t0 > budget_s:
+                break
+        return (time.perf_counter() - t0) / passes, threads
+    finally:
+        torch.set_num_threads(previous)
+
+
+def configs(args):
+    """Configurations 1, 3 and 4 measured the way configurations 2 and 5 are, each with the
+    reference's CPU path (dense fp32 attention and block mass in torch on the host threads)
+    timed on the same in-scope K/V.
+
+    1: one Qwen2.5-0.5B layer (14q/2kv, D 64, fp16), batch 1, 4096 tokens in 32-token blocks,
+       the 8 most recent blocks in HBM and 120 on host, 128 steps.
+    3: TinyLlama-1.1B architecture (22 layers, 32q/4kv, D 64, fp16, random init), 8192 prompt
+       tokens, 256 greedy tokens, sinks_heavy_hitter with a 41-block budget and 8 recent
+       blocks; decode only (the prompt is registered by a first call).
+    4: one Mistral-7B layer (32q/8kv, D 128, bf16), batch 4, 131072 tokens, window 4096:
+       32 in-window blocks in HBM and 96 on host, 32 steps."""
+    import torch
+
+    from pager_hf import PagedDecoder, PagedModel
+
+    rows = {}
+
+    def layer_run(name, *, hq, hkv, d, dtype, batch, ctx, resident, window, steps, warmup):
+        T = 32
+        nb = ctx // T
+        dec = PagedDecoder(num_layers=1, num_query_heads=hq, num_kv_heads=hkv, head_dim=d, tokens_per_block=T,
+                           dtype=dtype, device="cuda", pool_blocks=batch * (resident + 8),
+                           host_blocks=batch * (nb + 8), staging_blocks=64, staging_buffers=2)
+        g = torch.Generator(device="cuda").manual_seed(ctx)
+        sids, cpu_groups = [], []
+        for _ in range(batch):
+            sid = dec.add_session(capacity_tokens=ctx + steps + warmup + 64, vram_budget=resident * MIB16,
+                                  ram_budget=1 << 42, recent_window=resident - 1, policy="recent_only")
+            k = (torch.randn(1, hkv, ctx, d, device="cuda", generator=g) * 0.5).to(dtype)
+            v = (torch.randn(1, hkv, ctx, d, device="cuda", generator=g) * 0.5).to(dtype)
+            dec.prefill(sid, [k], [v], ctx)
+            lo = ctx - (window or ctx)
+            cpu_groups.append((k[0, :, lo:].cpu(), v[0, :, lo:].cpu()))
+            del k, v
+            sids.append(sid)
+        q = (torch.randn(batch, hq, d, device="cuda", generator=g) * 0.5).to(dtype)
+        kn = (torch.randn(batch, hkv, d, device="cuda", generator=g) * 0.5).to(dtype)
+        host = res_tok = 0
+
+        def one(i):
+            nonlocal host, res_tok
+            if window:
+                for sid in sids:
+                    dec.set_lo(sid, [ctx + i - window + 1])
+            dec.begin_step(sids)
+            st = dec.pool.step_stats()
+            dec.decode_layer(0, q, kn, kn)
+            dec.end_step(collect=False)
+            return st
+
+        for i in range(warmup):
+            one(i)
+        torch.cuda.synchronize()
+        dec.pool.sync()
+        t0 = time.perf_counter()
+        for i in range(warmup, warmup + steps):
+            st = one(i)
+            host += st["host_tokens"]
+            res_tok += st["resident_tokens"]
+        torch.cuda.synchronize()
+        dec.pool.sync()
+        dt = (time.perf_counter() - t0) / steps
+        dec.pool.close()
+        tok_bytes = 2 * hkv * d * 2
+        host_b, hbm_b = host / steps * tok_bytes, res_tok / steps * tok_bytes
+        cpu_s, threads = _cpu_attention_rate(cpu_groups, hq // hkv, d, args.cpu_seconds / 3)
+        cpu_bytes = sum(k.numel() * 2 * 2 for k, _ in cpu_groups)
+        rows[name] = {
+            "ms_per_step": round(dt * 1e3, 4),
+            "tokens_per_s": round(batch / dt, 1),
+            "kv_GBs": round((host_b + hbm_b) / dt / 1e9, 2),
+            "host_link": {"bytes_per_step": int(host_b), "GBs": round(host_b / dt / 1e9, 2),
+                          "frac_of_64": round(host_b / dt / 1e9 / LINK_PEAK_GBS, 4)},
+            "hbm": {"bytes_per_step": int(hbm_b), "GBs": round(hbm_b / dt / 1e9, 2)},
+            "cpu_baseline": {"kv_GBs": round(cpu_bytes / cpu_s / 1e9, 3), "tokens_per_s": round(batch / cpu_s, 1),
+                             "cores": threads, "kind": "port"},
+        }
+
+    layer_run("1", hq=14, hkv=2, d=64, dtype=torch.float16, batch=1, ctx=4096, resident=8, window=None, steps=128,
+              warmup=8)
+    layer_run("4", hq=32, hkv=8, d=128, dtype=torch.bfloat16, batch=4, ctx=131072, resident=32, window=4096,
+              steps=32, warmup=4)
+
+    # Configuration 3: the whole model through PagedModel.
+    from transformers import LlamaConfig, LlamaForCausalLM
+
+    cfg = LlamaConfig(hidden_size=2048, intermediate_size=5632, num_hidden_layers=22, num_attention_heads=32,
+                      num_key_value_heads=4, vocab_size=32000, max_position_embeddings=8448 + 64, rms_norm_eps=1e-5)
+    torch.manual_seed(7)
+    with torch.device("cuda"):
+        model = LlamaForCausalLM(cfg)
+    model = model.to(torch.float16).eval()
+    g = torch.Generator().manual_seed(8)
+    ids = torch.randint(0, 32000, (1, 8192), generator=g).cuda()
+    pm = PagedModel(model, vram_budget=41 * MIB16, ram_budget=1 << 40, recent_window=8,
+                    policy="sinks_heavy_hitter", tokens_per_block=32, max_context_tokens=8192 + 512)
+    first = pm.generate(ids, torch.ones_like(ids), 1)
+    ids2 = torch.cat([ids, torch.tensor([first], device="cuda")], dim=1)
+    n_new = 256
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    pm.generate(ids2, torch.ones_like(ids2), n_new)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / n_new
+    st = pm.last_run_stats
+    host_b = st.total_cpu_to_gpu_mb * 1e6 / n_new
+    kv_tok = 2 * 4 * 64 * 2 * 22
+    in_scope = 8192 + n_new // 2
+    pm.reset()
+    del model
+    torch.cuda.empty_cache()
+    # CPU: the attention of one decode step over all 22 layers at the mean context.
+    gen = torch.Generator().manual_seed(9)
+    groups = [((torch.randn(4, in_scope, 64, generator=gen) * 0.5).half(),
+               (torch.randn(4, in_scope, 64, generator=gen) * 0.5).half()) for _ in range(22)]
+    cpu_s, threads = _cpu_attention_rate(groups, 8, 64, args.cpu_seconds / 3)
+    rows["3"] = {
+        "ms_per_token": round(dt * 1e3, 3),
+        "tokens_per_s": round(1 / dt, 1),
+        "kv_GBs": round(in_scope * kv_tok / dt / 1e9, 2),
+        "host_link": {"bytes_per_token": int(host_b), "GBs": round(host_b / dt / 1e9, 2),
+                      "frac_of_64": round(host_b / dt / 1e9 / LINK_PEAK_GBS, 4)},
+        "mean_attention_in_gpu": round(st.mean_attention_in_gpu, 4),
+        "cpu_baseline": {"kv_GBs": round(in_scope * kv_tok / cpu_s / 1e9, 3), "tokens_per_s": round(1 / cpu_s, 1),
+                         "cores": threads, "kind": "port", "note": "attention of all 22 layers only"},
+    }
+    return {
+        "metric": "per-configuration decode-attention measurements (configurations 1, 3, 4)",
+        "value": rows["4"]["kv_GBs"],
+        "unit": "GB/s",
+        "higher_is_better": True,
+        "configs": rows,
+        "dtype": "fp16 (1, 3), bf16 (4)",
+        "data": "synthetic K/V and random-init weights",
+        "config": {"workload": "configurations 1, 3 and 4 as specified; value is configuration 4's K/V GB/s"},
+    }
+
+
 class SimpleTokenizer:
     eos_token_id = None
 
@@ -365,9 +534,9 @@ def main() -> int:
                     help="host blocks read in place over the host link, or copied into a staging ring")
     ap.add_argument("--resident-layers", type=int, default=24,
                     help="layers of the all-resident HBM measurement (0 skips it)")
-    ap.add_argument("--workload", choices=["batch8", "continuous", "register"], default="batch8",
+    ap.add_argument("--workload", choices=["batch8", "continuous", "register", "configs"], default="batch8",
                     help="batch8: the headline line; continuous: the 64-request continuous-batching run; "
-                         "register: prompt registration at 8k-64k tokens")
+                         "register: prompt registration at 8k-64k tokens; configs: configurations 1, 3, 4")
     ap.add_argument("--register-reps", type=int, default=3)
     ap.add_argument("--cb-rounds", type=int, default=24)
     ap.add_argument("--cb-extra-requests", type=int, default=64)
@@ -387,6 +556,11 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a HIP device", file=sys.stderr)
         return 2
+    if args.workload == "configs":
+        line = configs(args)
+        line.update({"n_gpus": 1, "steps": None, "warmup": None, "scaling": "weak", "vs_baseline": None})
+        print(json.dumps(line), flush=True)
+        return 0
     if args.workload == "register":
         line = register(args)
         line.update({"n_gpus": 1, "steps": args.register_reps, "warmup": 0, "scaling": "weak", "vs_baseline": None})

@@ -792,27 +792,46 @@ __global__ __launch_bounds__(256) void paged_merge_kernel(PagedArgs a) {
 // Per (session, block): mean over the session's rows and all query heads of
 // s_b * 2^(m_b - m_final) / l_final (log2 units), added into the session's mass accumulator
 // (paged_model.py:1041-1048 per layer).
-__global__ void mass_reduce_kernel(const SeqInfo* seqs, const int32_t* session_rows, const int32_t* session_first,
-                                   const float* mass_m, const float* mass_s, const float* mf, const float* lf,
-                                   float* mass_accum, int accum_stride, int hq, int mass_stride, int n_sessions,
-                                   int max_blocks) {
+// Per-block attention mass of each session, averaged over its rows and query heads and added
+// to mass_accum (one layer's share). Block b of row r, head h contributes
+// s_b * 2^(m_b - m_final) / l_final. Workgroup: 64 blocks x 4 head groups; each thread sums
+// its heads h = g, g + 4, ... (loads unrolled so they overlap), then the four groups are
+// added through LDS in a fixed order, so the result does not depend on scheduling.
+constexpr int kMassBlocksPerWG = 64;
+constexpr int kMassHeadGroups = 4;
+
+__global__ __launch_bounds__(256) void mass_reduce_kernel(const SeqInfo* seqs, const int32_t* session_rows,
+                                                          const int32_t* session_first, const float* mass_m,
+                                                          const float* mass_s, const float* mf, const float* lf,
+                                                          float* mass_accum, int accum_stride, int hq, int mass_stride,
+                                                          int n_sessions, int max_blocks) {
+  __shared__ float part[kMassHeadGroups][kMassBlocksPerWG];
   const int sess = blockIdx.y;
-  const int blk = blockIdx.x * blockDim.x + threadIdx.x;
-  if (sess >= n_sessions) return;
+  const int bl = threadIdx.x % kMassBlocksPerWG, hg = threadIdx.x / kMassBlocksPerWG;
+  const int blk = blockIdx.x * kMassBlocksPerWG + bl;
   const int first = session_first[sess], rows = session_rows[sess];
-  const SeqInfo si0 = seqs[first];
-  if (blk >= si0.n_mass || blk >= max_blocks) return;
+  const int n_mass = seqs[first].n_mass;
+  const bool live = blk < n_mass && blk < max_blocks;
   float total = 0.f;
-  for (int r = 0; r < rows; ++r) {
-    const SeqInfo si = seqs[first + r];
-    if (blk < si.mass_lo) continue;  // out of scope for this row: mass 0
-    for (int qh = 0; qh < hq; ++qh) {
-      const size_t row = (size_t)(first + r) * hq + qh;
-      const size_t mi = row * mass_stride + blk;
-      if (lf[row] > 0.f) total += mass_s[mi] * __builtin_amdgcn_exp2f(mass_m[mi] - mf[row]) / lf[row];
+  if (live) {
+    for (int r = 0; r < rows; ++r) {
+      if (blk < seqs[first + r].mass_lo) continue;  // out of scope for this row: mass 0
+      const size_t row0 = (size_t)(first + r) * hq;
+#pragma unroll 4
+      for (int qh = hg; qh < hq; qh += kMassHeadGroups) {
+        const size_t row = row0 + qh;
+        const float l = lf[row];
+        const size_t mi = row * mass_stride + blk;
+        if (l > 0.f) total += mass_s[mi] * __builtin_amdgcn_exp2f(mass_m[mi] - mf[row]) / l;
+      }
     }
   }
-  mass_accum[(size_t)sess * accum_stride + blk] += total / (float)(rows * hq);
+  part[hg][bl] = total;
+  __syncthreads();
+  if (hg == 0 && live) {
+    const float sum = ((part[0][bl] + part[1][bl]) + part[2][bl]) + part[3][bl];
+    mass_accum[(size_t)sess * accum_stride + blk] += sum / (float)(rows * hq);
+  }
 }
 
 template <class Ty, int D>
@@ -1027,7 +1046,7 @@ hipError_t launch_mass_reduce(const SeqInfo* seqs, const int32_t* session_rows, 
                               float* mass_accum, int accum_stride, int hq, int mass_stride, int n_sessions,
                               int max_blocks, hipStream_t stream) {
   if (n_sessions == 0 || max_blocks == 0) return hipSuccess;
-  dim3 grid((max_blocks + 255) / 256, n_sessions);
+  dim3 grid((max_blocks + kMassBlocksPerWG - 1) / kMassBlocksPerWG, n_sessions);
   mass_reduce_kernel<<<grid, 256, 0, stream>>>(seqs, session_rows, session_first, mass_m, mass_s, mf, lf, mass_accum,
                                                accum_stride, hq, mass_stride, n_sessions, max_blocks);
   return hipGetLastError();
