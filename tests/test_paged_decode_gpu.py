@@ -31,14 +31,15 @@ class Pair:
     """A PagedDecoder and the oracle driven with the same inputs."""
 
     def __init__(self, *, layers, hq, hkv, d, tpb, dtype, pool_blocks, host_blocks, staging_blocks=1024,
-                 blocks_per_workgroup=16, stream_mode="direct"):
+                 blocks_per_workgroup=16, stream_mode="direct", scale=None, softcap=None):
         self.dtype = dtype
         self.dec = PagedDecoder(num_layers=layers, num_query_heads=hq, num_kv_heads=hkv, head_dim=d,
                                 tokens_per_block=tpb, dtype=dtype, device="cuda", pool_blocks=pool_blocks,
                                 host_blocks=host_blocks, staging_blocks=staging_blocks,
-                                blocks_per_workgroup=blocks_per_workgroup, stream_mode=stream_mode)
+                                blocks_per_workgroup=blocks_per_workgroup, stream_mode=stream_mode, scale=scale,
+                                softcap=softcap)
         self.ora = PagedDecodeOracle(num_layers=layers, num_query_heads=hq, num_kv_heads=hkv, head_dim=d,
-                                     tokens_per_block=tpb)
+                                     tokens_per_block=tpb, scale=scale, softcap=softcap)
         self.layers, self.hq, self.hkv, self.d, self.tpb = layers, hq, hkv, d, tpb
         self.sids = []
 
@@ -200,3 +201,36 @@ def test_first_token_of_an_empty_session():
     for _ in range(40):
         p.step(g)
     assert p.dec.num_tokens(sid) == 40 and p.dec.num_blocks(sid) == 1
+
+
+# Geometry grid: head dims 32/64/128, n_rep 1/7/16, 16/32/64-token blocks (1, 2 and 4 tiles
+# per block), both dtypes, a non-default scale and a softcap, and a scoring policy so the
+# per-block mass is checked as well. Each case crosses a block boundary.
+GRID = [
+    # hq, hkv, d, tpb, dtype, scale, softcap, policy, mode
+    (4, 4, 32, 16, torch.float16, None, None, "sinks_heavy_hitter", "direct"),
+    (14, 2, 64, 64, torch.bfloat16, None, None, "heavy_hitter", "direct"),
+    (32, 2, 128, 32, torch.bfloat16, 0.07, 30.0, "sinks_heavy_hitter", "staged"),
+    (16, 1, 64, 16, torch.float16, None, 50.0, "recent_only", "staged"),
+    (8, 8, 128, 64, torch.float16, None, None, "sinks_recent", "direct"),
+]
+
+
+@pytest.mark.parametrize("hq,hkv,d,tpb,dtype,scale,softcap,policy,mode", GRID)
+def test_geometry_grid(hq, hkv, d, tpb, dtype, scale, softcap, policy, mode):
+    g = torch.Generator().manual_seed(hq * 131 + d + tpb)
+    p = Pair(layers=2, hq=hq, hkv=hkv, d=d, tpb=tpb, dtype=dtype, pool_blocks=96, host_blocks=256,
+             stream_mode=mode, scale=scale, softcap=softcap, staging_blocks=64)
+    ctx = 13 * tpb + 5
+    sid = p.add(ctx=ctx, rows=2, capacity=ctx + 3 * tpb, gen=g, vram_budget=5 * MIB16, ram_budget=512 * MIB16,
+                recent_window=2, rebalance_interval=2, policy=policy, lo=[0, tpb + 3])
+    errs = []
+    for _ in range(tpb + 4):  # crosses the next block boundary
+        res, ref, err = p.step(g)
+        errs.append(err)
+    assert max(errs) < TOL
+    if policy not in ("recent_only", "sinks_recent"):
+        got = np.array(res[sid]["block_attention"])
+        want = np.array(ref["placement"][sid]["scores"])
+        assert np.abs(got - want).max() < 2e-5
+    assert p.dec.pool.step_stats()["host_blocks"] > 0
