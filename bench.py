@@ -465,6 +465,78 @@ def configs(args):
     }
 
 
+def hbm_scale(args):
+    """The all-resident attention kernel as the bytes per launch grow: Qwen2.5-0.5B geometry
+    (14q/2kv, D 64, fp16) at batch 8, 16, 32 and 64 with contexts U[1024, 32768], and a
+    Mistral-7B layer (32q/8kv, D 128, bf16) at batch 4 x 32768 tokens. Every block resident,
+    several layers so the K/V read per step exceeds the MALL; event-timed launches."""
+    import torch
+
+    from pager_hf import PagedDecoder
+
+    T = 32
+    out = []
+
+    def measure(name, hq, hkv, d, dtype, ctxs, layers, steps=8, warmup=2):
+        nb = [c // T + 2 for c in ctxs]
+        dec = PagedDecoder(num_layers=layers, num_query_heads=hq, num_kv_heads=hkv, head_dim=d, tokens_per_block=T,
+                           dtype=dtype, device="cuda", pool_blocks=sum(nb) + 16 * len(ctxs),
+                           host_blocks=sum(nb) + 16 * len(ctxs), staging_blocks=16)
+        g = torch.Generator(device="cuda").manual_seed(len(ctxs))
+        sids = []
+        for c, n in zip(ctxs, nb):
+            sid = dec.add_session(capacity_tokens=c + 64, vram_budget=(n + 8) * MIB16, ram_budget=1 << 40,
+                                  recent_window=n + 4, policy="recent_only")
+            ks = [(torch.randn(1, hkv, c, d, device="cuda", generator=g) * 0.5).to(dtype) for _ in range(layers)]
+            vs = [(torch.randn(1, hkv, c, d, device="cuda", generator=g) * 0.5).to(dtype) for _ in range(layers)]
+            dec.prefill(sid, ks, vs, c, place=False)
+            del ks, vs
+            sids.append(sid)
+        S = len(ctxs)
+        q = (torch.randn(S, hq, d, device="cuda", generator=g) * 0.5).to(dtype)
+        kn = (torch.randn(S, hkv, d, device="cuda", generator=g) * 0.5).to(dtype)
+
+        def run(n):
+            for _ in range(n):
+                dec.begin_step(sids)
+                for layer in range(layers):
+                    dec.decode_layer(layer, q, kn, kn)
+                dec.end_step(collect=False)
+
+        run(warmup)
+        torch.cuda.synchronize()
+        dec.pool.sync()
+        dec.pool.kernel_time()
+        dec.pool.set_timing(True)
+        run(steps)
+        torch.cuda.synchronize()
+        dec.pool.sync()
+        ms, n, by = dec.pool.kernel_time()
+        dec.pool.close()
+        us = ms * 1e3 / n
+        out.append({"workload": name, "bytes_per_launch": by // n, "avg_launch_us": round(us, 2),
+                    "achieved": round(by / n / us / 1e3, 1), "frac": round(by / n / us / 1e3 / HBM_PEAK_GBS, 4)})
+
+    for batch in (8, 16, 32, 64):
+        ctxs = draw_contexts(CFG["seed"], batch, CFG["ctx_lo"], CFG["ctx_hi"])
+        layers = max(2, int(1.6e9 // (sum(ctxs) * 512)))  # > 1.5 GB per step: past the MALL
+        measure(f"0.5B layer, batch {batch}, contexts U[1024,32768], {layers} layers", 14, 2, 64, torch.float16,
+                ctxs, layers)
+    measure("Mistral-7B layer (32q/8kv, D 128, bf16), batch 4 x 32768, 4 layers", 32, 8, 128, torch.bfloat16,
+            [32768] * 4, 4)
+    return {
+        "metric": "all-resident paged attention HBM GB/s against bytes per launch",
+        "value": out[-1]["achieved"],
+        "unit": "GB/s",
+        "higher_is_better": True,
+        "rows": out,
+        "peak": HBM_PEAK_GBS,
+        "dtype": "fp16 / bf16",
+        "data": "synthetic K/V",
+        "config": {"workload": "all-resident decode attention at growing batch; value is the D=128 case"},
+    }
+
+
 class SimpleTokenizer:
     eos_token_id = None
 
@@ -534,9 +606,11 @@ def main() -> int:
                     help="host blocks read in place over the host link, or copied into a staging ring")
     ap.add_argument("--resident-layers", type=int, default=24,
                     help="layers of the all-resident HBM measurement (0 skips it)")
-    ap.add_argument("--workload", choices=["batch8", "continuous", "register", "configs"], default="batch8",
+    ap.add_argument("--workload", choices=["batch8", "continuous", "register", "configs", "hbm-scale"],
+                    default="batch8",
                     help="batch8: the headline line; continuous: the 64-request continuous-batching run; "
-                         "register: prompt registration at 8k-64k tokens; configs: configurations 1, 3, 4")
+                         "register: prompt registration at 8k-64k tokens; configs: configurations 1, 3, 4; "
+                         "hbm-scale: the all-resident kernel against bytes per launch")
     ap.add_argument("--register-reps", type=int, default=3)
     ap.add_argument("--cb-rounds", type=int, default=24)
     ap.add_argument("--cb-extra-requests", type=int, default=64)
@@ -556,6 +630,11 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a HIP device", file=sys.stderr)
         return 2
+    if args.workload == "hbm-scale":
+        line = hbm_scale(args)
+        line.update({"n_gpus": 1, "steps": 8, "warmup": 2, "scaling": "weak", "vs_baseline": None})
+        print(json.dumps(line), flush=True)
+        return 0
     if args.workload == "configs":
         line = configs(args)
         line.update({"n_gpus": 1, "steps": None, "warmup": None, "scaling": "weak", "vs_baseline": None})
