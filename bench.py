@@ -421,21 +421,24 @@ def configs(args):
     model = model.to(torch.float16).eval()
     g = torch.Generator().manual_seed(8)
     ids = torch.randint(0, 32000, (1, 8192), generator=g).cuda()
-    pm = PagedModel(model, vram_budget=41 * MIB16, ram_budget=1 << 40, recent_window=8,
-                    policy="sinks_heavy_hitter", tokens_per_block=32, max_context_tokens=8192 + 512)
-    first = pm.generate(ids, torch.ones_like(ids), 1)
-    ids2 = torch.cat([ids, torch.tensor([first], device="cuda")], dim=1)
     n_new = 256
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    pm.generate(ids2, torch.ones_like(ids2), n_new)
-    torch.cuda.synchronize()
-    dt = (time.perf_counter() - t0) / n_new
-    st = pm.last_run_stats
+    timed = {}
+    for graphs in (False, True):
+        pm = PagedModel(model, vram_budget=41 * MIB16, ram_budget=1 << 40, recent_window=8,
+                        policy="sinks_heavy_hitter", tokens_per_block=32, max_context_tokens=8192 + 512,
+                        use_hip_graphs=graphs)
+        first = pm.generate(ids, torch.ones_like(ids), 1)
+        ids2 = torch.cat([ids, torch.tensor([first], device="cuda")], dim=1)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        pm.generate(ids2, torch.ones_like(ids2), n_new)
+        torch.cuda.synchronize()
+        timed[graphs] = ((time.perf_counter() - t0) / n_new, pm.last_run_stats)
+        pm.reset()
+    dt, st = timed[True]
     host_b = st.total_cpu_to_gpu_mb * 1e6 / n_new
     kv_tok = 2 * 4 * 64 * 2 * 22
     in_scope = 8192 + n_new // 2
-    pm.reset()
     del model
     torch.cuda.empty_cache()
     # CPU: the attention of one decode step over all 22 layers at the mean context.
@@ -446,6 +449,8 @@ def configs(args):
     rows["3"] = {
         "ms_per_token": round(dt * 1e3, 3),
         "tokens_per_s": round(1 / dt, 1),
+        "eager_ms_per_token": round(timed[False][0] * 1e3, 3),
+        "note": "decode steps replayed from captured HIP graphs (use_hip_graphs=True); eager for comparison",
         "kv_GBs": round(in_scope * kv_tok / dt / 1e9, 2),
         "host_link": {"bytes_per_token": int(host_b), "GBs": round(host_b / dt / 1e9, 2),
                       "frac_of_64": round(host_b / dt / 1e9 / LINK_PEAK_GBS, 4)},

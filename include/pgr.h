@@ -35,7 +35,7 @@ extern "C" {
 
 /* ---- library ------------------------------------------------------------------------- */
 
-/* ABI version of this header (increments when an entry point is added or changed); 3. */
+/* ABI version of this header (increments when an entry point is added or changed); 4. */
 int pgr_abi_version(void);
 /* Message of the last failing call on this thread ("" if none). */
 const char* pgr_last_error(void);
@@ -220,6 +220,12 @@ int pgr_kv_decode_layer(void* kv, int32_t layer, const void* q, const void* k_ne
  * are written to completed[] (the new block id is then length / T - 1).
  * Replaces _append_new_full_blocks_from_grown_tail, paged_model.py:1210-1233. */
 int pgr_kv_end_step(void* kv, int32_t* completed, int32_t* n_completed);
+/* No counterpart in the reference (its decode step is not graph-captured). For callers that
+ * capture decode steps in a HIP graph: writes up to cap values describing what the open
+ * step's launches take as arguments (workspace pointers, grid sizes, mass stride) and
+ * returns their number. A graph captured in a step stays valid for any later step with the
+ * same values, since each step's plan is uploaded to the same workspace before replay. */
+int pgr_kv_step_signature(void* kv, int64_t* out, int64_t cap);
 /* Attaches a placement handle (pgr_pager_new) to session sid; the store does not own it.
  * scores_from_mass != 0 for attention-scored policies (mass-driven scores). */
 int pgr_kv_attach_pager(void* kv, int32_t sid, void* pager, int32_t scores_from_mass);

@@ -125,7 +125,7 @@ int kv_rc(pgr::PagedKV* kv, int rc) {
 
 extern "C" {
 
-int pgr_abi_version(void) { return 3; }
+int pgr_abi_version(void) { return 4; }
 
 const char* pgr_last_error(void) { return g_last_error.c_str(); }
 
@@ -351,6 +351,13 @@ int pgr_kv_decode_layer(void* kv, int32_t layer, const void* q, const void* k_ne
   if (!(scale > 0.f) || !std::isfinite(scale)) return set_err(pgr::kErrInvalid, "scale must be positive and finite");
   return kv_rc(kv_of(kv), kv_of(kv)->decode_layer(layer, q, k_new, v_new, out, mass_accum, accum_stride, scale,
                                                   softcap > 0.f ? softcap : 0.f, as_stream(stream)));
+}
+
+int pgr_kv_step_signature(void* kv, int64_t* out, int64_t cap) {
+  if (!kv || (cap && !out)) return set_err(pgr::kErrInvalid, "null pointer");
+  const int rc = kv_of(kv)->step_signature(out, cap);
+  if (rc < 0) return set_err(rc, "step_signature outside a decode step");
+  return rc;
 }
 
 int pgr_kv_end_step(void* kv, int32_t* completed, int32_t* n_completed) {

@@ -971,7 +971,6 @@ int PagedKV::decode_layer(int layer, const void* q, const void* k_new, const voi
   pl.scale = scale;
   pl.softcap = softcap;
   const int n_launch = (int)launch_work_begin_.size();
-  if (cfg_.stream_mode == 0) stats_.stream_bytes += (uint64_t)step_stats_.host_blocks * rec;
   size_t ci = 0;
   for (int L = 0; L < n_launch; ++L) {
     const int buf = (step_stage_base_ + L) % cfg_.staging_buffers;
@@ -1018,9 +1017,30 @@ int PagedKV::decode_layer(int layer, const void* q, const void* k_new, const voi
   return kOk;
 }
 
+int PagedKV::step_signature(int64_t* out, int64_t cap) const {
+  if (!in_step_) return kErrState;
+  std::vector<int64_t> v = {
+      (int64_t)(uintptr_t)ws_, (int64_t)(uintptr_t)d_seqs_, (int64_t)(uintptr_t)d_work_,
+      (int64_t)(uintptr_t)d_sess_rows_, (int64_t)(uintptr_t)d_sess_first_, (int64_t)(uintptr_t)d_pm_,
+      (int64_t)(uintptr_t)d_pl_, (int64_t)(uintptr_t)d_pacc_, (int64_t)(uintptr_t)d_mass_m_,
+      (int64_t)(uintptr_t)d_mass_s_, (int64_t)(uintptr_t)d_mf_, (int64_t)(uintptr_t)d_lf_,
+      (int64_t)cfg_.stream_mode, (int64_t)seqs_.size(), (int64_t)step_sids_.size(), (int64_t)mass_stride_,
+      (int64_t)launch_work_begin_.size()};
+  for (size_t L = 0; L < launch_work_begin_.size(); ++L) {
+    v.push_back(launch_work_begin_[L]);
+    v.push_back(launch_work_end_[L]);
+  }
+  if (out)
+    for (size_t i = 0; i < v.size() && (int64_t)i < cap; ++i) out[i] = v[i];
+  return (int)v.size();
+}
+
 int PagedKV::end_step(int32_t* completed, int* n_completed) {
   if (!in_step_) return fail(kErrState, "end_step without begin_step");
   const int64_t T = cfg_.tokens_per_block;
+  // Host blocks read in place this step, every layer (counted here rather than per launch,
+  // so that steps replayed from a captured graph are counted too).
+  if (cfg_.stream_mode == 0) stats_.stream_bytes += (uint64_t)step_stats_.host_blocks * rec_bytes() * cfg_.num_layers;
   int c = 0;
   for (size_t i = 0; i < step_sids_.size(); ++i) {
     Session& s = sessions_[step_sids_[i]];

@@ -114,6 +114,11 @@ class PagedKV {
   int decode_layer(int layer, const void* q, const void* k_new, const void* v_new, void* out, float* mass_accum,
                    int64_t accum_stride, float scale, float softcap, hipStream_t stream);
   int end_step(int32_t* completed_sessions, int* n_completed);
+  // Everything the open step's launches take as arguments besides the caller's tensors:
+  // workspace pointers, grid sizes, the mass stride. Launches captured in a graph stay valid
+  // for a later step with the same signature (the plan they read is uploaded per step).
+  // Returns the number of values (writes at most cap), or kErrState outside a step.
+  int step_signature(int64_t* out, int64_t cap) const;
 
   // Per-step placement glue of paged_model.py:768-812 for sessions with an attached pager:
   // scores (uniform, or this step's block mass averaged over layers and normalized), then

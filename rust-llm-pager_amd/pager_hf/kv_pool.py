@@ -128,6 +128,14 @@ class NativeKVPool:
         arr = (ctypes.c_int32 * len(lo))(*[int(x) for x in lo])
         self._call("set_lo", self.lib.pgr_kv_set_lo, sid, arr)
 
+    def step_signature(self) -> tuple[int, ...]:
+        """Launch arguments of the open step (workspace pointers, grids, mass stride): a graph
+        captured in one step may be replayed in any later step with the same signature."""
+        n = nat.check(self.lib.pgr_kv_step_signature(self.handle, None, 0), "step_signature")
+        arr = _i64_array(n)
+        nat.check(self.lib.pgr_kv_step_signature(self.handle, arr, n), "step_signature")
+        return tuple(arr[:n])
+
     def reorder_rows(self, sid: int, src_rows) -> None:
         """New row r of session `sid` takes old row src_rows[r]'s K/V history (beam search)."""
         arr = (ctypes.c_int32 * len(src_rows))(*[int(x) for x in src_rows])

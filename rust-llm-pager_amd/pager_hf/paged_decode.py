@@ -99,6 +99,10 @@ class PagedDecoder:
         self._tokens: dict[int, int] = {}  # session length, mirrored to avoid native round trips
         self._step: list[int] | None = None
         self._mass: torch.Tensor | None = None
+        # Persistent per-step mass accumulator [sessions, blocks] with a fixed row stride, so
+        # a decode step captured in a graph keeps pointing at valid memory; it is replaced
+        # (new pointer) only when a step needs more rows or blocks.
+        self._mass_buf: torch.Tensor | None = None
         self._n_mass: list[int] = []
 
     # -- sessions ------------------------------------------------------------------------
@@ -192,7 +196,14 @@ class PagedDecoder:
         for sid in sids:
             self._tokens[sid] += 1
         if any(self.sessions[sid].needs_attention for sid in sids):
-            self._mass = torch.zeros((len(sids), max(self._n_mass) + 1), dtype=torch.float32, device=self.device)
+            rows, width = len(sids), max(self._n_mass) + 1
+            buf = self._mass_buf
+            if buf is None or buf.shape[0] < rows or buf.shape[1] < width:
+                r = max(rows, 0 if buf is None else buf.shape[0])
+                w = max(2 * width, 0 if buf is None else buf.shape[1])
+                buf = self._mass_buf = torch.empty((r, w), dtype=torch.float32, device=self.device)
+            buf[:rows, :width].zero_()
+            self._mass = buf
         else:
             self._mass = None
 

@@ -104,11 +104,16 @@ class PagedModel:
         streaming_group_size_blocks: int = 64,
         max_context_tokens: int | None = None,
         stream_mode: str = "direct",
+        use_hip_graphs: bool = False,
     ):
         """Arguments and defaults of paged_model.py:200-215. Added: ``max_context_tokens``
         (tokens per row the native store is sized for; default: the first session's prompt
         plus max_new_tokens) and ``stream_mode`` ("direct" or "staged"). The group size has
         no effect: the native kernel covers every block in one launch.
+        ``use_hip_graphs=True`` replays decode steps from a captured HIP graph (direct
+        stream mode only): the first decode step runs eagerly, a step whose launch signature
+        differs from the captured one (a new block changes the grids about once per block)
+        is captured and replayed, later steps with the same signature are replayed.
         ``use_streaming_attention=False`` selects the reference's reload mode, which copies
         every block back into one HBM cache per step and runs the model's own attention
         (paged_model.py:717-760). For the supported model types it computes the same
@@ -117,6 +122,14 @@ class PagedModel:
             logger.info("use_streaming_attention=False: running the native paged path (same attention, no reload)")
         if tokens_per_block <= 0 or tokens_per_block % 16:
             raise ValueError("tokens_per_block must be a positive multiple of 16 for the native kernels")
+        if use_hip_graphs and stream_mode != "direct":
+            raise ValueError("use_hip_graphs needs stream_mode='direct' (staged copies run on a second stream)")
+        self.use_hip_graphs = use_hip_graphs
+        self._graph = None
+        self._graph_sig = None
+        self._graph_pool = None
+        self._graph_io = None
+        self._graph_warm = False
         self.model = model
         self.tokens_per_block = tokens_per_block
         self.prefill_chunk_tokens = prefill_chunk_tokens
@@ -165,6 +178,7 @@ class PagedModel:
             self._lock.release()
 
     def _close(self) -> None:
+        self._graph = self._graph_sig = self._graph_io = None
         if self._decoder is not None:
             self._decoder.pool.close()
         self._decoder = None
@@ -503,9 +517,13 @@ class PagedModel:
         dec.begin_step([sid])
         host_blocks = dec.pool.step_stats()["host_blocks"]
         try:
-            with self._paged_attention():
-                out = self.model(input_ids=input_id_tensor, position_ids=position_ids, use_cache=False,
-                                 logits_to_keep=1)
+            if self.use_hip_graphs:
+                logits = self._graph_forward(input_id_tensor, position_ids)
+            else:
+                with self._paged_attention():
+                    out = self.model(input_ids=input_id_tensor, position_ids=position_ids, use_cache=False,
+                                     logits_to_keep=1)
+                logits = out.logits[:, -1, :]
         except BaseException:
             dec.end_step(collect=False)
             raise
@@ -519,7 +537,40 @@ class PagedModel:
             "cpu_to_gpu_copies": host_blocks * self._num_layers,
             "attention_in_gpu": st["attention_in_gpu"],
         }
-        return out.logits[:, -1, :], step
+        return logits, step
+
+    def _graph_forward(self, input_ids: torch.Tensor, position_ids: torch.Tensor) -> torch.Tensor:
+        """The decode forward of an open step from a captured HIP graph. The native launches
+        read the step's plan from the store's workspace, uploaded by begin_step, so a graph
+        stays valid while the launch signature (workspace pointers, grids, mass buffer) and
+        the input shapes are unchanged. Returns the last-position logits [B, V]; the tensor
+        is reused by the next step."""
+        dec = self._decoder
+        mass = dec._mass
+        sig = (dec.pool.step_signature(), None if mass is None else (mass.data_ptr(), mass.stride(0)),
+               tuple(input_ids.shape))
+        if not self._graph_warm:  # first decode step: eager, so libraries set up outside capture
+            self._graph_warm = True
+            with self._paged_attention():
+                out = self.model(input_ids=input_ids, position_ids=position_ids, use_cache=False, logits_to_keep=1)
+            return out.logits[:, -1, :]
+        if self._graph is None or sig != self._graph_sig:
+            # The previous graph stays alive until the new one is captured: its memory pool is
+            # shared, and releasing the last graph of a pool releases the pool.
+            ids, pos = input_ids.clone(), position_ids.clone()
+            graph = torch.cuda.CUDAGraph()
+            if self._graph_pool is None:
+                self._graph_pool = torch.cuda.graph_pool_handle()
+            with self._paged_attention():
+                with torch.cuda.graph(graph, pool=self._graph_pool):
+                    out = self.model(input_ids=ids, position_ids=pos, use_cache=False, logits_to_keep=1)
+            self._graph, self._graph_sig, self._graph_io = graph, sig, (ids, pos, out.logits)
+        else:
+            ids, pos, _ = self._graph_io
+            ids.copy_(input_ids)
+            pos.copy_(position_ids)
+        self._graph.replay()
+        return self._graph_io[2][:, -1, :]
 
     @staticmethod
     def _position_ids_from_mask(attention_mask: torch.Tensor) -> torch.Tensor:

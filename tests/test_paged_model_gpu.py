@@ -214,3 +214,39 @@ def test_reload_mode_flag_gives_the_same_tokens():
     a = PagedModel(model, **kw).generate(ids, mask, 16)
     b = PagedModel(model, use_streaming_attention=False, **kw).generate(ids, mask, 16)
     assert a == b
+
+
+@pytest.mark.parametrize("policy", ["sinks_heavy_hitter", "recent_only"])
+def test_hip_graph_steps_match_eager_steps(policy):
+    """Decode steps replayed from captured HIP graphs give the eager steps' logits and tokens,
+    across block boundaries (each new block changes the launch signature: re-capture)."""
+    from pager_hf import PagedModel
+
+    model = _model(SMALL, seed=17, init_std=0.05)
+    g = torch.Generator().manual_seed(18)
+    ids = torch.randint(0, SMALL["vocab_size"], (2, 300), generator=g).cuda()
+    mask = torch.ones_like(ids)
+    mask[1, :40] = 0
+    kw = dict(vram_budget=4 * MIB16, ram_budget=1 << 40, recent_window=2, policy=policy, tokens_per_block=16)
+    eager = PagedModel(model, **kw)
+    graph = PagedModel(model, use_hip_graphs=True, **kw)
+    with torch.inference_mode():
+        for pm in (eager, graph):
+            pm._start_session(ids, mask, 80)
+        nxt, cur = ids[:, -1:], mask
+        worst = 0.0
+        for step in range(80):
+            a, _ = eager._forward_step(nxt, cur)
+            b, _ = graph._forward_step(nxt, cur)
+            worst = max(worst, float((a.float() - b.float()).abs().max()))
+            nxt = torch.argmax(a, dim=-1, keepdim=True)
+            assert torch.equal(nxt, torch.argmax(b, dim=-1, keepdim=True)), f"step {step}"
+            cur = torch.cat([cur, cur.new_ones((2, 1))], dim=1)
+        assert graph._graph is not None  # steps were replayed from a graph
+    assert worst < 1e-2, worst
+    eager.reset()
+    graph.reset()
+    # The public path: the same tokens from generate().
+    g2 = PagedModel(model, use_hip_graphs=True, **kw)
+    e2 = PagedModel(model, **kw)
+    assert g2.generate(ids, mask, 40) == e2.generate(ids, mask, 40)
