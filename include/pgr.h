@@ -179,7 +179,10 @@ int pgr_kv_set_lo(void* kv, int32_t sid, const int32_t* lo_per_row);
  * Replaces KVBlockStore.reorder_batch_rows, kv_block_store.py:229-254 (and the tail
  * index_select of PagedModel._reorder_batch, paged_model.py:636-644). Synchronous. */
 int pgr_kv_reorder_rows(void* kv, int32_t sid, const int32_t* src_rows, int32_t n_rows, void* stream);
-/* Declares the length of an empty session (prefill); full blocks start host-side. */
+/* Declares the length of an empty session (prefill). Full blocks start host-side, holding no
+ * data and charged to no tier until the next pgr_kv_apply_tiers places them: one placed on
+ * the host then counts against the RAM budget (PGR_ERR_BUDGET past it), as the reference's
+ * first offload of a prompt block does (kv_block_store.py:83-99). */
 int pgr_kv_set_length(void* kv, int32_t sid, int64_t n_tokens);
 /* Writes tokens [0, n_tokens) of (sid, row, layer) from k, v [Hkv, n_src, D] (device).
  * Replaces _build_initial_store + real_past_to_blocks, paged_model.py:1183-1192 and

@@ -260,6 +260,7 @@ int PagedKV::add_session(int rows, int64_t capacity_tokens, const int32_t* lo_pe
   s.slot.assign((size_t)s.capacity_blocks * rows, -1);
   s.host_valid.assign((size_t)s.capacity_blocks * rows, 0);
   s.on_gpu.assign(s.capacity_blocks, 0);
+  s.placed.assign(s.capacity_blocks, 0);
   for (size_t i = 0; i < sessions_.size(); ++i)
     if (!sessions_[i].live) {
       sessions_[i] = std::move(s);
@@ -286,7 +287,7 @@ int PagedKV::remove_session(int sid) {
   for (int64_t b = 0; b < n_full; ++b) {
     if (s.on_gpu[b])
       gpu_bytes_ -= bb;
-    else
+    else if (s.placed[b])
       cpu_bytes_ -= bb;
   }
   for (int r = 0; r < s.rows; ++r) host_free(s.row[r].host_off, s.capacity_blocks);
@@ -417,10 +418,12 @@ int PagedKV::set_length(int sid, int64_t n_tokens) {
   if (n_tokens < 0 || (n_tokens + T - 1) / T >= s.capacity_blocks)
     return fail(kErrCapacity, "n_tokens exceeds the session capacity");
   const int64_t n_full = n_tokens / T;
-  // Full blocks start on the host side (tier 1 in the pager's terms) with no data yet;
-  // the open block, if any, gets its HBM slot now.
-  for (int64_t b = 0; b < n_full; ++b) s.on_gpu[b] = 0;
-  cpu_bytes_ += n_full * block_bytes_all_layers(sid);
+  // Full blocks start on the host side with no data and uncharged: their first apply_tiers
+  // places them, charging HBM or the RAM budget. The open block, if any, gets its HBM slot now.
+  for (int64_t b = 0; b < n_full; ++b) {
+    s.on_gpu[b] = 0;
+    s.placed[b] = 0;
+  }
   if (n_tokens % T != 0) {
     for (int r = 0; r < s.rows; ++r) {
       const int sl = alloc_slot();
@@ -529,6 +532,7 @@ int PagedKV::put_block(int sid, int64_t block_id, const void* key, const void* v
     s.host_valid[block_id * s.rows + r] = 0;
   }
   s.on_gpu[block_id] = 1;
+  s.placed[block_id] = 1;
   s.n_tokens += T;
   gpu_bytes_ += block_bytes_all_layers(sid);
   return kOk;
@@ -634,7 +638,8 @@ int PagedKV::apply_tiers(int sid, const uint8_t* tiers, int64_t n_tiers, int64_t
       if ((rc = order_streams()) != kOk) break;
       rc = move_block(s, b, true, stream);
       if (rc != kOk) break;
-      cpu_bytes_ -= bb;
+      if (s.placed[b]) cpu_bytes_ -= bb;
+      s.placed[b] = 1;
       gpu_bytes_ += bb;
       stats_.cpu_to_gpu_bytes += bb;
       stats_.cpu_to_gpu_copies += 1;
@@ -653,6 +658,16 @@ int PagedKV::apply_tiers(int sid, const uint8_t* tiers, int64_t n_tiers, int64_t
       stats_.gpu_to_cpu_bytes += bb;
       stats_.gpu_to_cpu_copies += 1;
       to_cpu[(*n_cpu)++] = b;
+    } else if (desired != 0 && !s.placed[b]) {
+      // A prompt block taking its first place on the host side (kv_block_store.py:83-99
+      // checks the budget the same way when the reference offloads it).
+      if (ram_budget_ >= 0 && cpu_bytes_ + bb > ram_budget_) {
+        *fail_block = b;
+        rc = fail(kErrBudget, "ram_budget exceeded");
+        break;
+      }
+      cpu_bytes_ += bb;
+      s.placed[b] = 1;
     }
   }
   // Evictions first: a load may reuse a slot an eviction of this call freed.
@@ -1049,6 +1064,7 @@ int PagedKV::end_step(int32_t* completed, int* n_completed) {
     if ((p + 1) % T == 0) {
       const int64_t b = p / T;
       s.on_gpu[b] = 1;
+      s.placed[b] = 1;
       for (int r = 0; r < s.rows; ++r) s.host_valid[b * s.rows + r] = 0;
       gpu_bytes_ += block_bytes_all_layers(step_sids_[i]);
       if (completed) completed[c] = step_sids_[i];

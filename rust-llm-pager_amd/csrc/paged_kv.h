@@ -164,6 +164,9 @@ class PagedKV {
     std::vector<int32_t> slot;
     std::vector<uint8_t> host_valid;  // [b * rows + r]
     std::vector<uint8_t> on_gpu;      // logical residency per full block [b]
+    // [b]: 1 once block b's bytes are charged to a tier. A prompt's blocks (set_length)
+    // hold no data until their first placement, which charges them against the RAM budget.
+    std::vector<uint8_t> placed;
     PlacementPager* pager = nullptr;  // not owned
     bool scores_from_mass = false;
   };
