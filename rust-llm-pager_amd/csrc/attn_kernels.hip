@@ -21,8 +21,9 @@
 // contiguous run of D/4 elements of K row n: chunk c, k-slot 4g+i <-> dim (D/4)g + 4c + i.
 // V is read as four token rows of D/16 contiguous elements (dims (D/16)n .. +D/16) and
 // transposed in registers with v_perm_b32 into the A operand of each of the D/16 M-tiles;
-// M-tile j, row r <-> dim (D/16)r + j. All global loads are 16/8/4-byte per lane and cover
-// whole 128-byte rows per instruction.
+// M-tile j, row r <-> dim (D/16)r + j. All global loads are 16/8/4-byte per lane. One K load
+// instruction covers half of each of the tile's 16 rows. One V load instruction covers four
+// whole rows, or at head_dim 64 a quarter of each of the 16 rows (see load_tile_rs).
 //
 // P is rounded to the K/V element type before the P.V product, as the reference does
 // (streaming_attention.py:178, :347, :428).
@@ -480,6 +481,15 @@ constexpr float kMInit = -1.0e30f;  // running max before any valid score (finit
 // rows 4g..4g+3 (v_lane, then +D elements). `r` covers one KV head of one record, `sk` / `sv` are
 // the tile's K and V byte offsets (wave-uniform, in SGPRs). A resource with no records makes
 // every load of the tile return zeros without a memory access.
+//
+// At head_dim 64, V load i of lane (g, n) reads row 4g + (i + n) % 4, so that one instruction
+// touches all 16 rows (cache lines) of the V tile rather than 4. Reads of the host mirror over
+// the host link run about 2% faster that way; unrotate_v puts the rows back in order before
+// the fold. At head_dim 128 (two lines per row) the same rotation read the host link 8%
+// slower, so the other head dims load rows in order.
+template <int D>
+constexpr bool kRotateV = D == 64;
+
 constexpr int kBufferFlags = 0x00020000;  // dword 3 of a raw buffer resource on gfx9
 
 template <int D>
@@ -487,9 +497,10 @@ __device__ __forceinline__ void load_tile_rs(Tile<D>& t, __amdgpu_buffer_rsrc_t 
                                              uint32_t k_lane, uint32_t v_lane) {
 #pragma unroll
   for (int i = 0; i < Tile<D>::KV4; ++i) t.k[i] = __builtin_amdgcn_raw_buffer_load_b128(r, k_lane + 16u * i, sk, 0);
+  const int rot = kRotateV<D> ? (int)(__lane_id() & 3) : 0;  // n % 4
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const uint32_t off = v_lane + (uint32_t)(i * D * 2);
+    const uint32_t off = v_lane + (uint32_t)(((i + rot) & 3) * D * 2);
     if constexpr (D == 32) {
       t.v[i][0] = __builtin_amdgcn_raw_buffer_load_b32(r, off, sv, 0);
     } else if constexpr (D == 64) {
@@ -503,6 +514,21 @@ __device__ __forceinline__ void load_tile_rs(Tile<D>& t, __amdgpu_buffer_rsrc_t 
       t.v[i][2] = x.z;
       t.v[i][3] = x.w;
     }
+  }
+}
+
+// Undoes the lane rotation of load_tile_rs: slot i holds row (i + r) % 4 with r = n % 4, so
+// row k sits in slot (k - r) % 4. Two select stages shift by r & 1, then by r & 2.
+template <int D>
+__device__ __forceinline__ void unrotate_v(Tile<D>& t, bool r1, bool r2) {
+#pragma unroll
+  for (int w = 0; w < Tile<D>::VW; ++w) {
+    const uint32_t a0 = t.v[0][w], a1 = t.v[1][w], a2 = t.v[2][w], a3 = t.v[3][w];
+    const uint32_t b0 = r1 ? a3 : a0, b1 = r1 ? a0 : a1, b2 = r1 ? a1 : a2, b3 = r1 ? a2 : a3;
+    t.v[0][w] = r2 ? b2 : b0;
+    t.v[1][w] = r2 ? b3 : b1;
+    t.v[2][w] = r2 ? b0 : b2;
+    t.v[3][w] = r2 ? b1 : b3;
   }
 }
 
@@ -584,7 +610,9 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(PagedArgs a) {
     }
   };
 
+  const bool rot1 = (n & 1) != 0, rot2 = (n & 2) != 0;
   auto fold = [&](Tile<D>& t, const TileMeta& mt) {
+    if constexpr (kRotateV<D>) unrotate_v<D>(t, rot1, rot2);
     f32x4 s4 = qk_tile<Ty, D>(t, q);
     if (capped) {
 #pragma unroll
@@ -882,18 +910,10 @@ hipError_t launch_dense_ty(const DenseArgs& a, int mode, int batch, int d, float
   }
 }
 
-// With start/stop events, the launch itself timestamps the kernel's execution (the events
-// bracket the dispatch packet, not the queue ahead of it).
 template <class Ty, int D>
-hipError_t launch_paged_t(const PagedArgs& a, int n_work, bool mass, hipEvent_t ev_start, hipEvent_t ev_stop,
-                          hipStream_t stream) {
+hipError_t launch_paged_t(const PagedArgs& a, int n_work, bool mass, hipStream_t stream) {
   dim3 grid(n_work, a.hkv);
-  if (ev_start != nullptr) {
-    if (mass)
-      hipExtLaunchKernelGGL(paged_attn_kernel<Ty, D, true>, grid, dim3(256), 0, stream, ev_start, ev_stop, 0, a);
-    else
-      hipExtLaunchKernelGGL(paged_attn_kernel<Ty, D, false>, grid, dim3(256), 0, stream, ev_start, ev_stop, 0, a);
-  } else if (mass) {
+  if (mass) {
     paged_attn_kernel<Ty, D, true><<<grid, 256, 0, stream>>>(a);
   } else {
     paged_attn_kernel<Ty, D, false><<<grid, 256, 0, stream>>>(a);
@@ -991,20 +1011,20 @@ hipError_t launch_paged(int dtype, int d, const PagedLaunch& p, hipStream_t stre
   if (dtype == kF16) {
     switch (d) {
       case 32:
-        return launch_paged_t<F16, 32>(a, p.n_work, mass, p.ev_start, p.ev_stop, stream);
+        return launch_paged_t<F16, 32>(a, p.n_work, mass, stream);
       case 64:
-        return launch_paged_t<F16, 64>(a, p.n_work, mass, p.ev_start, p.ev_stop, stream);
+        return launch_paged_t<F16, 64>(a, p.n_work, mass, stream);
       default:
-        return launch_paged_t<F16, 128>(a, p.n_work, mass, p.ev_start, p.ev_stop, stream);
+        return launch_paged_t<F16, 128>(a, p.n_work, mass, stream);
     }
   }
   switch (d) {
     case 32:
-      return launch_paged_t<BF16, 32>(a, p.n_work, mass, p.ev_start, p.ev_stop, stream);
+      return launch_paged_t<BF16, 32>(a, p.n_work, mass, stream);
     case 64:
-      return launch_paged_t<BF16, 64>(a, p.n_work, mass, p.ev_start, p.ev_stop, stream);
+      return launch_paged_t<BF16, 64>(a, p.n_work, mass, stream);
     default:
-      return launch_paged_t<BF16, 128>(a, p.n_work, mass, p.ev_start, p.ev_stop, stream);
+      return launch_paged_t<BF16, 128>(a, p.n_work, mass, stream);
   }
 }
 

@@ -1006,16 +1006,18 @@ int PagedKV::decode_layer(int layer, const void* q, const void* k_new, const voi
     pl.work = d_work_ + launch_work_begin_[L];
     pl.n_work = launch_work_end_[L] - launch_work_begin_[L];
     PendingTiming t{nullptr, nullptr, 0};
-    pl.ev_start = pl.ev_stop = nullptr;
     if (timing_) {
-      // Timing-only events: without a system-scope fence at record time they do not write
-      // back and invalidate the caches around the launch they stamp.
+      // Timing-only events recorded on the stream right before and after the launch. Without
+      // a system-scope fence at record time they do not write back and invalidate the caches
+      // around the launch they stamp. (Events handed to the launch itself read 15 to 18 us on
+      // the same launches, varying from process to process; these read a steady ~1 us above
+      // the kernel trace.)
       PGR_HIP(hipEventCreateWithFlags(&t.start, hipEventDisableSystemFence));
       PGR_HIP(hipEventCreateWithFlags(&t.stop, hipEventDisableSystemFence));
-      pl.ev_start = t.start;
-      pl.ev_stop = t.stop;
+      PGR_HIP(hipEventRecord(t.start, stream));
     }
     PGR_HIP(launch_paged(cfg_.dtype, cfg_.head_dim, pl, stream));
+    if (timing_) PGR_HIP(hipEventRecord(t.stop, stream));
     if (timing_) {
       int64_t ent = 0;
       for (int w = launch_work_begin_[L]; w < launch_work_end_[L]; ++w) ent += work_[w].entry_count;

@@ -48,8 +48,6 @@ struct PagedLaunch {
   float* lf;
   int n_work, hq, hkv, tokens_per_block, mass_stride;
   float scale, softcap;
-  hipEvent_t ev_start = nullptr;  // optional: timestamp the attention kernel's execution
-  hipEvent_t ev_stop = nullptr;
 };
 
 bool head_dim_supported(int d);
