@@ -90,6 +90,16 @@ __global__ void copy_records_kernel(void* const* bases, int src_tbl, int dst_tbl
   for (int64_t i = threadIdx.x; i < rec_vec; i += blockDim.x) dst[i] = src[i];
 }
 
+// The step plan, copied from the pinned upload buffer (read in place through its device
+// mapping) into the workspace. A copy kernel on the compute stream, rather than an SDMA copy,
+// keeps the plan upload on the queue that runs the attention: each hand-off between the copy
+// engine and the compute queue cost about 9 and 26 us per step.
+__global__ void plan_upload_kernel(const void* src, void* dst, int64_t n_vec) {
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n_vec) static_cast<u32x4*>(dst)[i] = static_cast<const u32x4*>(src)[i];
+}
+
 }  // namespace
 
 PagedKV::PagedKV(const PagedKVConfig& cfg) : cfg_(cfg) {}
@@ -930,6 +940,7 @@ int PagedKV::begin_step(const int32_t* sids, int n, hipStream_t stream) {
     plan_host_ = nullptr;
     const size_t want = std::max(plan_bytes, plan_host_bytes_ * 3 / 2);
     PGR_HIP(hipHostMalloc(&plan_host_, want, hipHostMallocDefault));
+    PGR_HIP(hipHostGetDevicePointer(&plan_host_dev_, plan_host_, 0));
     plan_host_bytes_ = want;
   } else {
     PGR_HIP(hipEventSynchronize(plan_uploaded_));
@@ -940,7 +951,10 @@ int PagedKV::begin_step(const int32_t* sids, int n, hipStream_t stream) {
   std::memcpy(h + o_srows, sess_rows.data(), sizeof(int32_t) * n);
   std::memcpy(h + o_sfirst, sess_first.data(), sizeof(int32_t) * n);
   char* d = static_cast<char*>(ws_);
-  PGR_HIP(hipMemcpyAsync(d, h, plan_bytes, hipMemcpyHostToDevice, stream));
+  // plan_bytes is a multiple of 256 (every carve is 256-aligned).
+  const int64_t n_vec = (int64_t)(plan_bytes / 16);
+  plan_upload_kernel<<<(unsigned)((n_vec + 255) / 256), 256, 0, stream>>>(plan_host_dev_, d, n_vec);
+  PGR_HIP(hipGetLastError());
   PGR_HIP(hipEventRecord(plan_uploaded_, stream));
   d_seqs_ = reinterpret_cast<SeqInfo*>(d + o_seqs);
   d_work_ = reinterpret_cast<WorkItem*>(d + o_work);

@@ -223,6 +223,7 @@ class PagedKV {
   int next_index_buf_ = 0;
   std::vector<int64_t> evict_pairs_, load_pairs_;  // moves of the current apply_tiers call
   void* plan_host_ = nullptr;  // pinned upload buffer for the step plan
+  void* plan_host_dev_ = nullptr;  // its device mapping
   size_t plan_host_bytes_ = 0;
   float* mass_host_ = nullptr;  // pinned readback of the step's block mass
   size_t mass_host_floats_ = 0;
