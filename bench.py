@@ -182,7 +182,7 @@ def continuous(args):
         total_vram_budget=conc * per_session_blocks * MIB16, total_ram_budget=1 << 42, policy=args.cb_policy,
         tokens_per_block=T, max_context_tokens=65536 + 1024, host_token_capacity=args.cb_host_tokens,
         max_queue_depth=n_req, device="cuda", stream_mode=args.cb_stream_mode, staging_blocks=args.cb_staging_blocks,
-        staging_buffers=2,
+        staging_buffers=args.cb_staging_buffers,
     )
     g = torch.Generator().manual_seed(6)
     reqs = [sched.submit(torch.randint(0, cfg.vocab_size, (1, n), generator=g), torch.ones(1, n, dtype=torch.long),
@@ -232,6 +232,7 @@ def continuous(args):
                                "median 4096, sigma 1) clipped [256, 65536], outputs U[64, 512], admit on finish",
                    "policy": args.cb_policy, "per_session_hbm_blocks": per_session_blocks, "tokens_per_block": T,
                    "stream_mode": args.cb_stream_mode, "staging_blocks": args.cb_staging_blocks,
+                   "staging_buffers": args.cb_staging_buffers,
                    "requests": n_req},
     }
 
@@ -621,8 +622,9 @@ def main() -> int:
     ap.add_argument("--cb-extra-requests", type=int, default=64)
     ap.add_argument("--cb-policy", default="recent_only")
     ap.add_argument("--cb-host-tokens", type=int, default=800_000)
-    ap.add_argument("--cb-stream-mode", choices=["direct", "staged"], default="direct")
-    ap.add_argument("--cb-staging-blocks", type=int, default=64, help="records per staging buffer (staged mode)")
+    ap.add_argument("--cb-stream-mode", choices=["direct", "staged"], default="staged")
+    ap.add_argument("--cb-staging-blocks", type=int, default=8192, help="records per staging buffer (staged mode)")
+    ap.add_argument("--cb-staging-buffers", type=int, default=2, help="staging buffers (staged mode)")
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
                     help="after timing, run one device copy of this size (counter calibration)")
     args = ap.parse_args()

@@ -90,6 +90,20 @@ __global__ void copy_records_kernel(void* const* bases, int src_tbl, int dst_tbl
   for (int64_t i = threadIdx.x; i < rec_vec; i += blockDim.x) dst[i] = src[i];
 }
 
+// Staged mode: records of one layer's host mirror (read in place through its device mapping)
+// into a staging buffer, by (host record, staging record) pairs. A fixed grid of a few dozen
+// workgroups keeps the host link busy while leaving the CUs to concurrent work.
+constexpr int kStageCopyWorkgroups = 96;
+__global__ void stage_copy_kernel(const void* host, void* stage, const int64_t* pairs, int64_t n_pairs,
+                                  int64_t rec_vec) {
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  for (int64_t p = blockIdx.x; p < n_pairs; p += gridDim.x) {
+    const u32x4* src = static_cast<const u32x4*>(host) + (size_t)pairs[2 * p] * rec_vec;
+    u32x4* dst = static_cast<u32x4*>(stage) + (size_t)pairs[2 * p + 1] * rec_vec;
+    for (int64_t i = threadIdx.x; i < rec_vec; i += blockDim.x) dst[i] = src[i];
+  }
+}
+
 // The step plan, copied from the pinned upload buffer (read in place through its device
 // mapping) into the workspace. A copy kernel on the compute stream, rather than an SDMA copy,
 // keeps the plan upload on the queue that runs the attention: each hand-off between the copy
@@ -131,6 +145,7 @@ PagedKV::~PagedKV() {
     hipEventDestroy(t.stop);
   }
   if (plan_uploaded_) hipEventDestroy(plan_uploaded_);
+  if (stage_copies_done_) hipEventDestroy(stage_copies_done_);
   if (compute_mark_) hipEventDestroy(compute_mark_);
   if (copy_mark_) hipEventDestroy(copy_mark_);
   if (copy_stream_) hipStreamDestroy(copy_stream_);
@@ -196,6 +211,7 @@ int PagedKV::init() {
     PGR_HIP(hipEventCreateWithFlags(&chunk_ready_[i], hipEventDisableTiming));
   }
   PGR_HIP(hipEventCreateWithFlags(&plan_uploaded_, hipEventDisableTiming));
+  PGR_HIP(hipEventCreateWithFlags(&stage_copies_done_, hipEventDisableTiming));
   PGR_HIP(hipEventCreateWithFlags(&compute_mark_, hipEventDisableTiming));
   PGR_HIP(hipEventCreateWithFlags(&copy_mark_, hipEventDisableTiming));
   for (IndexBuf& b : index_bufs_) PGR_HIP(hipEventCreateWithFlags(&b.done, hipEventDisableTiming));
@@ -834,10 +850,16 @@ int PagedKV::begin_step(const int32_t* sids, int n, hipStream_t stream) {
   }
   const bool any_host = !copies_.empty();
   n_chunks_ = any_host ? chunk + 1 : 0;
+  // Cross-layer prefetch (staged mode): when the step's host blocks fit one chunk and there
+  // are two or more buffers, layer l reads buffer (base + l) % buffers, and decode_layer(l)
+  // queues layer l+1's copies right after layer l's attention. The copies then run under the
+  // rest of layer l's work (projections, MLP), which leaves the host link idle otherwise.
+  prefetch_step_ = n_chunks_ == 1 && cfg_.staging_buffers >= 2;
+  prefetched_layer_ = -1;
   // The next step starts on the buffer after this step's last one, so its first copy does
   // not wait for this step's last reader.
   step_stage_base_ = stage_base_;
-  stage_base_ = (stage_base_ + n_chunks_) % cfg_.staging_buffers;
+  stage_base_ = (stage_base_ + (prefetch_step_ ? cfg_.num_layers : n_chunks_)) % cfg_.staging_buffers;
   const int n_launch = std::max(1, n_chunks_);
   // Work items. Each launch is cut into about target_wg / Hkv work items of nearly equal
   // size, so that every CU streams the same number of bytes in one round of workgroups;
@@ -923,6 +945,18 @@ int PagedKV::begin_step(const int32_t* sids, int n, hipStream_t stream) {
   const size_t o_work = carve(sizeof(WorkItem) * std::max<size_t>(work_.size(), 1));
   const size_t o_srows = carve(sizeof(int32_t) * std::max(n, 1));
   const size_t o_sfirst = carve(sizeof(int32_t) * std::max(n, 1));
+  // Staged mode: (host record, staging record) per record to stream, chunk by chunk.
+  stage_pairs_.clear();
+  chunk_pair_begin_.assign(n_chunks_ + 1, 0);
+  for (const CopyCmd& c : copies_) {
+    for (int64_t x = 0; x < c.count; ++x) {
+      stage_pairs_.push_back(c.host_rec + x);
+      stage_pairs_.push_back(c.stage_rec + x);
+    }
+    chunk_pair_begin_[c.chunk + 1] = (int64_t)stage_pairs_.size() / 2;
+  }
+  for (int c = 1; c <= n_chunks_; ++c) chunk_pair_begin_[c] = std::max(chunk_pair_begin_[c], chunk_pair_begin_[c - 1]);
+  const size_t o_spairs = carve(sizeof(int64_t) * std::max<size_t>(stage_pairs_.size(), 2));
   const size_t plan_bytes = off;
   const size_t o_pm = carve(sizeof(float) * (size_t)n_partials_ * hq);
   const size_t o_pl = carve(sizeof(float) * (size_t)n_partials_ * hq);
@@ -950,7 +984,14 @@ int PagedKV::begin_step(const int32_t* sids, int n, hipStream_t stream) {
   std::memcpy(h + o_work, work_.data(), sizeof(WorkItem) * work_.size());
   std::memcpy(h + o_srows, sess_rows.data(), sizeof(int32_t) * n);
   std::memcpy(h + o_sfirst, sess_first.data(), sizeof(int32_t) * n);
+  if (!stage_pairs_.empty()) std::memcpy(h + o_spairs, stage_pairs_.data(), sizeof(int64_t) * stage_pairs_.size());
   char* d = static_cast<char*>(ws_);
+  // A staging copy queued for a layer that was never decoded may still read the previous
+  // step's pair list on the copy stream: the upload waits for it before overwriting the plan.
+  if (stage_copy_pending_) {
+    PGR_HIP(hipStreamWaitEvent(stream, stage_copies_done_, 0));
+    stage_copy_pending_ = false;
+  }
   // plan_bytes is a multiple of 256 (every carve is 256-aligned).
   const int64_t n_vec = (int64_t)(plan_bytes / 16);
   plan_upload_kernel<<<(unsigned)((n_vec + 255) / 256), 256, 0, stream>>>(plan_host_dev_, d, n_vec);
@@ -960,6 +1001,7 @@ int PagedKV::begin_step(const int32_t* sids, int n, hipStream_t stream) {
   d_work_ = reinterpret_cast<WorkItem*>(d + o_work);
   d_sess_rows_ = reinterpret_cast<int32_t*>(d + o_srows);
   d_sess_first_ = reinterpret_cast<int32_t*>(d + o_sfirst);
+  d_stage_pairs_ = reinterpret_cast<int64_t*>(d + o_spairs);
   d_pm_ = reinterpret_cast<float*>(d + o_pm);
   d_pl_ = reinterpret_cast<float*>(d + o_pl);
   d_pacc_ = reinterpret_cast<float*>(d + o_pacc);
@@ -1000,22 +1042,42 @@ int PagedKV::decode_layer(int layer, const void* q, const void* k_new, const voi
   pl.scale = scale;
   pl.softcap = softcap;
   const int n_launch = (int)launch_work_begin_.size();
-  size_t ci = 0;
+  const int nbuf = cfg_.staging_buffers;
+  // Side stream: wait until the previous reader of buffer `buf` finished, then stream the
+  // host runs of chunk `L` of layer `lay` into it. `shift` moves the plan's records (laid out
+  // for the step's first buffer) to buffer `buf`.
+  auto issue_copies = [&](int lay, int L, int buf, int64_t shift) -> int {
+    // The pair list is part of the step plan: wait for its upload and for the buffer's last reader.
+    PGR_HIP(hipStreamWaitEvent(copy_stream_, plan_uploaded_, 0));
+    PGR_HIP(hipStreamWaitEvent(copy_stream_, buf_free_[buf], 0));
+    const int64_t p0 = chunk_pair_begin_[L], np = chunk_pair_begin_[L + 1] - p0;
+    if (np > 0) {
+      const unsigned grid = (unsigned)std::min<int64_t>(np, kStageCopyWorkgroups);
+      stage_copy_kernel<<<grid, 256, 0, copy_stream_>>>(host_dev_[lay], static_cast<char*>(stage_) + shift * (int64_t)rec,
+                                                        d_stage_pairs_ + 2 * p0, np, (int64_t)(rec / 16));
+      PGR_HIP(hipGetLastError());
+    }
+    for (const CopyCmd& c : copies_)
+      if (c.chunk == L) stats_.stream_copies += 1;
+    stats_.stream_bytes += (size_t)np * rec;
+    PGR_HIP(hipEventRecord(chunk_ready_[buf], copy_stream_));
+    PGR_HIP(hipEventRecord(stage_copies_done_, copy_stream_));
+    stage_copy_pending_ = true;
+    return kOk;
+  };
+  auto layer_buf = [&](int lay) { return (step_stage_base_ + lay) % nbuf; };
+  auto layer_shift = [&](int lay) {
+    return (int64_t)(layer_buf(lay) - step_stage_base_ % nbuf) * cfg_.staging_slots;
+  };
   for (int L = 0; L < n_launch; ++L) {
-    const int buf = (step_stage_base_ + L) % cfg_.staging_buffers;
+    const int buf = prefetch_step_ ? layer_buf(layer) : (step_stage_base_ + L) % nbuf;
     if (n_chunks_ > 0) {
-      // Side stream: wait until the previous reader of this buffer finished, stream the runs.
-      PGR_HIP(hipStreamWaitEvent(copy_stream_, buf_free_[buf], 0));
-      while (ci < copies_.size() && copies_[ci].chunk == L) {
-        const CopyCmd& c = copies_[ci++];
-        const char* src = static_cast<const char*>(host_[layer]) + (size_t)c.host_rec * rec;
-        char* dst = static_cast<char*>(stage_) + (size_t)c.stage_rec * rec;
-        PGR_HIP(hipMemcpyAsync(dst, src, (size_t)c.count * rec, hipMemcpyHostToDevice, copy_stream_));
-        stats_.stream_bytes += (size_t)c.count * rec;
-        stats_.stream_copies += 1;
+      if (!(prefetch_step_ && prefetched_layer_ == layer)) {
+        const int rc = issue_copies(layer, L, buf, prefetch_step_ ? layer_shift(layer) : 0);
+        if (rc != kOk) return rc;
       }
-      PGR_HIP(hipEventRecord(chunk_ready_[buf], copy_stream_));
       PGR_HIP(hipStreamWaitEvent(stream, chunk_ready_[buf], 0));
+      if (prefetch_step_) pl.stage = static_cast<const char*>(stage_) + layer_shift(layer) * (int64_t)rec;
     }
     pl.work = d_work_ + launch_work_begin_[L];
     pl.n_work = launch_work_end_[L] - launch_work_begin_[L];
@@ -1039,6 +1101,12 @@ int PagedKV::decode_layer(int layer, const void* q, const void* k_new, const voi
       timing_pending_.push_back(t);
     }
     if (n_chunks_ > 0) PGR_HIP(hipEventRecord(buf_free_[buf], stream));
+  }
+  prefetched_layer_ = -1;
+  if (prefetch_step_ && layer + 1 < cfg_.num_layers) {
+    const int rc = issue_copies(layer + 1, 0, layer_buf(layer + 1), layer_shift(layer + 1));
+    if (rc != kOk) return rc;
+    prefetched_layer_ = layer + 1;
   }
   PGR_HIP(launch_paged_merge(cfg_.dtype, cfg_.head_dim, pl, (int)seqs_.size(), stream));
   if (mass_accum) {

@@ -229,6 +229,8 @@ class PagedKV {
   size_t mass_host_floats_ = 0;
   hipStream_t copy_stream_ = nullptr;
   hipEvent_t plan_uploaded_ = nullptr;
+  hipEvent_t stage_copies_done_ = nullptr;  // after the last staging copy on the copy stream
+  bool stage_copy_pending_ = false;
   std::vector<hipEvent_t> buf_free_;
   std::vector<hipEvent_t> chunk_ready_;
   hipEvent_t compute_mark_ = nullptr;
@@ -256,6 +258,11 @@ class PagedKV {
   int n_partials_ = 0;
   int mass_stride_ = 0;
   int stage_base_ = 0;       // staging buffer of the next step's first chunk
+  std::vector<int64_t> stage_pairs_;      // staged mode: (host record, staging record) pairs
+  std::vector<int64_t> chunk_pair_begin_;  // first pair of each chunk, and the end
+  int64_t* d_stage_pairs_ = nullptr;       // the pairs in the uploaded plan
+  bool prefetch_step_ = false;  // staged mode, one chunk per layer: prefetch the next layer
+  int prefetched_layer_ = -1;   // layer whose copies are already queued in its buffer
   int step_stage_base_ = 0;  // staging buffer of the open step's first chunk
   // Device views into the workspace for the current step.
   SeqInfo* d_seqs_ = nullptr;

@@ -425,9 +425,12 @@ class PagedModel:
         blocks = -(-capacity // T) + 2
         dtype = next(self.model.parameters()).dtype
         device = input_ids.device
+        # Staged mode: each buffer holds a whole layer's host blocks, so every step streams
+        # one chunk per layer and queues the next layer's copies under the current layer.
         dec = PagedDecoder(
             num_layers=layers, num_query_heads=hq, num_kv_heads=hkv, head_dim=d, tokens_per_block=T, dtype=dtype,
-            device=device, pool_blocks=rows * blocks, host_blocks=rows * blocks, staging_blocks=64,
+            device=device, pool_blocks=rows * blocks, host_blocks=rows * blocks,
+            staging_blocks=rows * blocks if self.stream_mode == "staged" else 64,
             staging_buffers=2, ram_budget_bytes=self._ram_budget, stream_mode=self.stream_mode,
         )
         pads = (attention_mask.shape[1] - attention_mask.long().sum(dim=1)).tolist()

@@ -31,12 +31,12 @@ class Pair:
     """A PagedDecoder and the oracle driven with the same inputs."""
 
     def __init__(self, *, layers, hq, hkv, d, tpb, dtype, pool_blocks, host_blocks, staging_blocks=1024,
-                 blocks_per_workgroup=16, stream_mode="direct", scale=None, softcap=None):
+                 staging_buffers=2, blocks_per_workgroup=16, stream_mode="direct", scale=None, softcap=None):
         self.dtype = dtype
         self.dec = PagedDecoder(num_layers=layers, num_query_heads=hq, num_kv_heads=hkv, head_dim=d,
                                 tokens_per_block=tpb, dtype=dtype, device="cuda", pool_blocks=pool_blocks,
                                 host_blocks=host_blocks, staging_blocks=staging_blocks,
-                                blocks_per_workgroup=blocks_per_workgroup, stream_mode=stream_mode, scale=scale,
+                                staging_buffers=staging_buffers, blocks_per_workgroup=blocks_per_workgroup, stream_mode=stream_mode, scale=scale,
                                 softcap=softcap)
         self.ora = PagedDecodeOracle(num_layers=layers, num_query_heads=hq, num_kv_heads=hkv, head_dim=d,
                                      tokens_per_block=tpb, scale=scale, softcap=softcap)
@@ -150,6 +150,31 @@ def test_config4_mistral_layer_window_bf16(mode, staging_blocks):
             st = p.dec.pool.step_stats()
             assert st["host_blocks"] == 4 * 96  # in-window host blocks only
     assert p.ora.host_ids(p.sids[0], 0)[0] == (ctx + 3 - window) // 32
+
+
+@pytest.mark.parametrize("staging_blocks,staging_buffers", [(2048, 2), (2048, 3), (40, 2)])
+def test_staged_layers_prefetch_and_chunks(staging_blocks, staging_buffers):
+    """Staged mode over four layers. With a step's host blocks in one chunk, each layer's
+    copies are queued right after the previous layer's attention, into the next buffer (two
+    and three buffers). With a small staging buffer the step falls back to several chunks per
+    layer, copied layer by layer. Outputs, gather lists and placement match the oracle."""
+    g = torch.Generator().manual_seed(11)
+    ctx = [1200, 2500, 700]
+    p = Pair(layers=4, hq=8, hkv=2, d=64, tpb=32, dtype=torch.float16, pool_blocks=3 * 12,
+             host_blocks=sum(c // 32 + 8 for c in ctx), staging_blocks=staging_blocks,
+             staging_buffers=staging_buffers, stream_mode="staged")
+    for c in ctx:
+        p.add(ctx=c, capacity=c + 64, gen=g, vram_budget=8 * MIB16, ram_budget=1024 * MIB16, recent_window=7,
+              policy="recent_only")
+    errs = []
+    for step in range(40):
+        _, _, err = p.step(g, compute=step % 8 == 0 or step >= 37)
+        if err is not None:
+            errs.append(err)
+        st = p.dec.pool.step_stats()
+        assert st["host_blocks"] > 100
+        assert (st["chunks"] == 1) if staging_blocks >= 2048 else (st["chunks"] > 1)
+    assert len(errs) == 8
 
 
 @pytest.mark.parametrize("mode", ["direct", "staged"])
