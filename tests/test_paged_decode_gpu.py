@@ -66,8 +66,9 @@ class Pair:
         self.dec.set_lo(sid, lo)
         self.ora.set_lo(sid, lo)
 
-    def step(self, gen, *, compute=True, scale=0.5, sids=None):
+    def step(self, gen, *, compute=True, scale=0.5, sids=None, order=None):
         sids = self.sids if sids is None else sids
+        order = list(range(self.layers)) if order is None else order
         S = sum(self.dec.sessions[s].rows for s in sids)
         qs, ks, vs = [], [], []
         for _ in range(self.layers):
@@ -75,7 +76,9 @@ class Pair:
             ks.append((torch.randn(S, self.hkv, self.d, generator=gen) * scale).to(self.dtype))
             vs.append((torch.randn(S, self.hkv, self.d, generator=gen) * scale).to(self.dtype))
         self.dec.begin_step(sids)
-        outs = [self.dec.decode_layer(l, qs[l].cuda(), ks[l].cuda(), vs[l].cuda()) for l in range(self.layers)]
+        outs = [None] * self.layers
+        for l in order:
+            outs[l] = self.dec.decode_layer(l, qs[l].cuda(), ks[l].cuda(), vs[l].cuda())
         gather = [self.dec.step_host_blocks(i) for i in range(S)]
         res = self.dec.end_step()
         ref = self.ora.step(sids, [np32(x) for x in qs], [np32(x) for x in ks], [np32(x) for x in vs],
@@ -152,12 +155,15 @@ def test_config4_mistral_layer_window_bf16(mode, staging_blocks):
     assert p.ora.host_ids(p.sids[0], 0)[0] == (ctx + 3 - window) // 32
 
 
-@pytest.mark.parametrize("staging_blocks,staging_buffers", [(2048, 2), (2048, 3), (40, 2)])
-def test_staged_layers_prefetch_and_chunks(staging_blocks, staging_buffers):
+@pytest.mark.parametrize("staging_blocks,staging_buffers,order", [
+    (2048, 2, None), (2048, 3, None), (40, 2, None), (2048, 2, [2, 0, 3, 1]), (2048, 3, [3, 1, 0, 2])])
+def test_staged_layers_prefetch_and_chunks(staging_blocks, staging_buffers, order):
     """Staged mode over four layers. With a step's host blocks in one chunk, each layer's
     copies are queued right after the previous layer's attention, into the next buffer (two
     and three buffers). With a small staging buffer the step falls back to several chunks per
-    layer, copied layer by layer. Outputs, gather lists and placement match the oracle."""
+    layer, copied layer by layer. Layers decoded out of order abandon the queued copies and
+    reuse buffers; the results must not change. Outputs, gather lists and placement match
+    the oracle."""
     g = torch.Generator().manual_seed(11)
     ctx = [1200, 2500, 700]
     p = Pair(layers=4, hq=8, hkv=2, d=64, tpb=32, dtype=torch.float16, pool_blocks=3 * 12,
@@ -168,7 +174,7 @@ def test_staged_layers_prefetch_and_chunks(staging_blocks, staging_buffers):
               policy="recent_only")
     errs = []
     for step in range(40):
-        _, _, err = p.step(g, compute=step % 8 == 0 or step >= 37)
+        _, _, err = p.step(g, compute=step % 8 == 0 or step >= 37, order=order)
         if err is not None:
             errs.append(err)
         st = p.dec.pool.step_stats()
