@@ -206,15 +206,21 @@ int PagedKV::init() {
   PGR_HIP(hipStreamCreateWithFlags(&copy_stream_, hipStreamNonBlocking));
   buf_free_.resize(cfg_.staging_buffers);
   chunk_ready_.resize(cfg_.staging_buffers);
+  // Ordering events. They order GPU work against GPU work, or tell the host that the GPU has
+  // finished reading a pinned buffer; none guards device writes that the host then reads
+  // (the mass read-back synchronizes its stream). So none needs the system-scope release
+  // at record time, which writes back the caches: on the plan upload event that cost about
+  // 10 us per step between the upload and the attention launch.
+  const unsigned ev_flags = hipEventDisableTiming | hipEventDisableSystemFence;
   for (int i = 0; i < cfg_.staging_buffers; ++i) {
-    PGR_HIP(hipEventCreateWithFlags(&buf_free_[i], hipEventDisableTiming));
-    PGR_HIP(hipEventCreateWithFlags(&chunk_ready_[i], hipEventDisableTiming));
+    PGR_HIP(hipEventCreateWithFlags(&buf_free_[i], ev_flags));
+    PGR_HIP(hipEventCreateWithFlags(&chunk_ready_[i], ev_flags));
   }
-  PGR_HIP(hipEventCreateWithFlags(&plan_uploaded_, hipEventDisableTiming));
-  PGR_HIP(hipEventCreateWithFlags(&stage_copies_done_, hipEventDisableTiming));
-  PGR_HIP(hipEventCreateWithFlags(&compute_mark_, hipEventDisableTiming));
-  PGR_HIP(hipEventCreateWithFlags(&copy_mark_, hipEventDisableTiming));
-  for (IndexBuf& b : index_bufs_) PGR_HIP(hipEventCreateWithFlags(&b.done, hipEventDisableTiming));
+  PGR_HIP(hipEventCreateWithFlags(&plan_uploaded_, ev_flags));
+  PGR_HIP(hipEventCreateWithFlags(&stage_copies_done_, ev_flags));
+  PGR_HIP(hipEventCreateWithFlags(&compute_mark_, ev_flags));
+  PGR_HIP(hipEventCreateWithFlags(&copy_mark_, ev_flags));
+  for (IndexBuf& b : index_bufs_) PGR_HIP(hipEventCreateWithFlags(&b.done, ev_flags));
   {
     std::vector<void*> bases(pool_);
     bases.insert(bases.end(), host_dev_.begin(), host_dev_.end());
