@@ -147,8 +147,11 @@ typedef struct pgr_kv_config_s {
 
 /* How decode reads host-resident blocks. DIRECT: the attention kernel reads them in place from
  * the pinned host mirror (mapped into the device address space) over the host link, in the
- * same launch as the HBM-resident blocks. STAGED: runs of host blocks are copied into an HBM
- * staging ring with hipMemcpyAsync on a side stream, double-buffered against the kernel. */
+ * same launch as the HBM-resident blocks. STAGED: a copy kernel on the store's side stream
+ * copies them into an HBM staging ring, double-buffered against the attention kernel. When a
+ * step's host blocks fit one buffer and staging_buffers >= 2, pgr_kv_decode_layer(l) also
+ * queues layer l+1's copies right after layer l's attention, so that they run under the
+ * caller's work between the two layers. */
 #define PGR_STREAM_DIRECT 0
 #define PGR_STREAM_STAGED 1
 

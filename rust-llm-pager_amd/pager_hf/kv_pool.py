@@ -3,7 +3,8 @@
 One NativeKVPool owns, for every layer, an HBM slot pool, a pinned host mirror and an HBM
 staging ring, plus the per-session block tables. ``stream_mode="direct"`` (default) has the
 decode kernel read host-resident blocks in place over the host link; ``"staged"`` copies
-them into the staging ring first. Sessions are groups of rows that share one
+them into the staging ring first (and, when one buffer holds a layer's host blocks, queues
+the next layer's copies under the current layer). Sessions are groups of rows that share one
 placement (the reference's one-PagedModel-per-session model, kv_block_store.py:36-56).
 """
 from __future__ import annotations
