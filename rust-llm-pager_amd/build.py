@@ -20,7 +20,10 @@ ARCH = "gfx950"
 # Packed FP32 instructions stay disabled for all device code. MFMA results live in VGPRs
 # (gfx950 allows it): the decode kernels rescale their accumulators with VALU ops, and
 # AGPR accumulators would cost a copy in and out per tile.
-DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-mllvm", "-amdgpu-mfma-vgpr-form=1"]
+# -amdgpu-kernarg-preload-count: leading kernel arguments arrive preloaded in SGPRs (gfx950),
+# so a kernel's first dependent loads do not wait for a load of its argument block.
+DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-mllvm", "-amdgpu-mfma-vgpr-form=1",
+                "-mllvm", "-amdgpu-kernarg-preload-count=16"]
 
 # (source, language, extra flags)
 SOURCES = [

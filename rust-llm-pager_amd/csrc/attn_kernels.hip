@@ -543,13 +543,17 @@ struct PagedRing {
   static constexpr int NB = 3;  // register tiles per wave
 };
 
+// The three pointers the first loads depend on come as separate leading arguments: the build
+// preloads leading kernel arguments into SGPRs, so a workgroup issues its work-item load
+// without first loading the argument block (one dependent memory hop less at start-up).
 template <class Ty, int D, bool kMass>
-__global__ __launch_bounds__(256) void paged_attn_kernel(PagedArgs a) {
+__global__ __launch_bounds__(256) void paged_attn_kernel(const WorkItem* __restrict__ work, uint16_t* pool,
+                                                         const uint16_t* stage, PagedArgs a) {
   constexpr int NB = PagedRing<D>::NB;
   constexpr int kWaveEntries = kMaxWorkEntries / kWaves;  // entries one wave folds at most
   __shared__ MergeSmem<D> sm;
   __shared__ float mass_sm[kMass ? kWaves : 1][kWaveEntries][2][kMaxRep];
-  const WorkItem* wi = a.work + blockIdx.x;
+  const WorkItem* wi = work + blockIdx.x;
   const int h = blockIdx.y;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
@@ -595,7 +599,7 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(PagedArgs a) {
   auto fetch = [&](Tile<D>& t, TileMeta& mt) {
     const int slot = fe == 0 ? en0.slot : fe == 1 ? en1.slot : fe == 2 ? en2.slot : en3.slot;
     const int bid = fe == 0 ? en0.block_id : fe == 1 ? en1.block_id : fe == 2 ? en2.block_id : en3.block_id;
-    const uint16_t* rb = slot >= 0 ? a.pool + (size_t)slot * rec : a.stage + (size_t)(-slot - 1) * rec;
+    const uint16_t* rb = slot >= 0 ? pool + (size_t)slot * rec : stage + (size_t)(-slot - 1) * rec;
     const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(rb + head_off), (short)0, nf < tiles ? 0x7fffffff : 0, kBufferFlags);
     const uint32_t sk = (uint32_t)(ftb * 16 * D * 2);
@@ -695,7 +699,7 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(PagedArgs a) {
   // block record. No workgroup of this launch reads that position (work covers [lo, hi)).
   if (append_slot >= 0 && threadIdx.x < D) {
     const size_t src = ((size_t)seq * a.hkv + h) * D + threadIdx.x;
-    uint16_t* dst = a.pool + (size_t)append_slot * rec + head_off + (size_t)append_pos * D + threadIdx.x;
+    uint16_t* dst = pool + (size_t)append_slot * rec + head_off + (size_t)append_pos * D + threadIdx.x;
     dst[0] = a.k_new[src];
     dst[v_off] = a.v_new[src];
   }
@@ -717,7 +721,7 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(PagedArgs a) {
 constexpr int kMergeBatch = 8;
 
 template <class Ty, int D>
-__global__ __launch_bounds__(256) void paged_merge_kernel(PagedArgs a) {
+__global__ __launch_bounds__(256) void paged_merge_kernel(const SeqInfo* __restrict__ seqs, PagedArgs a) {
   constexpr int kLanes = D / 2;          // threads per partial group (two dims each)
   constexpr int G = 256 / kLanes;        // partial groups
   constexpr int kU = kMergeBatch;
@@ -727,7 +731,7 @@ __global__ __launch_bounds__(256) void paged_merge_kernel(PagedArgs a) {
   const int tid = threadIdx.x;
   const int c = tid % kLanes, grp = tid / kLanes;
   const int hq = a.hq, h = qh / a.n_rep;
-  const SeqInfo* si = a.seqs + seq;
+  const SeqInfo* si = seqs + seq;  // preloaded leading argument, as in paged_attn_kernel
   const int P = si->partial_count, base = si->partial_base;  // P >= 1: every sequence has a work item
   const size_t kv_row = ((size_t)seq * a.hkv + h) * D;
 
@@ -914,9 +918,9 @@ template <class Ty, int D>
 hipError_t launch_paged_t(const PagedArgs& a, int n_work, bool mass, hipStream_t stream) {
   dim3 grid(n_work, a.hkv);
   if (mass) {
-    paged_attn_kernel<Ty, D, true><<<grid, 256, 0, stream>>>(a);
+    paged_attn_kernel<Ty, D, true><<<grid, 256, 0, stream>>>(a.work, a.pool, a.stage, a);
   } else {
-    paged_attn_kernel<Ty, D, false><<<grid, 256, 0, stream>>>(a);
+    paged_attn_kernel<Ty, D, false><<<grid, 256, 0, stream>>>(a.work, a.pool, a.stage, a);
   }
   return hipGetLastError();
 }
@@ -1047,7 +1051,7 @@ hipError_t launch_paged_merge(int dtype, int d, const PagedLaunch& p, int n_seq,
   a.scale = p.scale;
   a.softcap = p.softcap;
   dim3 grid(n_seq, p.hq);
-#define PGR_MERGE(TY, DD) paged_merge_kernel<TY, DD><<<grid, 256, 0, stream>>>(a)
+#define PGR_MERGE(TY, DD) paged_merge_kernel<TY, DD><<<grid, 256, 0, stream>>>(a.seqs, a)
   if (dtype == kF16) {
     if (d == 32) PGR_MERGE(F16, 32);
     else if (d == 64) PGR_MERGE(F16, 64);
