@@ -40,7 +40,7 @@ def draw_contexts(seed, batch, lo, hi):
     return torch.randint(lo, hi + 1, (batch,), generator=g).tolist()
 
 
-def build(steps_total, staging_blocks=2048, staging_buffers=3, blocks_per_wg=16, resident_blocks=None,
+def build(steps_total, staging_blocks=2048, staging_buffers=3, blocks_per_wg=32, resident_blocks=None,
           target_wg=0, layers=1, stream_mode="direct"):
     import torch
 

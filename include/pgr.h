@@ -140,7 +140,7 @@ typedef struct pgr_kv_config_s {
   int64_t host_records;     /* pinned host records per layer */
   int64_t staging_slots;    /* records per staging buffer */
   int32_t staging_buffers;  /* ring depth, >= 1 (2 = double buffering) */
-  int32_t blocks_per_workgroup; /* most block entries per workgroup (4..16) */
+  int32_t blocks_per_workgroup; /* most block entries per workgroup (4..32; 0 = 32) */
   int32_t target_workgroups;    /* workgroups a launch aims for (0 = a multiple of the CU count) */
   int32_t stream_mode;          /* PGR_STREAM_DIRECT (0) or PGR_STREAM_STAGED (1), see below */
 } pgr_kv_config_t;

@@ -571,11 +571,11 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(const WorkItem* __restr
   const uint32_t k_lane = (uint32_t)(n * D + (D / 4) * g) * 2u;
   const uint32_t v_lane = (uint32_t)(4 * g * D + (D / 16) * n) * 2u;
 
-  // This wave's entries wave, wave+4, wave+8, wave+12 (slot, block id), held in SGPRs.
-  // Entries past entry_count are never fetched (the slots exist in every work item).
-  static_assert(kWaveEntries == 4, "one wave folds at most four entries");
-  const BlockEntry en0 = wi->entries[wave], en1 = wi->entries[wave + kWaves];
-  const BlockEntry en2 = wi->entries[wave + 2 * kWaves], en3 = wi->entries[wave + 3 * kWaves];
+  // This wave's entries are wave, wave+4, wave+8, ... (slot, block id). The one being
+  // fetched and the next one sit in SGPRs; the one after is read (a scalar load) when a
+  // block starts, a block ahead of its use. Entries past entry_count are never fetched (the
+  // slots exist in every work item).
+  BlockEntry ecur = wi->entries[wave], enxt = wi->entries[wave + kWaves];
 
   u32x4 q[D / 32];  // loaded behind the first tile (below)
 
@@ -597,8 +597,7 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(const WorkItem* __restr
   // last tile goes through an empty buffer resource and returns at once with zeros.
   int nf = 0, fe = 0, ftb = 0;
   auto fetch = [&](Tile<D>& t, TileMeta& mt) {
-    const int slot = fe == 0 ? en0.slot : fe == 1 ? en1.slot : fe == 2 ? en2.slot : en3.slot;
-    const int bid = fe == 0 ? en0.block_id : fe == 1 ? en1.block_id : fe == 2 ? en2.block_id : en3.block_id;
+    const int slot = ecur.slot, bid = ecur.block_id;
     const uint16_t* rb = slot >= 0 ? pool + (size_t)slot * rec : stage + (size_t)(-slot - 1) * rec;
     const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(rb + head_off), (short)0, nf < tiles ? 0x7fffffff : 0, kBufferFlags);
@@ -611,6 +610,8 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(const WorkItem* __restr
     if (++ftb == tpb) {
       ftb = 0;
       ++fe;
+      ecur = enxt;
+      if (fe + 1 < kWaveEntries) enxt = wi->entries[wave + (fe + 1) * kWaves];
     }
   };
 
@@ -685,7 +686,7 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(const WorkItem* __restr
   if constexpr (kMass) {
     if (g == 0 && real) {
       for (int e = 0; e < my_blocks; ++e) {
-        const int bid = e == 0 ? en0.block_id : e == 1 ? en1.block_id : e == 2 ? en2.block_id : en3.block_id;
+        const int bid = wi->entries[wave + e * kWaves].block_id;
         if (bid < n_mass) {
           const size_t mi = ((size_t)seq * a.hq + qh) * a.mass_stride + bid;
           a.mass_m[mi] = mass_sm[wave][e][0][n];

@@ -260,7 +260,7 @@ void* pgr_kv_create(const pgr_kv_config_t* c) {
   cfg.host_records = c->host_records;
   cfg.staging_slots = c->staging_slots;
   cfg.staging_buffers = c->staging_buffers;
-  cfg.blocks_per_workgroup = c->blocks_per_workgroup > 0 ? c->blocks_per_workgroup : 16;
+  cfg.blocks_per_workgroup = c->blocks_per_workgroup > 0 ? c->blocks_per_workgroup : 32;
   cfg.target_workgroups = c->target_workgroups > 0 ? c->target_workgroups : 0;
   cfg.stream_mode = c->stream_mode;
   auto* kv = new (std::nothrow) pgr::PagedKV(cfg);

@@ -867,11 +867,13 @@ int PagedKV::begin_step(const int32_t* sids, int n, hipStream_t stream) {
   step_stage_base_ = stage_base_;
   stage_base_ = (stage_base_ + (prefetch_step_ ? cfg_.num_layers : n_chunks_)) % cfg_.staging_buffers;
   const int n_launch = std::max(1, n_chunks_);
-  // Work items. Each launch is cut into about target_wg / Hkv work items of nearly equal
-  // size, so that every CU streams the same number of bytes in one round of workgroups;
-  // each sequence gets work items in proportion to its entries in that launch (at most
-  // E_max entries each, at least one entry per wave when the launch is small). A sequence
-  // with nothing stored in scope gets one empty work item: its workgroup runs the merge.
+  // Work items. A launch is cut into whole rounds of target_wg / Hkv work items of nearly
+  // equal size: the fewest rounds whose items hold at most E_max entries each, so that
+  // every CU streams the same number of bytes and no round runs part-full (a few items past
+  // a whole round start a straggler round of their own). A small launch gets at least one
+  // entry per wave instead. Each sequence gets work items in proportion to its entries in
+  // that launch, by largest remainders so that the items add up exactly. A sequence with
+  // nothing stored in scope gets one empty work item: its workgroup runs the merge.
   std::vector<int> seq_wg(seqs_.size(), 0);
   std::vector<int> seq_entries(seqs_.size(), 0);
   for (const Pending& pe : pend) ++seq_entries[pe.seq];
@@ -895,17 +897,46 @@ int PagedKV::begin_step(const int32_t* sids, int n, hipStream_t stream) {
     launch_work_begin_[L] = (int)work_.size();
     const auto& idx = by_launch[L];
     const int64_t N = (int64_t)idx.size();
-    const int64_t want_items = std::max<int64_t>(1, target_wg / cfg_.kv_heads);
-    const int64_t items = std::max<int64_t>((N + E_max - 1) / E_max, std::min<int64_t>(want_items, (N + kWaves - 1) / kWaves));
-    size_t i = 0;
+    const int64_t per_round = std::max<int64_t>(1, target_wg / cfg_.kv_heads);
+    int64_t items;
+    if (N <= per_round * kWaves) {
+      items = std::max<int64_t>(1, (N + kWaves - 1) / kWaves);
+    } else {
+      const int64_t rounds = (N + (int64_t)E_max * per_round - 1) / ((int64_t)E_max * per_round);
+      items = rounds * per_round;
+    }
+    // Items per sequence run: proportional shares, at least ceil(ns / E_max) and at most ns
+    // each, the remaining items to the largest remainders.
+    std::vector<int64_t> run_ns, run_ws;
+    std::vector<double> run_rem;
+    for (size_t i = 0; i < idx.size();) {
+      size_t e = i;
+      while (e < idx.size() && pend[idx[e]].seq == pend[idx[i]].seq) ++e;
+      run_ns.push_back((int64_t)(e - i));
+      i = e;
+    }
+    int64_t assigned = 0;
+    for (int64_t ns : run_ns) {
+      const double q = (double)ns * (double)items / (double)std::max<int64_t>(N, 1);
+      int64_t w = std::max<int64_t>((int64_t)q, std::max<int64_t>(1, (ns + E_max - 1) / E_max));
+      w = std::min<int64_t>(w, ns);
+      run_ws.push_back(w);
+      run_rem.push_back(q - (double)w);
+      assigned += w;
+    }
+    std::vector<size_t> order(run_ns.size());
+    for (size_t r = 0; r < order.size(); ++r) order[r] = r;
+    std::stable_sort(order.begin(), order.end(), [&](size_t x, size_t y) { return run_rem[x] > run_rem[y]; });
+    for (size_t k = 0; assigned < items && k < order.size(); ++k)
+      if (run_ws[order[k]] < run_ns[order[k]]) {
+        ++run_ws[order[k]];
+        ++assigned;
+      }
+    size_t i = 0, run = 0;
     while (i < idx.size()) {
       const int seq = pend[idx[i]].seq;
-      size_t e = i;
-      while (e < idx.size() && pend[idx[e]].seq == seq) ++e;
-      const int64_t ns = (int64_t)(e - i);
-      int64_t ws = (int64_t)std::llround((double)ns * (double)items / (double)std::max<int64_t>(N, 1));
-      ws = std::max<int64_t>(ws, std::max<int64_t>(1, (ns + E_max - 1) / E_max));
-      ws = std::min<int64_t>(ws, ns);
+      const int64_t ns = run_ns[run], ws = run_ws[run];
+      ++run;
       for (int64_t k = 0; k < ws; ++k) {
         const int64_t cnt = ns / ws + (k < ns % ws ? 1 : 0);
         WorkItem w = new_item(seq);

@@ -41,7 +41,7 @@ struct PagedKVConfig {
   int64_t host_records = 0;      // pinned host records per layer
   int64_t staging_slots = 0;     // records per staging buffer
   int staging_buffers = 2;       // ring depth
-  int blocks_per_workgroup = 16; // most block entries folded by one workgroup (4 waves)
+  int blocks_per_workgroup = 32; // most block entries folded by one workgroup (4 waves)
   int target_workgroups = 0;     // workgroups a launch aims for (0: a multiple of the CU count)
   int stream_mode = 0;           // 0: kernels read host blocks in place; 1: staged copies
 };

@@ -33,8 +33,8 @@ struct BlockEntry {
   int32_t block_id;  // logical block id within the sequence; first token = block_id * tokens_per_block
 };
 
-// Block entries one workgroup folds at most (4 waves x 4 blocks).
-constexpr int kMaxWorkEntries = 16;
+// Block entries one workgroup folds at most (4 waves x 8 blocks).
+constexpr int kMaxWorkEntries = 32;
 
 // One workgroup's share of a paged decode step (times num_kv_heads via blockIdx.y). Self-
 // contained, so a workgroup needs a single (scalar) read before it issues its K/V loads.

@@ -52,7 +52,7 @@ class NativeKVPool:
         host_blocks: int,
         staging_blocks: int = 2048,
         staging_buffers: int = 2,
-        blocks_per_workgroup: int = 16,
+        blocks_per_workgroup: int = 32,
         target_workgroups: int = 0,
         stream_mode: str = "direct",
     ):

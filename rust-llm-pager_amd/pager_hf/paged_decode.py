@@ -63,7 +63,7 @@ class PagedDecoder:
         staging_blocks: int = 2048,
         staging_buffers: int = 2,
         ram_budget_bytes: int | None = None,
-        blocks_per_workgroup: int = 16,
+        blocks_per_workgroup: int = 32,
         target_workgroups: int = 0,
         scale: float | None = None,
         softcap: float | None = None,

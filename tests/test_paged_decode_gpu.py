@@ -31,7 +31,7 @@ class Pair:
     """A PagedDecoder and the oracle driven with the same inputs."""
 
     def __init__(self, *, layers, hq, hkv, d, tpb, dtype, pool_blocks, host_blocks, staging_blocks=1024,
-                 staging_buffers=2, blocks_per_workgroup=16, stream_mode="direct", scale=None, softcap=None):
+                 staging_buffers=2, blocks_per_workgroup=32, stream_mode="direct", scale=None, softcap=None):
         self.dtype = dtype
         self.dec = PagedDecoder(num_layers=layers, num_query_heads=hq, num_kv_heads=hkv, head_dim=d,
                                 tokens_per_block=tpb, dtype=dtype, device="cuda", pool_blocks=pool_blocks,
@@ -181,6 +181,31 @@ def test_staged_layers_prefetch_and_chunks(staging_blocks, staging_buffers, orde
         assert st["host_blocks"] > 100
         assert (st["chunks"] == 1) if staging_blocks >= 2048 else (st["chunks"] > 1)
     assert len(errs) == 8
+
+
+@pytest.mark.parametrize("mode", ["direct", "staged"])
+def test_work_items_of_many_blocks(mode):
+    """Work items of more than 16 blocks: 16-token blocks, batch 12 at 7k-14k tokens (about
+    8,000 in-scope blocks for one round of work items, 3 workgroups per CU), so a wave folds
+    five or six blocks and reads their entries one block ahead. The planner sizes items in
+    whole rounds. A scoring policy checks the per-block mass as well."""
+    g = torch.Generator().manual_seed(21)
+    ctx = torch.randint(7000, 14001, (12,), generator=g).tolist()
+    p = Pair(layers=1, hq=8, hkv=2, d=64, tpb=16, dtype=torch.bfloat16, pool_blocks=12 * 40,
+             host_blocks=sum(c // 16 + 16 for c in ctx), staging_blocks=8192, stream_mode=mode)
+    for c in ctx:
+        p.add(ctx=c, capacity=c + 64, gen=g, vram_budget=32 * MIB16, ram_budget=4096 * MIB16, recent_window=8,
+              rebalance_interval=4, policy="sinks_heavy_hitter")
+    per_round = 3 * torch.cuda.get_device_properties(0).multi_processor_count // 2  # workgroups / Hkv
+    for step in range(6):
+        res, ref, err = p.step(g)
+        st = p.dec.pool.step_stats()
+        assert st["work_items"] % per_round == 0
+        assert st["host_blocks"] + st["resident_tokens"] // 16 > 16 * st["work_items"]  # > 16 blocks per item
+        for sid in p.sids:
+            got = np.array(res[sid]["block_attention"])
+            want = np.array(ref["placement"][sid]["scores"])
+            assert np.abs(got - want).max() < 2e-5
 
 
 @pytest.mark.parametrize("mode", ["direct", "staged"])
