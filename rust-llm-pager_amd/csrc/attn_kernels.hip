@@ -27,7 +27,6 @@
 //
 // P is rounded to the K/V element type before the P.V product, as the reference does
 // (streaming_attention.py:178, :347, :428).
-#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include "pgr_common.h"
