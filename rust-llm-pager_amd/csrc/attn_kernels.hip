@@ -458,6 +458,10 @@ struct PagedArgs {
   uint16_t* pool;         // layer pool base
   const uint16_t* stage;  // staging base
   const WorkItem* work;
+  WorkItem* work_out;     // first launch of a step: device copy of the plan (see PagedLaunch)
+  const void* aux_src;
+  void* aux_dst;
+  int64_t aux_vec;
   const SeqInfo* seqs;
   float* pm;              // [slot][Hq], log2 units
   float* pl;
@@ -569,6 +573,21 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(const WorkItem* __restr
   const int append_slot = wi->append_slot, append_pos = wi->append_pos;
   const uint32_t k_lane = (uint32_t)(n * D + (D / 4) * g) * 2u;
   const uint32_t v_lane = (uint32_t)(4 * g * D + (D / 16) * n) * 2u;
+
+  if (a.work_out != nullptr) {
+    // First launch of a step: `work` is the pinned plan buffer. This workgroup's work item
+    // (head 0 only) and its share of the rest of the plan go to the device copy that every
+    // later kernel of the step reads. Issued first, beside the scalar loads of the work item
+    // that the first fetch waits for anyway.
+    static_assert(sizeof(WorkItem) % 16 == 0, "work items copy as 16-byte vectors");
+    constexpr int kItemVec = (int)(sizeof(WorkItem) / 16);
+    if (h == 0 && (int)threadIdx.x < kItemVec)
+      reinterpret_cast<u32x4*>(a.work_out + blockIdx.x)[threadIdx.x] = reinterpret_cast<const u32x4*>(wi)[threadIdx.x];
+    const int64_t stride = (int64_t)gridDim.x * gridDim.y * blockDim.x;
+    for (int64_t v = ((int64_t)blockIdx.y * gridDim.x + blockIdx.x) * blockDim.x + threadIdx.x; v < a.aux_vec;
+         v += stride)
+      static_cast<u32x4*>(a.aux_dst)[v] = static_cast<const u32x4*>(a.aux_src)[v];
+  }
 
   // This wave's entries are wave, wave+4, wave+8, ... (slot, block id). The one being
   // fetched and the next one sit in SGPRs; the one after is read (a scalar load) when a
@@ -988,13 +1007,17 @@ hipError_t launch_finalize(int dtype, const float* acc, const float* l, void* ou
 
 hipError_t launch_paged(int dtype, int d, const PagedLaunch& p, hipStream_t stream) {
   if (p.n_work == 0) return hipSuccess;
-  PagedArgs a;
+  PagedArgs a{};
   a.q = static_cast<const uint16_t*>(p.q);
   a.k_new = static_cast<const uint16_t*>(p.k_new);
   a.v_new = static_cast<const uint16_t*>(p.v_new);
   a.pool = static_cast<uint16_t*>(p.pool);
   a.stage = static_cast<const uint16_t*>(p.stage);
   a.work = p.work;
+  a.work_out = p.work_out;
+  a.aux_src = p.aux_src;
+  a.aux_dst = p.aux_dst;
+  a.aux_vec = p.aux_vec;
   a.seqs = p.seqs;
   a.pm = p.pm;
   a.pl = p.pl;

@@ -132,7 +132,10 @@ PagedKV::~PagedKV() {
     if (b.host) hipHostFree(b.host);
     if (b.done) hipEventDestroy(b.done);
   }
-  if (plan_host_) hipHostFree(plan_host_);
+  for (PlanBuf& b : plan_bufs_) {
+    if (b.host) hipHostFree(b.host);
+    if (b.read) hipEventDestroy(b.read);
+  }
   if (mass_host_) hipHostFree(mass_host_);
   for (hipEvent_t e : buf_free_) hipEventDestroy(e);
   for (hipEvent_t e : chunk_ready_) hipEventDestroy(e);
@@ -217,6 +220,7 @@ int PagedKV::init() {
     PGR_HIP(hipEventCreateWithFlags(&chunk_ready_[i], ev_flags));
   }
   PGR_HIP(hipEventCreateWithFlags(&plan_uploaded_, ev_flags));
+  for (PlanBuf& b : plan_bufs_) PGR_HIP(hipEventCreateWithFlags(&b.read, ev_flags));
   PGR_HIP(hipEventCreateWithFlags(&stage_copies_done_, ev_flags));
   PGR_HIP(hipEventCreateWithFlags(&compute_mark_, ev_flags));
   PGR_HIP(hipEventCreateWithFlags(&copy_mark_, ev_flags));
@@ -978,8 +982,8 @@ int PagedKV::begin_step(const int32_t* sids, int n, hipStream_t stream) {
     off = align_up(off + bytes, 256);
     return at;
   };
+  // Plan: the per-sequence and per-session arrays, the staging pairs, then the work items.
   const size_t o_seqs = carve(sizeof(SeqInfo) * S);
-  const size_t o_work = carve(sizeof(WorkItem) * std::max<size_t>(work_.size(), 1));
   const size_t o_srows = carve(sizeof(int32_t) * std::max(n, 1));
   const size_t o_sfirst = carve(sizeof(int32_t) * std::max(n, 1));
   // Staged mode: (host record, staging record) per record to stream, chunk by chunk.
@@ -994,6 +998,7 @@ int PagedKV::begin_step(const int32_t* sids, int n, hipStream_t stream) {
   }
   for (int c = 1; c <= n_chunks_; ++c) chunk_pair_begin_[c] = std::max(chunk_pair_begin_[c], chunk_pair_begin_[c - 1]);
   const size_t o_spairs = carve(sizeof(int64_t) * std::max<size_t>(stage_pairs_.size(), 2));
+  const size_t o_work = carve(sizeof(WorkItem) * std::max<size_t>(work_.size(), 1));
   const size_t plan_bytes = off;
   const size_t o_pm = carve(sizeof(float) * (size_t)n_partials_ * hq);
   const size_t o_pl = carve(sizeof(float) * (size_t)n_partials_ * hq);
@@ -1004,19 +1009,29 @@ int PagedKV::begin_step(const int32_t* sids, int n, hipStream_t stream) {
   const size_t o_lf = carve(sizeof(float) * (size_t)S * hq);
   int rc = ensure_workspace(off);
   if (rc != kOk) return rc;
-  // Pinned upload buffer: wait for the previous step's upload before overwriting it.
-  if (plan_bytes > plan_host_bytes_) {
-    PGR_HIP(hipEventSynchronize(plan_uploaded_));
-    if (plan_host_) PGR_HIP(hipHostFree(plan_host_));
-    plan_host_ = nullptr;
-    const size_t want = std::max(plan_bytes, plan_host_bytes_ * 3 / 2);
-    PGR_HIP(hipHostMalloc(&plan_host_, want, hipHostMallocDefault));
-    PGR_HIP(hipHostGetDevicePointer(&plan_host_dev_, plan_host_, 0));
-    plan_host_bytes_ = want;
-  } else {
-    PGR_HIP(hipEventSynchronize(plan_uploaded_));
+  // Pinned plan buffer; wait until the GPU has read it before overwriting it. With several
+  // layers per step the first launch reads the plan early in its step, so one buffer holds
+  // the host back by little, and a launch signature stays the same from step to step (a
+  // captured graph replays). With one layer the first launch is the whole step: the steps
+  // alternate between two buffers, so that the host can plan a step while the GPU runs the
+  // one before.
+  if (cfg_.num_layers == 1) plan_buf_ ^= 1;
+  PlanBuf& pb = plan_bufs_[plan_buf_];
+  if (pb.pending) {
+    PGR_HIP(hipEventSynchronize(pb.read));
+    pb.pending = false;
   }
-  char* h = static_cast<char*>(plan_host_);
+  if (plan_bytes > pb.bytes) {
+    if (pb.host) PGR_HIP(hipHostFree(pb.host));
+    pb.host = nullptr;
+    const size_t want = std::max(plan_bytes, pb.bytes * 3 / 2);
+    PGR_HIP(hipHostMalloc(&pb.host, want, hipHostMallocDefault));
+    PGR_HIP(hipHostGetDevicePointer(&pb.dev, pb.host, 0));
+    pb.bytes = want;
+  }
+  plan_aux_bytes_ = o_work;
+  plan_work_off_ = o_work;
+  char* h = static_cast<char*>(pb.host);
   std::memcpy(h + o_seqs, seqs_.data(), sizeof(SeqInfo) * S);
   std::memcpy(h + o_work, work_.data(), sizeof(WorkItem) * work_.size());
   std::memcpy(h + o_srows, sess_rows.data(), sizeof(int32_t) * n);
@@ -1024,16 +1039,25 @@ int PagedKV::begin_step(const int32_t* sids, int n, hipStream_t stream) {
   if (!stage_pairs_.empty()) std::memcpy(h + o_spairs, stage_pairs_.data(), sizeof(int64_t) * stage_pairs_.size());
   char* d = static_cast<char*>(ws_);
   // A staging copy queued for a layer that was never decoded may still read the previous
-  // step's pair list on the copy stream: the upload waits for it before overwriting the plan.
+  // step's pair list on the copy stream: the plan is not overwritten before it has run.
   if (stage_copy_pending_) {
     PGR_HIP(hipStreamWaitEvent(stream, stage_copies_done_, 0));
     stage_copy_pending_ = false;
   }
-  // plan_bytes is a multiple of 256 (every carve is 256-aligned).
-  const int64_t n_vec = (int64_t)(plan_bytes / 16);
-  plan_upload_kernel<<<(unsigned)((n_vec + 255) / 256), 256, 0, stream>>>(plan_host_dev_, d, n_vec);
-  PGR_HIP(hipGetLastError());
-  PGR_HIP(hipEventRecord(plan_uploaded_, stream));
+  plan_on_device_ = false;
+  if (cfg_.stream_mode == 1) {
+    // Staged mode: the staging copies read the pair list before any attention launch runs,
+    // so the whole plan goes to the workspace first. plan_bytes is a multiple of 256.
+    const int64_t n_vec = (int64_t)(plan_bytes / 16);
+    plan_upload_kernel<<<(unsigned)((n_vec + 255) / 256), 256, 0, stream>>>(pb.dev, d, n_vec);
+    PGR_HIP(hipGetLastError());
+    PGR_HIP(hipEventRecord(plan_uploaded_, stream));
+    PGR_HIP(hipEventRecord(pb.read, stream));
+    pb.pending = true;
+    plan_on_device_ = true;
+  }
+  // Direct mode: the step's first attention launch reads its work items from the pinned
+  // buffer and copies the plan into the workspace for every later kernel (decode_layer).
   d_seqs_ = reinterpret_cast<SeqInfo*>(d + o_seqs);
   d_work_ = reinterpret_cast<WorkItem*>(d + o_work);
   d_sess_rows_ = reinterpret_cast<int32_t*>(d + o_srows);
@@ -1118,6 +1142,20 @@ int PagedKV::decode_layer(int layer, const void* q, const void* k_new, const voi
     }
     pl.work = d_work_ + launch_work_begin_[L];
     pl.n_work = launch_work_end_[L] - launch_work_begin_[L];
+    pl.work_out = nullptr;
+    pl.aux_src = nullptr;
+    pl.aux_dst = nullptr;
+    pl.aux_vec = 0;
+    const bool first_read = !plan_on_device_;  // direct mode, first decode_layer of the step
+    if (first_read) {
+      const PlanBuf& pb = plan_bufs_[plan_buf_];
+      pl.work = reinterpret_cast<const WorkItem*>(static_cast<const char*>(pb.dev) + plan_work_off_) +
+                launch_work_begin_[L];
+      pl.work_out = d_work_ + launch_work_begin_[L];
+      pl.aux_src = pb.dev;
+      pl.aux_dst = ws_;
+      pl.aux_vec = (int64_t)(plan_aux_bytes_ / 16);
+    }
     PendingTiming t{nullptr, nullptr, 0};
     if (timing_) {
       // Timing-only events recorded on the stream right before and after the launch. Without
@@ -1131,6 +1169,12 @@ int PagedKV::decode_layer(int layer, const void* q, const void* k_new, const voi
     }
     PGR_HIP(launch_paged(cfg_.dtype, cfg_.head_dim, pl, stream));
     if (timing_) PGR_HIP(hipEventRecord(t.stop, stream));
+    if (first_read) {
+      PlanBuf& pb = plan_bufs_[plan_buf_];
+      PGR_HIP(hipEventRecord(pb.read, stream));
+      pb.pending = true;
+      plan_on_device_ = true;
+    }
     if (timing_) {
       int64_t ent = 0;
       for (int w = launch_work_begin_[L]; w < launch_work_end_[L]; ++w) ent += work_[w].entry_count;
@@ -1161,7 +1205,7 @@ int PagedKV::step_signature(int64_t* out, int64_t cap) const {
       (int64_t)(uintptr_t)d_pl_, (int64_t)(uintptr_t)d_pacc_, (int64_t)(uintptr_t)d_mass_m_,
       (int64_t)(uintptr_t)d_mass_s_, (int64_t)(uintptr_t)d_mf_, (int64_t)(uintptr_t)d_lf_,
       (int64_t)cfg_.stream_mode, (int64_t)seqs_.size(), (int64_t)step_sids_.size(), (int64_t)mass_stride_,
-      (int64_t)launch_work_begin_.size()};
+      (int64_t)launch_work_begin_.size(), (int64_t)(uintptr_t)plan_bufs_[plan_buf_].dev, (int64_t)plan_on_device_};
   for (size_t L = 0; L < launch_work_begin_.size(); ++L) {
     v.push_back(launch_work_begin_[L]);
     v.push_back(launch_work_end_[L]);

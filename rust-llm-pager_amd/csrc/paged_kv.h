@@ -222,9 +222,20 @@ class PagedKV {
   IndexBuf index_bufs_[kIndexBufs];
   int next_index_buf_ = 0;
   std::vector<int64_t> evict_pairs_, load_pairs_;  // moves of the current apply_tiers call
-  void* plan_host_ = nullptr;  // pinned upload buffer for the step plan
-  void* plan_host_dev_ = nullptr;  // its device mapping
-  size_t plan_host_bytes_ = 0;
+  // The step plan goes to one of two pinned buffers, alternately, so that the host can write
+  // the next step's plan while the GPU still reads this one.
+  struct PlanBuf {
+    void* host = nullptr;  // pinned
+    void* dev = nullptr;   // its device mapping
+    size_t bytes = 0;
+    hipEvent_t read = nullptr;  // after the GPU's last read of this buffer
+    bool pending = false;
+  };
+  PlanBuf plan_bufs_[2];
+  int plan_buf_ = 0;             // buffer of the open step
+  bool plan_on_device_ = false;  // the workspace holds the open step's plan
+  size_t plan_aux_bytes_ = 0;    // plan bytes ahead of the work items
+  size_t plan_work_off_ = 0;     // offset of the work items in the plan
   float* mass_host_ = nullptr;  // pinned readback of the step's block mass
   size_t mass_host_floats_ = 0;
   hipStream_t copy_stream_ = nullptr;

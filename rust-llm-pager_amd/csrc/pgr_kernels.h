@@ -37,6 +37,13 @@ struct PagedLaunch {
   void* pool;
   const void* stage;
   const WorkItem* work;
+  // The step's first launch (direct mode) reads `work` from the pinned plan buffer and copies
+  // it to work_out, and the aux_vec 16-byte vectors at aux_src (the rest of the plan) to
+  // aux_dst, for the kernels after it. Null / 0 otherwise.
+  WorkItem* work_out = nullptr;
+  const void* aux_src = nullptr;
+  void* aux_dst = nullptr;
+  int64_t aux_vec = 0;
   const SeqInfo* seqs;
   float* pm;
   float* pl;

@@ -29,6 +29,7 @@ from __future__ import annotations
 
 import logging
 import threading
+from collections import OrderedDict
 from contextlib import contextmanager
 from dataclasses import dataclass
 
@@ -125,10 +126,8 @@ class PagedModel:
         if use_hip_graphs and stream_mode != "direct":
             raise ValueError("use_hip_graphs needs stream_mode='direct' (staged copies run on a second stream)")
         self.use_hip_graphs = use_hip_graphs
-        self._graph = None
-        self._graph_sig = None
+        self._graphs: OrderedDict = OrderedDict()  # launch signature -> (graph, (ids, pos, logits))
         self._graph_pool = None
-        self._graph_io = None
         self._graph_warm = False
         self.model = model
         self.tokens_per_block = tokens_per_block
@@ -178,7 +177,7 @@ class PagedModel:
             self._lock.release()
 
     def _close(self) -> None:
-        self._graph = self._graph_sig = self._graph_io = None
+        self._graphs.clear()
         if self._decoder is not None:
             self._decoder.pool.close()
         self._decoder = None
@@ -542,12 +541,17 @@ class PagedModel:
         }
         return logits, step
 
+    # Captured graphs kept at once: a step whose signature was seen recently (a sequence
+    # returning to an earlier block count, beam rows) replays without a new capture.
+    _MAX_GRAPHS = 4
+
     def _graph_forward(self, input_ids: torch.Tensor, position_ids: torch.Tensor) -> torch.Tensor:
         """The decode forward of an open step from a captured HIP graph. The native launches
-        read the step's plan from the store's workspace, uploaded by begin_step, so a graph
-        stays valid while the launch signature (workspace pointers, grids, mass buffer) and
-        the input shapes are unchanged. Returns the last-position logits [B, V]; the tensor
-        is reused by the next step."""
+        read the step's plan from the store's pinned plan buffer and workspace, written by
+        begin_step, so a graph stays valid while the launch signature (plan buffer and
+        workspace pointers, grids, mass buffer) and the input shapes are unchanged: one graph
+        is kept per signature. Returns the last-position logits [B, V]; the tensor is reused
+        by the next replay of the same graph."""
         dec = self._decoder
         mass = dec._mass
         sig = (dec.pool.step_signature(), None if mass is None else (mass.data_ptr(), mass.stride(0)),
@@ -557,9 +561,10 @@ class PagedModel:
             with self._paged_attention():
                 out = self.model(input_ids=input_ids, position_ids=position_ids, use_cache=False, logits_to_keep=1)
             return out.logits[:, -1, :]
-        if self._graph is None or sig != self._graph_sig:
-            # The previous graph stays alive until the new one is captured: its memory pool is
-            # shared, and releasing the last graph of a pool releases the pool.
+        entry = self._graphs.get(sig)
+        if entry is None:
+            # Older graphs stay alive until the new one is captured: the memory pool is shared,
+            # and releasing the last graph of a pool releases the pool.
             ids, pos = input_ids.clone(), position_ids.clone()
             graph = torch.cuda.CUDAGraph()
             if self._graph_pool is None:
@@ -567,13 +572,17 @@ class PagedModel:
             with self._paged_attention():
                 with torch.cuda.graph(graph, pool=self._graph_pool):
                     out = self.model(input_ids=ids, position_ids=pos, use_cache=False, logits_to_keep=1)
-            self._graph, self._graph_sig, self._graph_io = graph, sig, (ids, pos, out.logits)
+            entry = (graph, (ids, pos, out.logits))
+            self._graphs[sig] = entry
+            while len(self._graphs) > self._MAX_GRAPHS:
+                self._graphs.popitem(last=False)
         else:
-            ids, pos, _ = self._graph_io
+            self._graphs.move_to_end(sig)
+            ids, pos, _ = entry[1]
             ids.copy_(input_ids)
             pos.copy_(position_ids)
-        self._graph.replay()
-        return self._graph_io[2][:, -1, :]
+        entry[0].replay()
+        return entry[1][2][:, -1, :]
 
     @staticmethod
     def _position_ids_from_mask(attention_mask: torch.Tensor) -> torch.Tensor:

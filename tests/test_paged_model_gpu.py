@@ -242,7 +242,7 @@ def test_hip_graph_steps_match_eager_steps(policy):
             nxt = torch.argmax(a, dim=-1, keepdim=True)
             assert torch.equal(nxt, torch.argmax(b, dim=-1, keepdim=True)), f"step {step}"
             cur = torch.cat([cur, cur.new_ones((2, 1))], dim=1)
-        assert graph._graph is not None  # steps were replayed from a graph
+        assert len(graph._graphs) > 0  # steps were replayed from captured graphs
     assert worst < 1e-2, worst
     eager.reset()
     graph.reset()
