@@ -228,9 +228,10 @@ int pgr_kv_decode_layer(void* kv, int32_t layer, const void* q, const void* k_ne
 int pgr_kv_end_step(void* kv, int32_t* completed, int32_t* n_completed);
 /* No counterpart in the reference (its decode step is not graph-captured). For callers that
  * capture decode steps in a HIP graph: writes up to cap values describing what the open
- * step's launches take as arguments (workspace pointers, grid sizes, mass stride) and
- * returns their number. A graph captured in a step stays valid for any later step with the
- * same values, since each step's plan is uploaded to the same workspace before replay. */
+ * step's launches take as arguments (plan buffer and workspace pointers, grid sizes, mass
+ * stride) and returns their number. A graph captured in a step stays valid for any later
+ * step with the same values, since pgr_kv_begin_step writes each step's plan to the same
+ * buffers before replay. */
 int pgr_kv_step_signature(void* kv, int64_t* out, int64_t cap);
 /* Attaches a placement handle (pgr_pager_new) to session sid; the store does not own it.
  * scores_from_mass != 0 for attention-scored policies (mass-driven scores). */
