@@ -25,6 +25,7 @@ before the step; uniform over N if the total is not positive).
 """
 from __future__ import annotations
 
+import logging
 from dataclasses import dataclass, field
 
 import torch
@@ -32,6 +33,11 @@ import torch
 import pager as _pager
 
 from .kv_pool import NativeKVPool
+
+logger = logging.getLogger(__name__)
+
+# Warn once host-resident bytes pass this share of ram_budget_bytes (kv_block_store.py:10-13).
+_RAM_BUDGET_WARNING_THRESHOLD = 0.8
 
 _POLICIES_WITHOUT_ATTENTION_SIGNAL = frozenset({"recent_only", "sinks_recent"})  # paged_model.py:40
 
@@ -86,6 +92,7 @@ class PagedDecoder:
             stream_mode=stream_mode,
         )
         self.pool.set_ram_budget(ram_budget_bytes)
+        self._ram_budget = ram_budget_bytes
         self.device = self.pool.device
         self.num_layers = num_layers
         self.num_query_heads = num_query_heads
@@ -174,11 +181,24 @@ class PagedDecoder:
             if rc != 0:
                 raise RuntimeError(f"ram_budget exceeded while placing block {fail_block}")
             moves = {"to_gpu": to_gpu, "to_cpu": to_cpu}
+            host_ids = [b for b in range(n_blocks) if b >= len(tiers) or tiers[b] != 0]
+            if host_ids:  # prompt blocks placed host-side count as offloaded (kv_block_store.py:101-108)
+                self._warn_ram_usage(host_ids[-1])
         if n_tokens:
             for layer in range(self.num_layers):
                 for row in range(s.rows):
                     self.pool.import_tokens(sid, row, layer, keys[layer][row], values[layer][row], n_tokens)
         return moves
+
+    def _warn_ram_usage(self, block_id: int) -> None:
+        """The reference's warning when an offload leaves host-resident bytes above 80% of the
+        RAM budget (kv_block_store.py:101-108)."""
+        if not self._ram_budget:
+            return
+        cpu = self.pool.resident_bytes()[1]
+        if cpu > _RAM_BUDGET_WARNING_THRESHOLD * self._ram_budget:
+            logger.warning("ram_budget usage at %.0f%% after offloading block %d (%.2f MB of %.2f MB budget).",
+                           100.0 * cpu / self._ram_budget, block_id, cpu / 1_000_000, self._ram_budget / 1_000_000)
 
     def num_blocks(self, sid: int) -> int:
         return self.pool.session_info(sid)[1]
@@ -256,6 +276,13 @@ class PagedDecoder:
         if rc != 0:
             bad = next(r[3] for r in rows if r[3] >= 0)
             raise RuntimeError(f"ram_budget exceeded: moving block {bad} to CPU")
+        mo, last_to_cpu = 0, None
+        for _, ng, nc, _, _ in rows:
+            if nc:
+                last_to_cpu = moves[mo + ng + nc - 1]
+            mo += ng + nc
+        if last_to_cpu is not None:
+            self._warn_ram_usage(last_to_cpu)
         if not collect:
             return {}
         results = {}

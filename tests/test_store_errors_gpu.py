@@ -99,7 +99,7 @@ def test_misaligned_import_is_rejected():
         dec.prefill(sid, ks, vs, 50)
 
 
-def test_ram_budget_exceeded_during_placement():
+def test_ram_budget_exceeded_during_placement(caplog):
     """The store's host-RAM budget (kv_block_store.py:86-99): placement that would offload
     past it raises, naming the budget."""
     dec = _dec(ram_budget_bytes=20_000)  # one 16-token block of this geometry is 8 KiB
@@ -113,7 +113,9 @@ def test_ram_budget_exceeded_during_placement():
     assert dec.pool.resident_bytes() == (0, 0)
     sid = dec.add_session(capacity_tokens=400, vram_budget=4 * MIB16, ram_budget=1 << 30, recent_window=3,
                           policy="recent_only")
-    ks, vs = _kv(100)  # 4 in HBM, 2 on the host: within the budget
-    dec.prefill(sid, ks, vs, 100)
+    ks, vs = _kv(100)  # 4 in HBM, 2 on the host: within the budget, above 80% of it
+    with caplog.at_level("WARNING"):
+        dec.prefill(sid, ks, vs, 100)
     assert dec.pool.resident_bytes()[1] == 2 * 8192
+    assert "ram_budget usage at 82% after offloading block 1" in caplog.text
     _step(dec, [sid])
