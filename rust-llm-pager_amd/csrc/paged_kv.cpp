@@ -5,8 +5,9 @@
 // then one Triton launch per 64-block group (two passes for attention-scoring policies).
 // Here one plan per step covers all layers: resident blocks are read in place from the HBM
 // pool; host blocks are read in place from the pinned host mirror by the same kernel over
-// the host link (direct mode), or streamed in contiguous runs into a staging ring on a side
-// stream with one kernel launch per staged chunk (staged mode); a merge kernel follows.
+// the host link (direct mode), or copied by a copy kernel into a staging ring on a side
+// stream, with one attention launch per staged chunk and the next layer's copies queued
+// under the current layer (staged mode); a merge kernel follows.
 #include "paged_kv.h"
 
 #include <algorithm>
@@ -104,10 +105,11 @@ __global__ void stage_copy_kernel(const void* host, void* stage, const int64_t* 
   }
 }
 
-// The step plan, copied from the pinned upload buffer (read in place through its device
-// mapping) into the workspace. A copy kernel on the compute stream, rather than an SDMA copy,
-// keeps the plan upload on the queue that runs the attention: each hand-off between the copy
-// engine and the compute queue cost about 9 and 26 us per step.
+// Staged mode: the step plan, copied from the pinned plan buffer (read in place through its
+// device mapping) into the workspace; in direct mode the step's first attention launch does
+// this copy itself. A copy kernel on the compute stream, rather than an SDMA copy, keeps the
+// upload on the queue that runs the attention: each hand-off between the copy engine and the
+// compute queue cost about 9 and 26 us per step.
 __global__ void plan_upload_kernel(const void* src, void* dst, int64_t n_vec) {
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -212,8 +214,8 @@ int PagedKV::init() {
   // Ordering events. They order GPU work against GPU work, or tell the host that the GPU has
   // finished reading a pinned buffer; none guards device writes that the host then reads
   // (the mass read-back synchronizes its stream). So none needs the system-scope release
-  // at record time, which writes back the caches: on the plan upload event that cost about
-  // 10 us per step between the upload and the attention launch.
+  // at record time, which writes back the caches: on the event between a plan upload and
+  // the attention launch that cost about 2 us per step.
   const unsigned ev_flags = hipEventDisableTiming | hipEventDisableSystemFence;
   for (int i = 0; i < cfg_.staging_buffers; ++i) {
     PGR_HIP(hipEventCreateWithFlags(&buf_free_[i], ev_flags));

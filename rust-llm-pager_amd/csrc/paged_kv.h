@@ -115,8 +115,9 @@ class PagedKV {
                    int64_t accum_stride, float scale, float softcap, hipStream_t stream);
   int end_step(int32_t* completed_sessions, int* n_completed);
   // Everything the open step's launches take as arguments besides the caller's tensors:
-  // workspace pointers, grid sizes, the mass stride. Launches captured in a graph stay valid
-  // for a later step with the same signature (the plan they read is uploaded per step).
+  // plan buffer and workspace pointers, grid sizes, the mass stride. Launches captured in a
+  // graph stay valid for a later step with the same signature (begin_step writes each step's
+  // plan to the same buffers).
   // Returns the number of values (writes at most cap), or kErrState outside a step.
   int step_signature(int64_t* out, int64_t cap) const;
 
