@@ -183,6 +183,37 @@ def test_staged_layers_prefetch_and_chunks(staging_blocks, staging_buffers, orde
     assert len(errs) == 8
 
 
+@pytest.mark.parametrize("mode,layers", [("direct", 1), ("direct", 2), ("staged", 2)])
+def test_sessions_join_and_leave_between_steps(mode, layers):
+    """Sessions join (the step plan grows) and leave (their ids are reused by later
+    sessions) between steps. A single-layer decoder alternates between two pinned plan
+    buffers, a two-layer one keeps one. Every step matches the oracle."""
+    g = torch.Generator().manual_seed(31)
+    p = Pair(layers=layers, hq=8, hkv=2, d=64, tpb=16, dtype=torch.float16, pool_blocks=400, host_blocks=3000,
+             staging_blocks=1024, stream_mode=mode)
+    live = []
+
+    def join():
+        c = int(torch.randint(50, 1500, (1,), generator=g))
+        live.append(p.add(ctx=c, capacity=c + 64, gen=g, vram_budget=6 * MIB16, ram_budget=1024 * MIB16,
+                          recent_window=3, policy="recent_only"))
+
+    for _ in range(3):
+        join()
+    reused = False
+    for step in range(24):
+        if step % 4 == 1:
+            join()
+            reused = reused or live[-1] < max(live[:-1])
+        if step % 6 == 5 and len(live) > 2:
+            sid = live.pop(0)
+            p.dec.remove_session(sid)
+            del p.ora.sessions[sid]
+            p.sids.remove(sid)
+        p.step(g, sids=list(live))
+    assert reused  # a freed session id was handed out again
+
+
 @pytest.mark.parametrize("mode", ["direct", "staged"])
 def test_work_items_of_many_blocks(mode):
     """Work items of more than 16 blocks: 16-token blocks, batch 12 at 7k-14k tokens (about
