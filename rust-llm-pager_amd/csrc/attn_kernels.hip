@@ -473,6 +473,8 @@ struct PagedArgs {
   float* lf;
   int hq, hkv, n_rep, tokens_per_block, mass_stride;
   float scale, softcap;
+  uint32_t* plan_flag;    // merge: pinned word for plan_token (see PagedLaunch), or null
+  uint32_t plan_token;
 };
 
 constexpr float kLog2e = 1.4426950408889634f;
@@ -753,6 +755,10 @@ __global__ __launch_bounds__(256) void paged_merge_kernel(const SeqInfo* __restr
   const SeqInfo* si = seqs + seq;  // preloaded leading argument, as in paged_attn_kernel
   const int P = si->partial_count, base = si->partial_base;  // P >= 1: every sequence has a work item
   const size_t kv_row = ((size_t)seq * a.hkv + h) * D;
+  // The attention launches before this merge have finished: tell the host that the step's
+  // plan buffer is free (a system-scope vector store into pinned host memory).
+  if (a.plan_flag != nullptr && seq == 0 && qh == 0 && tid == 0)
+    __hip_atomic_store(a.plan_flag, a.plan_token, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 
   // Group 0 also computes the current token's score (its loads overlap the partial loads).
   uint32_t qd = 0, kd = 0, vd = 0;
@@ -1073,6 +1079,8 @@ hipError_t launch_paged_merge(int dtype, int d, const PagedLaunch& p, int n_seq,
   a.n_rep = p.hq / p.hkv;
   a.scale = p.scale;
   a.softcap = p.softcap;
+  a.plan_flag = p.plan_flag;
+  a.plan_token = p.plan_token;
   dim3 grid(n_seq, p.hq);
 #define PGR_MERGE(TY, DD) paged_merge_kernel<TY, DD><<<grid, 256, 0, stream>>>(a.seqs, a)
   if (dtype == kF16) {

@@ -138,6 +138,7 @@ PagedKV::~PagedKV() {
     if (b.host) hipHostFree(b.host);
     if (b.read) hipEventDestroy(b.read);
   }
+  if (plan_flags_) hipHostFree(plan_flags_);
   if (mass_host_) hipHostFree(mass_host_);
   for (hipEvent_t e : buf_free_) hipEventDestroy(e);
   for (hipEvent_t e : chunk_ready_) hipEventDestroy(e);
@@ -171,6 +172,26 @@ int PagedKV::hip_fail(hipError_t e, const char* what) {
     hipError_t e_ = (call);                             \
     if (e_ != hipSuccess) return hip_fail(e_, #call);   \
   } while (0)
+
+// Waits until the merge launch after the buffer's last read has stored the buffer's token
+// into its pinned flag word. Polls the word without HIP calls: with a stream query every
+// ~25 us in the loop, the next launch on the stream started ~6 us late (by kernel trace),
+// as after a recorded event. Only after 2^22 polls (longer than a step) does it query the
+// stream, every 2^16 polls after that, to return an error from a failed stream instead of
+// spinning.
+int PagedKV::wait_plan_flag(const PlanBuf& pb, int idx) {
+  auto done = [&] { return (int32_t)(__atomic_load_n(plan_flags_ + idx, __ATOMIC_ACQUIRE) - pb.token) >= 0; };
+  for (uint64_t poll = 1; !done(); ++poll) {
+    __builtin_ia32_pause();
+    if (poll < (1u << 22) || (poll & 0xffff) != 0) continue;
+    const hipError_t e = hipStreamQuery(pb.stream);
+    if (e == hipErrorNotReady) continue;
+    if (e != hipSuccess) return hip_fail(e, "hipStreamQuery (plan buffer wait)");
+    if (done()) break;
+    return fail(kErrState, "plan buffer still marked as read after its stream drained");
+  }
+  return kOk;
+}
 
 size_t PagedKV::rec_bytes() const {
   return (size_t)2 * cfg_.kv_heads * cfg_.tokens_per_block * cfg_.head_dim * 2;
@@ -223,6 +244,9 @@ int PagedKV::init() {
   }
   PGR_HIP(hipEventCreateWithFlags(&plan_uploaded_, ev_flags));
   for (PlanBuf& b : plan_bufs_) PGR_HIP(hipEventCreateWithFlags(&b.read, ev_flags));
+  PGR_HIP(hipHostMalloc(reinterpret_cast<void**>(&plan_flags_), 256, hipHostMallocDefault));
+  std::memset(plan_flags_, 0, 256);
+  PGR_HIP(hipHostGetDevicePointer(reinterpret_cast<void**>(&plan_flags_dev_), plan_flags_, 0));
   PGR_HIP(hipEventCreateWithFlags(&stage_copies_done_, ev_flags));
   PGR_HIP(hipEventCreateWithFlags(&compute_mark_, ev_flags));
   PGR_HIP(hipEventCreateWithFlags(&copy_mark_, ev_flags));
@@ -1020,8 +1044,13 @@ int PagedKV::begin_step(const int32_t* sids, int n, hipStream_t stream) {
   if (cfg_.num_layers == 1) plan_buf_ ^= 1;
   PlanBuf& pb = plan_bufs_[plan_buf_];
   if (pb.pending) {
-    PGR_HIP(hipEventSynchronize(pb.read));
     pb.pending = false;
+    if (pb.by_flag) {
+      const int rc = wait_plan_flag(pb, plan_buf_);
+      if (rc != kOk) return rc;
+    } else {
+      PGR_HIP(hipEventSynchronize(pb.read));
+    }
   }
   if (plan_bytes > pb.bytes) {
     if (pb.host) PGR_HIP(hipHostFree(pb.host));
@@ -1056,6 +1085,7 @@ int PagedKV::begin_step(const int32_t* sids, int n, hipStream_t stream) {
     PGR_HIP(hipEventRecord(plan_uploaded_, stream));
     PGR_HIP(hipEventRecord(pb.read, stream));
     pb.pending = true;
+    pb.by_flag = false;
     plan_on_device_ = true;
   }
   // Direct mode: the step's first attention launch reads its work items from the pinned
@@ -1132,6 +1162,8 @@ int PagedKV::decode_layer(int layer, const void* q, const void* k_new, const voi
   auto layer_shift = [&](int lay) {
     return (int64_t)(layer_buf(lay) - step_stage_base_ % nbuf) * cfg_.staging_slots;
   };
+  uint32_t* merge_flag = nullptr;  // set when this call makes the step's first (plan-reading) launch
+  uint32_t merge_token = 0;
   for (int L = 0; L < n_launch; ++L) {
     const int buf = prefetch_step_ ? layer_buf(layer) : (step_stage_base_ + L) % nbuf;
     if (n_chunks_ > 0) {
@@ -1172,9 +1204,20 @@ int PagedKV::decode_layer(int layer, const void* q, const void* k_new, const voi
     PGR_HIP(launch_paged(cfg_.dtype, cfg_.head_dim, pl, stream));
     if (timing_) PGR_HIP(hipEventRecord(t.stop, stream));
     if (first_read) {
+      // The merge below stores the buffer's token once this launch has finished. Under stream
+      // capture nothing runs now: the buffer is not marked, as for the replays of a captured
+      // graph, whose callers synchronize between steps.
       PlanBuf& pb = plan_bufs_[plan_buf_];
-      PGR_HIP(hipEventRecord(pb.read, stream));
-      pb.pending = true;
+      hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+      PGR_HIP(hipStreamIsCapturing(stream, &cap));
+      if (cap == hipStreamCaptureStatusNone) {
+        pb.token = ++plan_token_;
+        pb.by_flag = true;
+        pb.pending = true;
+        pb.stream = stream;
+        merge_flag = plan_flags_dev_ + plan_buf_;
+        merge_token = pb.token;
+      }
       plan_on_device_ = true;
     }
     if (timing_) {
@@ -1191,6 +1234,8 @@ int PagedKV::decode_layer(int layer, const void* q, const void* k_new, const voi
     if (rc != kOk) return rc;
     prefetched_layer_ = layer + 1;
   }
+  pl.plan_flag = merge_flag;
+  pl.plan_token = merge_token;
   PGR_HIP(launch_paged_merge(cfg_.dtype, cfg_.head_dim, pl, (int)seqs_.size(), stream));
   if (mass_accum) {
     PGR_HIP(launch_mass_reduce(d_seqs_, d_sess_rows_, d_sess_first_, d_mass_m_, d_mass_s_, d_mf_, d_lf_, mass_accum,

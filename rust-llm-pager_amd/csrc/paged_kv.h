@@ -225,14 +225,25 @@ class PagedKV {
   std::vector<int64_t> evict_pairs_, load_pairs_;  // moves of the current apply_tiers call
   // The step plan goes to one of two pinned buffers, alternately, so that the host can write
   // the next step's plan while the GPU still reads this one.
+  // In direct mode the GPU's last read of a buffer is the step's first attention launch; the
+  // merge launch after it stores the buffer's token into a pinned flag word, which the host
+  // polls. An event recorded between the two launches held the merge back by ~4.5 us per
+  // step. Staged mode waits on `read` instead.
   struct PlanBuf {
     void* host = nullptr;  // pinned
     void* dev = nullptr;   // its device mapping
     size_t bytes = 0;
     hipEvent_t read = nullptr;  // after the GPU's last read of this buffer
     bool pending = false;
+    bool by_flag = false;       // pending on the flag word rather than on `read`
+    uint32_t token = 0;         // flag value that marks the pending read as done
+    hipStream_t stream = nullptr;  // stream of the pending read
   };
   PlanBuf plan_bufs_[2];
+  uint32_t* plan_flags_ = nullptr;      // pinned, one word per plan buffer
+  uint32_t* plan_flags_dev_ = nullptr;  // their device mapping
+  uint32_t plan_token_ = 0;             // last token handed out
+  int wait_plan_flag(const PlanBuf& pb, int idx);
   int plan_buf_ = 0;             // buffer of the open step
   bool plan_on_device_ = false;  // the workspace holds the open step's plan
   size_t plan_aux_bytes_ = 0;    // plan bytes ahead of the work items

@@ -55,6 +55,11 @@ struct PagedLaunch {
   float* lf;
   int n_work, hq, hkv, tokens_per_block, mass_stride;
   float scale, softcap;
+  // Merge launch only: when set, the merge stores plan_token to *plan_flag (pinned host memory)
+  // as it starts, telling the host that the attention launches before it, and so their read of
+  // the step's plan buffer, have finished.
+  uint32_t* plan_flag = nullptr;
+  uint32_t plan_token = 0;
 };
 
 bool head_dim_supported(int d);

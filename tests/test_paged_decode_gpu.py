@@ -214,6 +214,41 @@ def test_sessions_join_and_leave_between_steps(mode, layers):
     assert reused  # a freed session id was handed out again
 
 
+@pytest.mark.parametrize("mode,layers", [("direct", 1), ("direct", 2), ("staged", 1)])
+def test_back_to_back_steps_without_host_sync(mode, layers):
+    """Steps issued back to back with no host synchronisation, as a serving loop issues them.
+    Each step reads ~45 MB of host blocks per layer, so the host plans the next steps while
+    the GPU still runs this one: only the plan buffers' reuse guard (the merge's flag word in
+    direct mode, an event in staged mode) keeps every launch on its own step's plan. Every
+    step's output is checked against the oracle afterwards."""
+    g = torch.Generator().manual_seed(41)
+    ctx = [30000, 21000, 12500, 25000]
+    S, hq, hkv, d, n = len(ctx), 14, 2, 64, 40
+    p = Pair(layers=layers, hq=hq, hkv=hkv, d=d, tpb=32, dtype=torch.float16, pool_blocks=S * 40,
+             host_blocks=sum(c // 32 + 8 for c in ctx), staging_blocks=4096, stream_mode=mode)
+    for c in ctx:
+        p.add(ctx=c, capacity=c + n + 32, gen=g, vram_budget=32 * MIB16, ram_budget=4096 * MIB16,
+              recent_window=31, policy="recent_only")
+    qs = [[(torch.randn(S, hq, d, generator=g) * 0.5).half() for _ in range(layers)] for _ in range(n)]
+    ks = [[(torch.randn(S, hkv, d, generator=g) * 0.5).half() for _ in range(layers)] for _ in range(n)]
+    vs = [[(torch.randn(S, hkv, d, generator=g) * 0.5).half() for _ in range(layers)] for _ in range(n)]
+    qd = [[x.cuda() for x in step] for step in qs]
+    kd = [[x.cuda() for x in step] for step in ks]
+    vd = [[x.cuda() for x in step] for step in vs]
+    outs = torch.empty(n, layers, S, hq, d, dtype=torch.float16, device="cuda")
+    torch.cuda.synchronize()
+    for i in range(n):
+        p.dec.begin_step(p.sids)
+        for l in range(layers):
+            p.dec.decode_layer(l, qd[i][l], kd[i][l], vd[i][l], outs[i, l])
+        p.dec.end_step(collect=False)
+    torch.cuda.synchronize()
+    for i in range(n):
+        ref = p.ora.step(p.sids, [np32(x) for x in qs[i]], [np32(x) for x in ks[i]], [np32(x) for x in vs[i]])
+        err = max(np.abs(np32(outs[i, l]) - ref["out"][l]).max() for l in range(layers))
+        assert err < TOL, f"step {i}: max-abs error {err}"
+
+
 @pytest.mark.parametrize("mode", ["direct", "staged"])
 def test_work_items_of_many_blocks(mode):
     """Work items of more than 16 blocks: 16-token blocks, batch 12 at 7k-14k tokens (about
