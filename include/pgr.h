@@ -231,7 +231,10 @@ int pgr_kv_end_step(void* kv, int32_t* completed, int32_t* n_completed);
  * step's launches take as arguments (plan buffer and workspace pointers, grid sizes, mass
  * stride) and returns their number. A graph captured in a step stays valid for any later
  * step with the same values, since pgr_kv_begin_step writes each step's plan to the same
- * buffers before replay. */
+ * buffers before replay. Eager steps guard those buffers themselves (begin_step waits until
+ * the GPU has read the buffer it is about to overwrite); captured and replayed launches do
+ * not, so a replaying caller lets the replay's first launch finish (e.g. synchronizes the
+ * stream) before the next pgr_kv_begin_step. */
 int pgr_kv_step_signature(void* kv, int64_t* out, int64_t cap);
 /* Attaches a placement handle (pgr_pager_new) to session sid; the store does not own it.
  * scores_from_mass != 0 for attention-scored policies (mass-driven scores). */
