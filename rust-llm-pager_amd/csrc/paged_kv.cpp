@@ -152,8 +152,7 @@ PagedKV::~PagedKV() {
   }
   if (plan_uploaded_) hipEventDestroy(plan_uploaded_);
   if (stage_copies_done_) hipEventDestroy(stage_copies_done_);
-  if (compute_mark_) hipEventDestroy(compute_mark_);
-  if (copy_mark_) hipEventDestroy(copy_mark_);
+  if (moves_done_) hipEventDestroy(moves_done_);
   if (copy_stream_) hipStreamDestroy(copy_stream_);
 }
 
@@ -190,6 +189,16 @@ int PagedKV::wait_plan_flag(const PlanBuf& pb, int idx) {
     if (done()) break;
     return fail(kErrState, "plan buffer still marked as read after its stream drained");
   }
+  return kOk;
+}
+
+// Tier moves run on the stream apply_tiers was given. Work queued on another stream that
+// reads or reuses records (kernels, copies, slot reuse) waits for them through one event;
+// work on the same stream is ordered already.
+int PagedKV::order_after_moves(hipStream_t stream) {
+  if (!moves_queued_ || moves_stream_ == stream) return kOk;
+  PGR_HIP(hipEventRecord(moves_done_, moves_stream_));
+  PGR_HIP(hipStreamWaitEvent(stream, moves_done_, 0));
   return kOk;
 }
 
@@ -248,8 +257,7 @@ int PagedKV::init() {
   std::memset(plan_flags_, 0, 256);
   PGR_HIP(hipHostGetDevicePointer(reinterpret_cast<void**>(&plan_flags_dev_), plan_flags_, 0));
   PGR_HIP(hipEventCreateWithFlags(&stage_copies_done_, ev_flags));
-  PGR_HIP(hipEventCreateWithFlags(&compute_mark_, ev_flags));
-  PGR_HIP(hipEventCreateWithFlags(&copy_mark_, ev_flags));
+  PGR_HIP(hipEventCreateWithFlags(&moves_done_, ev_flags));
   for (IndexBuf& b : index_bufs_) PGR_HIP(hipEventCreateWithFlags(&b.done, ev_flags));
   {
     std::vector<void*> bases(pool_);
@@ -408,6 +416,7 @@ int PagedKV::reorder_rows(int sid, const int32_t* src, int n, hipStream_t stream
   if (n != rows) return fail(kErrInvalid, "reorder_rows takes one source row per row of the session");
   for (int r = 0; r < rows; ++r)
     if (src[r] < 0 || src[r] >= rows) return fail(kErrInvalid, "source row out of range");
+  if (int rc0 = order_after_moves(stream); rc0 != kOk) return rc0;
   // The first new row that takes an old row inherits its records (HBM slots and host
   // range). Every later taker reuses the records of an old row that no new row takes --
   // there are exactly as many of those, and every row of a session holds records for the
@@ -508,6 +517,7 @@ int PagedKV::import_tokens(int sid, int row, int layer, const void* k, const voi
   const int64_t T = cfg_.tokens_per_block;
   const int64_t nb = (n_tokens + T - 1) / T;
   if (nb == 0) return kOk;
+  if (int rc0 = order_after_moves(stream); rc0 != kOk) return rc0;
   // One launch: resident blocks into their pool slots, host blocks straight into the
   // pinned mirror through its device mapping.
   IndexBuf* ib = nullptr;
@@ -539,8 +549,7 @@ int PagedKV::export_tokens(int sid, int row, int layer, void* k, void* v, int64_
   const int64_t T = cfg_.tokens_per_block;
   const int64_t nb = (n_tokens + T - 1) / T;
   if (nb == 0) return kOk;
-  // Evictions and loads queued on the copy stream may still be writing these records.
-  PGR_HIP(hipStreamSynchronize(copy_stream_));
+  if (int rc0 = order_after_moves(stream); rc0 != kOk) return rc0;
   IndexBuf* ib = nullptr;
   int rc = acquire_index_buf((size_t)nb, &ib);
   if (rc != kOk) return rc;
@@ -566,6 +575,7 @@ int PagedKV::put_block(int sid, int64_t block_id, const void* key, const void* v
   if (s.n_tokens % T != 0) return fail(kErrState, "put_block needs a block-aligned session (no open block)");
   if (block_id != s.n_tokens / T) return fail(kErrInvalid, "put_block: block ids must be registered in order");
   if (block_id + 1 >= s.capacity_blocks) return fail(kErrCapacity, "session capacity reached");
+  if (int rc0 = order_after_moves(stream); rc0 != kOk) return rc0;
   std::vector<int32_t> slots(s.rows);
   for (int r = 0; r < s.rows; ++r) {
     const int sl = alloc_slot();
@@ -606,8 +616,7 @@ int PagedKV::get_block(int sid, int64_t block_id, void* key, void* value, hipStr
   Session& s = sessions_[sid];
   const int64_t T = cfg_.tokens_per_block;
   if (block_id < 0 || block_id >= s.n_tokens / T) return fail(kErrKey, "block is not a registered full block");
-  // Evictions and loads queued on the copy stream may still be writing this block.
-  PGR_HIP(hipStreamSynchronize(copy_stream_));
+  if (int rc0 = order_after_moves(stream); rc0 != kOk) return rc0;
   const bool on_gpu = s.on_gpu[block_id] != 0;
   // Record index per row: pool slots, or host mirror records read in place.
   IndexBuf* ib = nullptr;
@@ -658,8 +667,8 @@ int PagedKV::move_block(Session& s, int64_t b, bool to_gpu, hipStream_t) {
           stats_.evict_bytes_copied += rec * cfg_.num_layers;
           s.host_valid[k] = 1;
         }
-        // Recycled only by later work ordered after copy_mark_ (see apply_tiers); a load of
-        // this same call that takes the slot is copied after the evictions.
+        // Recycled only by work queued after this call's copies on the caller's stream; a
+        // load of this same call that takes the slot is copied after the evictions.
         free_slot(sl);
         s.slot[k] = -1;
       }
@@ -679,25 +688,17 @@ int PagedKV::apply_tiers(int sid, const uint8_t* tiers, int64_t n_tiers, int64_t
   *n_gpu = 0;
   *n_cpu = 0;
   *fail_block = -1;
-  // Copies run after everything already queued on the caller's stream (kernels reading
-  // the blocks being evicted), and the caller's stream waits for them before reusing slots.
-  // Both orderings are set up on the first move only: a call that moves nothing leaves the
-  // two streams independent.
-  bool ordered = false;
-  auto order_streams = [&]() -> int {
-    if (ordered) return kOk;
-    ordered = true;
-    PGR_HIP(hipEventRecord(compute_mark_, stream));
-    PGR_HIP(hipStreamWaitEvent(copy_stream_, compute_mark_, 0));
-    return kOk;
-  };
+  // The copies run on the caller's stream: after the kernels already queued there (which
+  // may read the blocks being evicted) and before any later work reuses a freed slot. The
+  // caller's next kernels wait for them in any case, and a hand-off through the store's copy
+  // stream (two events and a cross-queue wait) added ~30 us to a decode step with an eviction.
+  if (int rc0 = order_after_moves(stream); rc0 != kOk) return rc0;
   evict_pairs_.clear();
   load_pairs_.clear();
   int rc = kOk;
   for (int64_t b = 0; b < n_full; ++b) {
     const int desired = b < n_tiers ? tiers[b] : 2;
     if (desired == 0 && !s.on_gpu[b]) {
-      if ((rc = order_streams()) != kOk) break;
       rc = move_block(s, b, true, stream);
       if (rc != kOk) break;
       if (s.placed[b]) cpu_bytes_ -= bb;
@@ -712,7 +713,6 @@ int PagedKV::apply_tiers(int sid, const uint8_t* tiers, int64_t n_tiers, int64_t
         rc = fail(kErrBudget, "ram_budget exceeded");
         break;
       }
-      if ((rc = order_streams()) != kOk) break;
       rc = move_block(s, b, false, stream);
       if (rc != kOk) break;
       cpu_bytes_ += bb;
@@ -740,16 +740,14 @@ int PagedKV::apply_tiers(int sid, const uint8_t* tiers, int64_t n_tiers, int64_t
     // Timing-only events: no system-scope fence (cache writeback and invalidate) at record.
     hipEventCreateWithFlags(&t.start, hipEventDisableSystemFence);
     hipEventCreateWithFlags(&t.stop, hipEventDisableSystemFence);
-    hipEventRecord(t.start, copy_stream_);
+    hipEventRecord(t.start, stream);
     const int l = cfg_.num_layers;
-    const int crc = dir == 0 ? launch_copies(pairs, 0, l, copy_stream_) : launch_copies(pairs, l, 0, copy_stream_);
-    hipEventRecord(t.stop, copy_stream_);
+    const int crc = dir == 0 ? launch_copies(pairs, 0, l, stream) : launch_copies(pairs, l, 0, stream);
+    hipEventRecord(t.stop, stream);
     move_timing_.push_back(t);
     if (crc != kOk && rc == kOk) rc = crc;
-  }
-  if (ordered) {
-    PGR_HIP(hipEventRecord(copy_mark_, copy_stream_));
-    PGR_HIP(hipStreamWaitEvent(stream, copy_mark_, 0));
+    moves_stream_ = stream;
+    moves_queued_ = true;
   }
   return rc;
 }
@@ -774,6 +772,7 @@ int PagedKV::default_workgroups() const {
 
 int PagedKV::begin_step(const int32_t* sids, int n, hipStream_t stream) {
   if (in_step_) return fail(kErrState, "begin_step while a step is open");
+  if (int rc0 = order_after_moves(stream); rc0 != kOk) return rc0;
   const int64_t T = cfg_.tokens_per_block;
   const int E_max = std::min(kMaxWorkEntries, std::max(kWaves, cfg_.blocks_per_workgroup));
   const int64_t target_wg = cfg_.target_workgroups > 0 ? cfg_.target_workgroups : default_workgroups();
@@ -1110,6 +1109,13 @@ int PagedKV::decode_layer(int layer, const void* q, const void* k_new, const voi
                           float* mass_accum, int64_t accum_stride, float scale, float softcap, hipStream_t stream) {
   if (!in_step_) return fail(kErrState, "decode_layer outside begin_step/end_step");
   if (layer < 0 || layer >= cfg_.num_layers) return fail(kErrInvalid, "layer out of range");
+  // Under stream capture nothing runs now: no cross-stream wait is recorded (the capture
+  // starts after the caller's earlier work), and no plan buffer is marked as read (below).
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  PGR_HIP(hipStreamIsCapturing(stream, &cap));
+  const bool capturing = cap != hipStreamCaptureStatusNone;
+  if (!capturing)
+    if (int rc0 = order_after_moves(stream); rc0 != kOk) return rc0;
   const int hq = cfg_.query_heads;
   const int T = cfg_.tokens_per_block;
   const size_t rec = rec_bytes();
@@ -1208,9 +1214,7 @@ int PagedKV::decode_layer(int layer, const void* q, const void* k_new, const voi
       // capture nothing runs now: the buffer is not marked, as for the replays of a captured
       // graph, whose callers synchronize between steps.
       PlanBuf& pb = plan_bufs_[plan_buf_];
-      hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-      PGR_HIP(hipStreamIsCapturing(stream, &cap));
-      if (cap == hipStreamCaptureStatusNone) {
+      if (!capturing) {
         pb.token = ++plan_token_;
         pb.by_flag = true;
         pb.pending = true;

@@ -253,11 +253,14 @@ class PagedKV {
   hipStream_t copy_stream_ = nullptr;
   hipEvent_t plan_uploaded_ = nullptr;
   hipEvent_t stage_copies_done_ = nullptr;  // after the last staging copy on the copy stream
+  // Stream of the last tier moves (apply_tiers runs its copies on the caller's stream).
+  hipStream_t moves_stream_ = nullptr;
+  bool moves_queued_ = false;
+  hipEvent_t moves_done_ = nullptr;
+  int order_after_moves(hipStream_t stream);
   bool stage_copy_pending_ = false;
   std::vector<hipEvent_t> buf_free_;
   std::vector<hipEvent_t> chunk_ready_;
-  hipEvent_t compute_mark_ = nullptr;
-  hipEvent_t copy_mark_ = nullptr;
   std::vector<int32_t> free_slots_;
   std::vector<std::pair<int64_t, int64_t>> host_free_;  // (offset, count), sorted by offset
   std::vector<Session> sessions_;

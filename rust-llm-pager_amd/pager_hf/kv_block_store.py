@@ -3,8 +3,8 @@
 A block is one ``tokens_per_block`` slice of every layer of one session, exchanged in the
 reference layout ``key, value [num_layers, batch, block_len, kv_heads, head_dim]``. Storage
 is the native store's layer-major HBM slot pools and block-id-addressed pinned host mirror
-(see kv_pool.py); movement is asynchronous copies on a side stream instead of blocking,
-fully synchronized per-block ``.to()`` calls.
+(see kv_pool.py); movement is asynchronous copy kernels on the caller's stream instead of
+blocking, fully synchronized per-block ``.to()`` calls.
 
 Kept from the reference: method names and return values, ascending-id ``apply_tiers`` with
 tier 0 -> GPU and anything else -> CPU (ids past ``len(tiers)`` -> CPU), ``KeyError("Block N is

@@ -66,7 +66,7 @@ class Pair:
         self.dec.set_lo(sid, lo)
         self.ora.set_lo(sid, lo)
 
-    def step(self, gen, *, compute=True, scale=0.5, sids=None, order=None):
+    def step(self, gen, *, compute=True, scale=0.5, sids=None, order=None, end_stream=None):
         sids = self.sids if sids is None else sids
         order = list(range(self.layers)) if order is None else order
         S = sum(self.dec.sessions[s].rows for s in sids)
@@ -80,7 +80,11 @@ class Pair:
         for l in order:
             outs[l] = self.dec.decode_layer(l, qs[l].cuda(), ks[l].cuda(), vs[l].cuda())
         gather = [self.dec.step_host_blocks(i) for i in range(S)]
-        res = self.dec.end_step()
+        if end_stream is None:
+            res = self.dec.end_step()
+        else:  # placement copies queued on another stream than the step's launches
+            with torch.cuda.stream(end_stream):
+                res = self.dec.end_step()
         ref = self.ora.step(sids, [np32(x) for x in qs], [np32(x) for x in ks], [np32(x) for x in vs],
                             compute=compute)
         assert gather == ref["gather"], "gather index lists differ"
@@ -212,6 +216,27 @@ def test_sessions_join_and_leave_between_steps(mode, layers):
             p.sids.remove(sid)
         p.step(g, sids=list(live))
     assert reused  # a freed session id was handed out again
+
+
+@pytest.mark.parametrize("mode", ["direct", "staged"])
+def test_tier_moves_on_another_stream(mode):
+    """end_step (and with it the eviction copies) runs on a side stream on alternate steps,
+    while begin_step and the attention launches run on the default stream. The evictions run
+    on the stream they were issued on; the next step's launches must still wait for them
+    before reading the evicted blocks from the host mirror or reusing their slots."""
+    g = torch.Generator().manual_seed(51)
+    ctx = [700, 1300, 2100, 410, 990]
+    p = Pair(layers=2, hq=8, hkv=2, d=64, tpb=16, dtype=torch.float16, pool_blocks=5 * 12,
+             host_blocks=sum(c // 16 + 8 for c in ctx), staging_blocks=1024, stream_mode=mode)
+    for c in ctx:
+        p.add(ctx=c, capacity=c + 64, gen=g, vram_budget=6 * MIB16, ram_budget=1024 * MIB16, recent_window=3,
+              policy="recent_only")
+    side = torch.cuda.Stream()
+    evicted = 0
+    for step in range(40):
+        res, _, _ = p.step(g, end_stream=side if step % 2 else None)
+        evicted += sum(len(r["to_cpu"]) for r in res.values())
+    assert evicted >= 8  # blocks complete and leave HBM on many steps
 
 
 @pytest.mark.parametrize("mode,layers", [("direct", 1), ("direct", 2), ("staged", 1)])
