@@ -181,7 +181,9 @@ int PagedKV::hip_fail(hipError_t e, const char* what) {
 int PagedKV::wait_plan_flag(const PlanBuf& pb, int idx) {
   auto done = [&] { return (int32_t)(__atomic_load_n(plan_flags_ + idx, __ATOMIC_ACQUIRE) - pb.token) >= 0; };
   for (uint64_t poll = 1; !done(); ++poll) {
+#if defined(__x86_64__)
     __builtin_ia32_pause();
+#endif
     if (poll < (1u << 22) || (poll & 0xffff) != 0) continue;
     const hipError_t e = hipStreamQuery(pb.stream);
     if (e == hipErrorNotReady) continue;
