@@ -205,7 +205,9 @@ int pgr_kv_put_block(void* kv, int32_t sid, int64_t block_id, const void* key, c
 int pgr_kv_get_block(void* kv, int32_t sid, int64_t block_id, void* key, void* value, void* stream);
 /* Moves full blocks to the tier the pager assigned (0 = HBM, else host; ids >= n_tiers ->
  * host), ascending by id; writes moved ids. PGR_ERR_BUDGET with *fail_block when an
- * offload would exceed the RAM budget (earlier moves stay done).
+ * offload would exceed the RAM budget (earlier moves stay done). The copies are queued on
+ * `stream`, after the work already there; this store's later calls on another stream wait
+ * for them through one event.
  * Replaces KVBlockStore.apply_tiers, kv_block_store.py:206-227 (offload :75-131, load :133-163). */
 int pgr_kv_apply_tiers(void* kv, int32_t sid, const uint8_t* tiers, int64_t n_tiers, int64_t* to_gpu, int64_t* n_gpu,
                        int64_t* to_cpu, int64_t* n_cpu, int64_t* fail_block, void* stream);
