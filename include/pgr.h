@@ -35,7 +35,7 @@ extern "C" {
 
 /* ---- library ------------------------------------------------------------------------- */
 
-/* ABI version of this header (increments when an entry point is added or changed); 4. */
+/* ABI version of this header (increments when an entry point is added or changed); 5. */
 int pgr_abi_version(void);
 /* Message of the last failing call on this thread ("" if none). */
 const char* pgr_last_error(void);
@@ -168,6 +168,9 @@ typedef struct pgr_kv_step_stats_s {
 /* Creates a store (allocates HBM pools, pinned host mirror, staging). NULL on failure.
  * Replaces KVBlockStore.__init__, pager_hf/kv_block_store.py:41-56. */
 void* pgr_kv_create(const pgr_kv_config_t* cfg);
+/* Waits for the store's work and frees it. Call it before the process exits: the HIP runtime
+ * tears itself down at exit, and a store still alive then would free device memory into a
+ * runtime that no longer exists. */
 void pgr_kv_destroy(void* kv);
 /* New session with `rows` sequences and room for capacity_tokens tokens; lo_per_row = first
  * valid token per row (left padding), NULL = 0. Returns the session id (>= 0). */
@@ -206,8 +209,9 @@ int pgr_kv_get_block(void* kv, int32_t sid, int64_t block_id, void* key, void* v
 /* Moves full blocks to the tier the pager assigned (0 = HBM, else host; ids >= n_tiers ->
  * host), ascending by id; writes moved ids. PGR_ERR_BUDGET with *fail_block when an
  * offload would exceed the RAM budget (earlier moves stay done). The copies are queued on
- * `stream`, after the work already there; this store's later calls on another stream wait
- * for them through one event.
+ * `stream`, after the work already there, and after the last decode step's launches when
+ * those ran on another stream (that stream must still be valid); this store's later calls
+ * on another stream wait for the copies through one event recorded here.
  * Replaces KVBlockStore.apply_tiers, kv_block_store.py:206-227 (offload :75-131, load :133-163). */
 int pgr_kv_apply_tiers(void* kv, int32_t sid, const uint8_t* tiers, int64_t n_tiers, int64_t* to_gpu, int64_t* n_gpu,
                        int64_t* to_cpu, int64_t* n_cpu, int64_t* fail_block, void* stream);
@@ -235,9 +239,13 @@ int pgr_kv_end_step(void* kv, int32_t* completed, int32_t* n_completed);
  * step with the same values, since pgr_kv_begin_step writes each step's plan to the same
  * buffers before replay. Eager steps guard those buffers themselves (begin_step waits until
  * the GPU has read the buffer it is about to overwrite); captured and replayed launches do
- * not, so a replaying caller lets the replay's first launch finish (e.g. synchronizes the
- * stream) before the next pgr_kv_begin_step. */
+ * not, so a replaying caller calls pgr_kv_step_replayed after each replay. */
 int pgr_kv_step_signature(void* kv, int64_t* out, int64_t cap);
+/* No counterpart in the reference (see pgr_kv_step_signature). After replaying the open
+ * step's decode launches from a captured graph on `stream`: the next pgr_kv_begin_step waits
+ * until the work queued on `stream` so far has run before it writes the plan buffer that
+ * the replay reads, and placement on another stream waits for it too. */
+int pgr_kv_step_replayed(void* kv, void* stream);
 /* Attaches a placement handle (pgr_pager_new) to session sid; the store does not own it.
  * scores_from_mass != 0 for attention-scored policies (mass-driven scores). */
 int pgr_kv_attach_pager(void* kv, int32_t sid, void* pager, int32_t scores_from_mass);
@@ -246,7 +254,9 @@ int pgr_kv_attach_pager(void* kv, int32_t sid, void* pager, int32_t scores_from_
  * over num_layers and normalized to sum 1), on_step(N-1), force_rebalance(N-1) when a block
  * completed, apply_tiers(tiers()). counts[5*i..] = {new block id or -1, n to HBM, n to host,
  * failing block or -1, n scores}; moves / scores (may be NULL) receive each session's moved
- * ids (to HBM then to host) and the scores handed to the pager.
+ * ids (to HBM then to host) and the scores handed to the pager. On a `stream` other than
+ * the one the step's decode_layer calls used, the mass read-back and the tier moves first
+ * wait for the step's launches (the decode stream must still be valid).
  * Replaces _forward_step's placement tail and _finalize_streaming_block_attention,
  * paged_model.py:768-812 and :865-876. */
 int pgr_kv_end_step_place(void* kv, const float* mass_accum, int64_t accum_stride, int32_t num_layers,

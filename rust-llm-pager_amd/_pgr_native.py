@@ -33,7 +33,7 @@ MODE_FOLD_FIXED = 3
 STREAM_DIRECT = 0
 STREAM_STAGED = 1
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 c_i32, c_i64, c_u8, c_u32, c_u64 = ctypes.c_int32, ctypes.c_int64, ctypes.c_uint8, ctypes.c_uint32, ctypes.c_uint64
 c_f32, c_f64, c_size, c_vp = ctypes.c_float, ctypes.c_double, ctypes.c_size_t, ctypes.c_void_p
@@ -138,6 +138,7 @@ SIGNATURES: dict[str, tuple] = {
     "pgr_kv_set_lo": (ctypes.c_int, [c_vp, c_i32, P(c_i32)]),
     "pgr_kv_reorder_rows": (ctypes.c_int, [c_vp, c_i32, P(c_i32), c_i32, c_vp]),
     "pgr_kv_step_signature": (ctypes.c_int, [c_vp, P(c_i64), c_i64]),
+    "pgr_kv_step_replayed": (ctypes.c_int, [c_vp, c_vp]),
     "pgr_kv_set_length": (ctypes.c_int, [c_vp, c_i32, c_i64]),
     "pgr_kv_import": (ctypes.c_int, [c_vp, c_i32, c_i32, c_i32, c_vp, c_vp, c_i64, c_i64, c_vp]),
     "pgr_kv_export": (ctypes.c_int, [c_vp, c_i32, c_i32, c_i32, c_vp, c_vp, c_i64, c_vp]),

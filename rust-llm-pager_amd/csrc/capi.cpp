@@ -125,7 +125,7 @@ int kv_rc(pgr::PagedKV* kv, int rc) {
 
 extern "C" {
 
-int pgr_abi_version(void) { return 4; }
+int pgr_abi_version(void) { return 5; }
 
 const char* pgr_last_error(void) { return g_last_error.c_str(); }
 
@@ -358,6 +358,11 @@ int pgr_kv_step_signature(void* kv, int64_t* out, int64_t cap) {
   const int rc = kv_of(kv)->step_signature(out, cap);
   if (rc < 0) return set_err(rc, "step_signature outside a decode step");
   return rc;
+}
+
+int pgr_kv_step_replayed(void* kv, void* stream) {
+  if (!kv) return set_err(pgr::kErrInvalid, "null store");
+  return kv_rc(kv_of(kv), kv_of(kv)->step_replayed(as_stream(stream)));
 }
 
 int pgr_kv_end_step(void* kv, int32_t* completed, int32_t* n_completed) {

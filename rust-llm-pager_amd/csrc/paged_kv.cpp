@@ -153,6 +153,7 @@ PagedKV::~PagedKV() {
   if (plan_uploaded_) hipEventDestroy(plan_uploaded_);
   if (stage_copies_done_) hipEventDestroy(stage_copies_done_);
   if (moves_done_) hipEventDestroy(moves_done_);
+  if (decode_done_) hipEventDestroy(decode_done_);
   if (copy_stream_) hipStreamDestroy(copy_stream_);
 }
 
@@ -194,14 +195,35 @@ int PagedKV::wait_plan_flag(const PlanBuf& pb, int idx) {
   return kOk;
 }
 
-// Tier moves run on the stream apply_tiers was given. Work queued on another stream that
-// reads or reuses records (kernels, copies, slot reuse) waits for them through one event;
-// work on the same stream is ordered already.
+// Tier moves run on the stream apply_tiers was given, which records moves_done_ after them.
+// Work queued on another stream that reads or reuses records (kernels, copies, slot reuse)
+// waits for that event, once per stream; work on the same stream is ordered already.
 int PagedKV::order_after_moves(hipStream_t stream) {
   if (!moves_queued_ || moves_stream_ == stream) return kOk;
-  PGR_HIP(hipEventRecord(moves_done_, moves_stream_));
+  if (std::find(moves_waited_.begin(), moves_waited_.end(), stream) != moves_waited_.end()) return kOk;
   PGR_HIP(hipStreamWaitEvent(stream, moves_done_, 0));
+  moves_waited_.push_back(stream);
   return kOk;
+}
+
+// Placement on a stream other than the step's decode stream waits for the decode launches
+// (their appends and block mass) before it reads the mass or copies records. The event is
+// recorded on the decode stream when the first such call comes, so a step whose placement
+// runs on its own stream pays nothing.
+int PagedKV::order_after_decode(hipStream_t stream) {
+  if (!decode_pending_ || decode_stream_ == stream) return kOk;
+  if (std::find(decode_waited_.begin(), decode_waited_.end(), stream) != decode_waited_.end()) return kOk;
+  if (decode_waited_.empty()) PGR_HIP(hipEventRecord(decode_done_, decode_stream_));
+  PGR_HIP(hipStreamWaitEvent(stream, decode_done_, 0));
+  decode_waited_.push_back(stream);
+  return kOk;
+}
+
+void PagedKV::forget_streams() {
+  moves_queued_ = false;
+  moves_waited_.clear();
+  decode_pending_ = false;
+  decode_waited_.clear();
 }
 
 size_t PagedKV::rec_bytes() const {
@@ -260,6 +282,7 @@ int PagedKV::init() {
   PGR_HIP(hipHostGetDevicePointer(reinterpret_cast<void**>(&plan_flags_dev_), plan_flags_, 0));
   PGR_HIP(hipEventCreateWithFlags(&stage_copies_done_, ev_flags));
   PGR_HIP(hipEventCreateWithFlags(&moves_done_, ev_flags));
+  PGR_HIP(hipEventCreateWithFlags(&decode_done_, ev_flags));
   for (IndexBuf& b : index_bufs_) PGR_HIP(hipEventCreateWithFlags(&b.done, ev_flags));
   {
     std::vector<void*> bases(pool_);
@@ -348,6 +371,7 @@ int PagedKV::remove_session(int sid) {
   Session& s = sessions_[sid];
   // Slots may still be read by queued kernels or copies: drain before recycling them.
   PGR_HIP(hipDeviceSynchronize());
+  forget_streams();
   const int64_t T = cfg_.tokens_per_block;
   const int64_t n_full = s.n_tokens / T;
   for (int64_t b = 0; b < s.capacity_blocks; ++b)
@@ -440,6 +464,7 @@ int PagedKV::reorder_rows(int sid, const int32_t* src, int n, hipStream_t stream
         return fail(kErrState, "rows of a session differ in residency");
   // Queued kernels and copies may still read or write this session's records.
   PGR_HIP(hipDeviceSynchronize());
+  forget_streams();
   std::vector<int32_t> slot(s.slot.size(), -1);
   std::vector<uint8_t> hv(s.host_valid.size(), 0);
   std::vector<int64_t> pairs, host_pairs;  // (from record, to record) in the pool / host mirror
@@ -694,7 +719,10 @@ int PagedKV::apply_tiers(int sid, const uint8_t* tiers, int64_t n_tiers, int64_t
   // may read the blocks being evicted) and before any later work reuses a freed slot. The
   // caller's next kernels wait for them in any case, and a hand-off through the store's copy
   // stream (two events and a cross-queue wait) added ~30 us to a decode step with an eviction.
+  // On a stream other than the last decode step's, the copies also wait for that step's
+  // launches, which may still append to a block being evicted.
   if (int rc0 = order_after_moves(stream); rc0 != kOk) return rc0;
+  if (int rc0 = order_after_decode(stream); rc0 != kOk) return rc0;
   evict_pairs_.clear();
   load_pairs_.clear();
   int rc = kOk;
@@ -735,6 +763,7 @@ int PagedKV::apply_tiers(int sid, const uint8_t* tiers, int64_t n_tiers, int64_t
     }
   }
   // Evictions first: a load may reuse a slot an eviction of this call freed.
+  bool launched = false;
   for (int dir = 0; dir < 2; ++dir) {
     std::vector<int64_t>& pairs = dir == 0 ? evict_pairs_ : load_pairs_;
     if (pairs.empty()) continue;
@@ -748,8 +777,15 @@ int PagedKV::apply_tiers(int sid, const uint8_t* tiers, int64_t n_tiers, int64_t
     hipEventRecord(t.stop, stream);
     move_timing_.push_back(t);
     if (crc != kOk && rc == kOk) rc = crc;
+    launched = true;
+  }
+  if (launched) {
+    // Later work on other streams waits for this event (order_after_moves), recorded now so
+    // that no later call touches this stream handle again.
+    PGR_HIP(hipEventRecord(moves_done_, stream));
     moves_stream_ = stream;
     moves_queued_ = true;
+    moves_waited_.clear();
   }
   return rc;
 }
@@ -757,6 +793,7 @@ int PagedKV::apply_tiers(int sid, const uint8_t* tiers, int64_t n_tiers, int64_t
 int PagedKV::ensure_workspace(size_t bytes) {
   if (bytes <= ws_bytes_) return kOk;
   PGR_HIP(hipDeviceSynchronize());
+  forget_streams();
   if (ws_) PGR_HIP(hipFree(ws_));
   ws_ = nullptr;
   const size_t want = std::max(bytes, ws_bytes_ * 3 / 2);
@@ -1112,7 +1149,8 @@ int PagedKV::decode_layer(int layer, const void* q, const void* k_new, const voi
   if (!in_step_) return fail(kErrState, "decode_layer outside begin_step/end_step");
   if (layer < 0 || layer >= cfg_.num_layers) return fail(kErrInvalid, "layer out of range");
   // Under stream capture nothing runs now: no cross-stream wait is recorded (the capture
-  // starts after the caller's earlier work), and no plan buffer is marked as read (below).
+  // starts after the caller's earlier work), and neither the plan buffer (below) nor the
+  // decode stream is marked; step_replayed does both for each replay.
   hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
   PGR_HIP(hipStreamIsCapturing(stream, &cap));
   const bool capturing = cap != hipStreamCaptureStatusNone;
@@ -1213,8 +1251,8 @@ int PagedKV::decode_layer(int layer, const void* q, const void* k_new, const voi
     if (timing_) PGR_HIP(hipEventRecord(t.stop, stream));
     if (first_read) {
       // The merge below stores the buffer's token once this launch has finished. Under stream
-      // capture nothing runs now: the buffer is not marked, as for the replays of a captured
-      // graph, whose callers synchronize between steps.
+      // capture nothing runs now and the captured launches carry no token: the caller marks
+      // the buffer after each replay of the graph (step_replayed).
       PlanBuf& pb = plan_bufs_[plan_buf_];
       if (!capturing) {
         pb.token = ++plan_token_;
@@ -1247,6 +1285,28 @@ int PagedKV::decode_layer(int layer, const void* q, const void* k_new, const voi
     PGR_HIP(launch_mass_reduce(d_seqs_, d_sess_rows_, d_sess_first_, d_mass_m_, d_mass_s_, d_mf_, d_lf_, mass_accum,
                                (int)accum_stride, hq, mass_stride_, (int)step_sids_.size(), mass_stride_, stream));
   }
+  if (!capturing) {
+    decode_stream_ = stream;
+    decode_pending_ = true;
+    decode_waited_.clear();
+  }
+  return kOk;
+}
+
+int PagedKV::step_replayed(hipStream_t stream) {
+  if (!in_step_) return fail(kErrState, "step_replayed outside begin_step/end_step");
+  PlanBuf& pb = plan_bufs_[plan_buf_];
+  // The event follows the whole replay; begin_step waits on it before it writes this buffer
+  // again (a replayed launch carries no flag token, unlike an eager one). It replaces a flag
+  // guard an eager launch of this step may have set, and covers that launch too.
+  PGR_HIP(hipEventRecord(pb.read, stream));
+  pb.pending = true;
+  pb.by_flag = false;
+  pb.stream = stream;
+  plan_on_device_ = true;
+  decode_stream_ = stream;
+  decode_pending_ = true;
+  decode_waited_.clear();
   return kOk;
 }
 
@@ -1315,6 +1375,9 @@ int PagedKV::end_step_place(const float* mass_accum, int64_t accum_stride, int n
     n_mass_old[i] = s.n_tokens / T;
     need_mass = need_mass || (s.pager && s.scores_from_mass);
   }
+  // Reading the mass and moving records on a stream other than the decode stream waits for
+  // the step's launches first.
+  if (int rc0 = order_after_decode(stream); rc0 != kOk) return rc0;
   if (need_mass) {
     if (!mass_accum || accum_stride <= 0) return fail(kErrInvalid, "scoring policy needs the mass accumulator");
     const size_t want = (size_t)n * accum_stride;
@@ -1484,6 +1547,7 @@ int PagedKV::kernel_time(double* ms, int64_t* launches, int64_t* bytes) {
 int PagedKV::sync() {
   PGR_HIP(hipStreamSynchronize(copy_stream_));
   PGR_HIP(hipDeviceSynchronize());
+  forget_streams();
   return kOk;
 }
 

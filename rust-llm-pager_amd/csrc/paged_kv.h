@@ -120,6 +120,11 @@ class PagedKV {
   // plan to the same buffers).
   // Returns the number of values (writes at most cap), or kErrState outside a step.
   int step_signature(int64_t* out, int64_t cap) const;
+  // The open step's launches were replayed from a captured graph on `stream` (no eager
+  // decode_layer call made them): marks the step's plan buffer as read once the work queued
+  // on `stream` so far has finished, so that a later begin_step does not overwrite it before
+  // the replayed launch that reads it has run.
+  int step_replayed(hipStream_t stream);
 
   // Per-step placement glue of paged_model.py:768-812 for sessions with an attached pager:
   // scores (uniform, or this step's block mass averaged over layers and normalized), then
@@ -253,11 +258,25 @@ class PagedKV {
   hipStream_t copy_stream_ = nullptr;
   hipEvent_t plan_uploaded_ = nullptr;
   hipEvent_t stage_copies_done_ = nullptr;  // after the last staging copy on the copy stream
-  // Stream of the last tier moves (apply_tiers runs its copies on the caller's stream).
+  // Tier moves run on the stream apply_tiers was given; moves_done_ is recorded there right
+  // after them. Work that a later call queues on another stream waits for that event once
+  // per stream (moves_waited_), so no stream handle of an earlier call is used again.
   hipStream_t moves_stream_ = nullptr;
   bool moves_queued_ = false;
   hipEvent_t moves_done_ = nullptr;
+  std::vector<hipStream_t> moves_waited_;
   int order_after_moves(hipStream_t stream);
+  // The step's decode launches run on the stream decode_layer was given. Placement
+  // (end_step_place, apply_tiers) on another stream reads the mass those launches write and
+  // evicts records they append to, so it first waits for them: an event recorded on
+  // decode_stream_ when such a call comes. The decode stream therefore has to stay valid
+  // until the step's placement has been issued.
+  hipStream_t decode_stream_ = nullptr;
+  bool decode_pending_ = false;
+  hipEvent_t decode_done_ = nullptr;
+  std::vector<hipStream_t> decode_waited_;
+  int order_after_decode(hipStream_t stream);
+  void forget_streams();  // after a device-wide synchronization
   bool stage_copy_pending_ = false;
   std::vector<hipEvent_t> buf_free_;
   std::vector<hipEvent_t> chunk_ready_;

@@ -137,6 +137,11 @@ class NativeKVPool:
         nat.check(self.lib.pgr_kv_step_signature(self.handle, arr, n), "step_signature")
         return tuple(arr[:n])
 
+    def step_replayed(self) -> None:
+        """The open step's launches were replayed from a captured graph on the current
+        stream: guard the step's plan buffer until that replay has run."""
+        self._call("step_replayed", self.lib.pgr_kv_step_replayed, self._stream())
+
     def reorder_rows(self, sid: int, src_rows) -> None:
         """New row r of session `sid` takes old row src_rows[r]'s K/V history (beam search)."""
         arr = (ctypes.c_int32 * len(src_rows))(*[int(x) for x in src_rows])

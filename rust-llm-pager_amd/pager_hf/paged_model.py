@@ -582,6 +582,9 @@ class PagedModel:
             ids.copy_(input_ids)
             pos.copy_(position_ids)
         entry[0].replay()
+        # The replayed attention launch reads the step's plan buffer; the next begin_step must
+        # not overwrite it before then (steps fed back to back, e.g. a continued prompt).
+        dec.pool.step_replayed()
         return entry[1][2][:, -1, :]
 
     @staticmethod

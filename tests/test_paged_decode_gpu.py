@@ -239,6 +239,27 @@ def test_tier_moves_on_another_stream(mode):
     assert evicted >= 8  # blocks complete and leave HBM on many steps
 
 
+@pytest.mark.parametrize("mode", ["direct", "staged"])
+def test_scoring_placement_on_another_stream(mode):
+    """A scoring policy with no recent window, placement on a side stream every other step:
+    the mass read-back and the eviction of the block that completed in this very step (its
+    last token appended by this step's launch on the default stream) must wait for the
+    step's launches."""
+    g = torch.Generator().manual_seed(52)
+    ctx = [3000, 5200, 4100]
+    p = Pair(layers=2, hq=8, hkv=2, d=64, tpb=16, dtype=torch.float16, pool_blocks=3 * 12,
+             host_blocks=sum(c // 16 + 8 for c in ctx), staging_blocks=1024, stream_mode=mode)
+    for c in ctx:
+        p.add(ctx=c, capacity=c + 80, gen=g, scale=1.0, vram_budget=12 * MIB16, ram_budget=1024 * MIB16,
+              recent_window=0, rebalance_interval=4, policy="sinks_heavy_hitter")
+    side = torch.cuda.Stream()
+    evicted = 0
+    for step in range(40):
+        res, _, _ = p.step(g, scale=1.0, end_stream=side if step % 2 else None)
+        evicted += sum(len(r["to_cpu"]) for r in res.values())
+    assert evicted >= 3
+
+
 @pytest.mark.parametrize("mode,layers", [("direct", 1), ("direct", 2), ("staged", 1)])
 def test_back_to_back_steps_without_host_sync(mode, layers):
     """Steps issued back to back with no host synchronisation, as a serving loop issues them.

@@ -250,3 +250,29 @@ def test_hip_graph_steps_match_eager_steps(policy):
     g2 = PagedModel(model, use_hip_graphs=True, **kw)
     e2 = PagedModel(model, **kw)
     assert g2.generate(ids, mask, 40) == e2.generate(ids, mask, 40)
+
+
+def test_hip_graphs_continue_a_session_with_fed_tokens():
+    """A second generate() call with HIP graphs first feeds the tokens the caller appended
+    since the first call: those steps run back to back with no host read between them, so
+    the host writes the next step's plan while earlier replays are still queued. Each replay
+    must read its own step's plan (same tokens as the eager path)."""
+    from pager_hf import PagedModel
+
+    model = _model(SMALL, seed=19, init_std=0.05)
+    g = torch.Generator().manual_seed(20)
+    ids = torch.randint(0, SMALL["vocab_size"], (1, 300), generator=g).cuda()
+    extra = torch.randint(0, SMALL["vocab_size"], (1, 45), generator=g).cuda()
+    kw = dict(vram_budget=4 * MIB16, ram_budget=1 << 40, recent_window=2, policy="recent_only", tokens_per_block=16,
+              max_context_tokens=640)
+    runs = []
+    for graphs in (False, True):
+        pm = PagedModel(model, use_hip_graphs=graphs, **kw)
+        first = pm.generate(ids, torch.ones_like(ids), 24)
+        ids2 = torch.cat([ids, torch.tensor([first], device="cuda"), extra], dim=1)
+        second = pm.generate(ids2, torch.ones_like(ids2), 24)
+        if graphs:
+            assert len(pm._graphs) > 0
+        runs.append((first, second))
+        pm.reset()
+    assert runs[1] == runs[0]
