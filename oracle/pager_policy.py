@@ -17,7 +17,9 @@ Rust semantics reproduced exactly:
 
 Pinned by: tests/test_oracle_pager.py (the ten Rust unit tests of core.rs:582-704 as
 properties, the README.md:389 placement list, bench/persistent_policy_compare_results.csv
-rows 2-3, and hand-worked cases for each helper).
+rows 2-3, and hand-worked cases for each helper) and tests/test_oracle_pager_hysteresis.py
+(hand-derived cases that run every swap of promote_vram_with_hysteresis and
+promote_ram_with_hysteresis and every trim of trim_ram, with exact-margin and tie cases).
 """
 from __future__ import annotations
 

@@ -229,11 +229,12 @@ def test_sinks_heavy_hitter_selection_by_hand():
     assert q.vram_block_ids() == [0, 1, 2, 3, 4, 5, 8, 10, 11]
 
 
-def test_heavy_hitter_hysteresis_swap_by_hand():
+def test_heavy_hitter_enforce_vram_budget_keeps_best_pinned_by_hand():
     """heavy_hitter, 3 VRAM, recent_window 0, blocks 0..5 (0..3 sinks and 5 recent pinned).
     First placement (no VRAM yet): pinned first -> {0,1,2} win by id order. A later
-    rebalance keeps pinned blocks even over the budget: {0,1,2,3,5} pinned -> enforce keeps
-    3 best by (pinned, score) = the 3 pinned with the highest scores."""
+    rebalance puts every pinned block in VRAM, over the budget: {0,1,2,3,5} pinned ->
+    enforce_vram_budget_keep_best keeps the 3 best by (pinned, score). No swap runs here
+    (no unpinned VRAM block): the swaps are pinned in test_oracle_pager_hysteresis.py."""
     p = op.Pager(3 * BLOCK, 100 * BLOCK, 0, 1000, 0.05, 0.2, "heavy_hitter")
     p.on_step(5, 0, [0.1, 0.1, 0.1, 0.1, 0.9, 0.1])
     assert p.vram_block_ids() == [0, 1, 2]
@@ -243,9 +244,10 @@ def test_heavy_hitter_hysteresis_swap_by_hand():
     assert p.vram_block_ids() == [0, 3, 5]
 
 
-def test_fill_and_trim_ram_by_score():
+def test_fill_ram_by_score():
     """sinks_heavy_hitter with 4 VRAM and 2 RAM: the rest goes to the spill tier, RAM keeps
-    the two best scores among the non-VRAM blocks."""
+    the two best scores among the non-VRAM blocks (fill_ram; trim_ram is pinned in
+    test_oracle_pager_hysteresis.py)."""
     p = op.Pager(4 * BLOCK, 2 * BLOCK, 0, 1000, 0.05, 0.2, "sinks_heavy_hitter")
     p.on_step(7, 0, [0.1, 0.1, 0.1, 0.1, 0.3, 0.7, 0.2, 0.1])
     # VRAM: 4 sinks (recent budget min(0, 2, 0) = 0); RAM: best of 4..7 = {5, 4}

@@ -247,7 +247,7 @@ def test_scoring_placement_on_another_stream(mode):
     step's launches."""
     g = torch.Generator().manual_seed(52)
     ctx = [3000, 5200, 4100]
-    p = Pair(layers=2, hq=8, hkv=2, d=64, tpb=16, dtype=torch.float16, pool_blocks=3 * 12,
+    p = Pair(layers=2, hq=8, hkv=2, d=64, tpb=16, dtype=torch.float16, pool_blocks=3 * 16,
              host_blocks=sum(c // 16 + 8 for c in ctx), staging_blocks=1024, stream_mode=mode)
     for c in ctx:
         p.add(ctx=c, capacity=c + 80, gen=g, scale=1.0, vram_budget=12 * MIB16, ram_budget=1024 * MIB16,
