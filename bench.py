@@ -205,7 +205,7 @@ def continuous(args):
     t_open = time.perf_counter() - t_open
     tokens0 = sum(len(r.generated_tokens) for r in reqs)
     host_bytes[0] = 0
-    live = sum(r.input_ids.shape[1] for r in sched._active)
+    live = sum(r.context_tokens for r in sched._active)
     t0 = time.perf_counter()
     for _ in range(args.cb_rounds):
         sched._admit_new_requests()
@@ -213,7 +213,7 @@ def continuous(args):
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     tokens = sum(len(r.generated_tokens) for r in reqs) - tokens0
-    sched.stop(timeout=0)
+    sched.stop()
     link = host_bytes[0] / dt / 1e9
     return {
         "metric": "continuous-batching decode tokens/s (64 concurrent, Qwen2.5-1.5B arch, 4 GB HBM K/V budget)",
@@ -604,7 +604,7 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--staging-blocks", type=int, default=2048, help="records per staging buffer")
     ap.add_argument("--staging-buffers", type=int, default=3)
-    ap.add_argument("--blocks-per-wg", type=int, default=16, help="largest block count per workgroup")
+    ap.add_argument("--blocks-per-wg", type=int, default=32, help="largest block count per workgroup")
     ap.add_argument("--resident-blocks", type=int, default=CFG["resident_blocks"],
                     help="HBM-resident blocks per sequence (1100 keeps every block resident)")
     ap.add_argument("--target-wg", type=int, default=0, help="workgroups per attention launch (0 = library default)")
@@ -709,6 +709,7 @@ def main() -> int:
             "contexts": ctx,
             "batch": c["batch"],
             "stream_mode": args.stream_mode,
+            "blocks_per_workgroup": args.blocks_per_wg,
             "staging": {"records_per_buffer": args.staging_blocks, "buffers": args.staging_buffers},
         },
         "tokens_per_s": round(c["batch"] * args.steps / dt, 2),

@@ -15,7 +15,8 @@ per block move, bytes = key + value of the whole block).
 
 Different by design: blocks are fixed-shape (the pool has fixed-size slots), registered in
 id order (the way PagedModel registers them, paged_model.py:1189-1231), and returned by
-``get_any``/``get_gpu`` as copies. ``reorder_batch_rows`` (beam search) is not provided.
+``get_any``/``get_gpu`` as copies. ``reorder_batch_rows`` (beam search) takes exactly one
+source row per row: rows can be duplicated or dropped, but the batch size stays the same.
 """
 from __future__ import annotations
 

@@ -50,32 +50,6 @@ def test_continuous_batching_ragged_requests_match_unpaged():
     sched.stop()
 
 
-def test_persistent_session_turns_match_one_long_generation():
-    from pager_hf.serving.scheduler import ContinuousBatchingScheduler
-
-    model = _model(SMALL, seed=22, init_std=0.05)
-    g = torch.Generator().manual_seed(10)
-    p = torch.randint(0, SMALL["vocab_size"], (1, 200), generator=g).cuda()
-    turn2 = torch.randint(0, SMALL["vocab_size"], (1, 30), generator=g).cuda()
-    sched = ContinuousBatchingScheduler(
-        model, SimpleNamespace(eos_token_id=None), max_concurrent_sessions=2, total_vram_budget=2 * 4 * MIB16,
-        total_ram_budget=1 << 40, tokens_per_block=16, max_context_tokens=512, device="cuda",
-    )
-    sid = sched.create_session()
-    r1 = sched.submit_turn(sid, p, torch.ones_like(p), max_new_tokens=12)
-    other = sched.submit(p[:, :150], torch.ones_like(p[:, :150]), max_new_tokens=20)  # batched alongside
-    _run_all(sched, [r1, other])
-    r2 = sched.submit_turn(sid, turn2, torch.ones_like(turn2), max_new_tokens=12)
-    _run_all(sched, [r2])
-    full = torch.cat([p, torch.tensor([r1.generated_tokens], device="cuda"), turn2], dim=1)
-    want1, _, gaps1 = _baseline(model, p, torch.ones_like(p), 12)
-    _check_free_running([r1.generated_tokens], want1, gaps1)
-    if r1.generated_tokens == want1[0]:
-        want2, _, gaps2 = _baseline(model, full, torch.ones_like(full), 12)
-        _check_free_running([r2.generated_tokens], want2, gaps2)
-    sched.delete_session(sid)
-    sched.stop()
-
 
 def test_mistral_sliding_window_per_row():
     """Sliding window 64 with sessions at different positions in one batched step."""

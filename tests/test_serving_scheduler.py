@@ -1,11 +1,10 @@
 """ContinuousBatchingScheduler host logic on the CPU, with a fake engine.
 
-Follows the reference's tests/test_serving_scheduler.py:71-425 case by case where the
-behaviour is shared (admission, EOS, the token stream, sessions and turns, capacity and
-backpressure, drain and health); the batching cases check this build's rule instead
-(fresh requests step alone, every started request joins one batched step per round).
-Rounds are driven directly (_admit_new_requests / _run_once) except where the background
-thread itself is under test.
+Follows the reference's tests/test_serving_scheduler.py:71-425 where the admission and
+round behaviour is shared (admission, EOS, the token stream, capacity and backpressure);
+the batching cases check this build's rule instead (fresh requests step alone, every
+started request joins one batched step per round). Rounds are driven directly
+(_admit_new_requests / _run_once) except where the background thread itself is under test.
 """
 from __future__ import annotations
 
@@ -16,12 +15,7 @@ from types import SimpleNamespace
 import pytest
 import torch
 
-from pager_hf.serving.scheduler import (
-    ContinuousBatchingScheduler,
-    SchedulerAtCapacityError,
-    SessionBusyError,
-    SessionCapacityError,
-)
+from pager_hf.serving.scheduler import ContinuousBatchingScheduler, SchedulerAtCapacityError
 
 EOS = 999
 VOCAB = 1000
@@ -91,15 +85,6 @@ def test_rejects_invalid_arguments():
                                     max_queue_depth=-1)
 
 
-def test_reload_mode_flag_is_accepted():
-    eng = FakeEngine([[5]])
-    sched = ContinuousBatchingScheduler(object(), SimpleNamespace(eos_token_id=EOS), max_concurrent_sessions=1,
-                                        total_vram_budget=1, total_ram_budget=1, use_streaming_attention=False,
-                                        engine=eng)
-    req = sched.submit(*prompt(), max_new_tokens=1)
-    drive(sched, 2)
-    assert req.generated_tokens == [5]
-
 
 def test_admission_respects_max_concurrent_sessions():
     sched, eng = make([[5, 6, 7]] * 3, max_concurrent=2)
@@ -148,51 +133,8 @@ def test_output_queue_drains_to_sentinel():
     assert got == [5, 6]
 
 
-def test_sessions_capacity_and_unique_ids():
-    sched, _ = make(max_concurrent=2)
-    a, b = sched.create_session(), sched.create_session()
-    assert a != b
-    with pytest.raises(SessionCapacityError):
-        sched.create_session()
 
 
-def test_submit_turn_unknown_session_raises_key_error():
-    sched, _ = make()
-    with pytest.raises(KeyError):
-        sched.submit_turn("nope", *prompt(), max_new_tokens=1)
-
-
-def test_turns_reuse_the_engine_session_and_feed_the_previous_output():
-    # The fake answers every step; the two steps that only feed turn 2's tokens answer 0.
-    sched, eng = make([[5, 6, 0, 0, 40, 41]])
-    sid = sched.create_session()
-    r1 = sched.submit_turn(sid, *prompt(), max_new_tokens=2)
-    drive(sched, 3)
-    assert r1.generated_tokens == [5, 6]
-    r2 = sched.submit_turn(sid, torch.tensor([[20, 21]]), torch.ones(1, 2, dtype=torch.long), max_new_tokens=2)
-    assert r2.input_ids[0].tolist() == [1, 2, 3, 5, 6, 20, 21]
-    drive(sched, 5)
-    assert r2.generated_tokens == [40, 41]
-    assert len(eng.opened) == 1  # one engine session across turns
-    # Turn 2 fed turn 1's last token and its own tokens; only the last one produced output.
-    assert eng.opened[0].fed == [3, 5, 6, 20, 21, 40]
-    assert not eng.opened[0].closed
-    sched.delete_session(sid)
-    assert eng.opened[0].closed
-
-
-def test_concurrent_turn_rejected_and_delete_waits_for_it():
-    sched, _ = make([[5, 6]])
-    sid = sched.create_session()
-    sched.submit_turn(sid, *prompt(), max_new_tokens=2)
-    with pytest.raises(SessionBusyError):
-        sched.submit_turn(sid, *prompt(), max_new_tokens=1)
-    with pytest.raises(SessionBusyError):
-        sched.delete_session(sid)
-    drive(sched, 3)
-    sched.delete_session(sid)
-    with pytest.raises(KeyError):
-        sched.delete_session(sid)
 
 
 def test_submit_raises_at_capacity():
@@ -203,44 +145,8 @@ def test_submit_raises_at_capacity():
         sched.submit(*prompt(), max_new_tokens=1)
 
 
-def test_submit_turn_at_capacity_does_not_mark_session_busy():
-    sched, _ = make(max_concurrent=1, max_queue_depth=0)
-    sid = sched.create_session()
-    sched.submit(*prompt(), max_new_tokens=1)
-    with pytest.raises(SchedulerAtCapacityError):
-        sched.submit_turn(sid, *prompt(), max_new_tokens=1)
-    assert sid not in sched._busy_sessions
 
 
-def test_health_reports_thread_status():
-    sched, _ = make([[5]])
-    assert sched.health()["thread_alive"] is False
-    sched.start()
-    try:
-        assert sched.health()["status"] == "ok"
-    finally:
-        sched.stop(timeout=5)
-    assert sched.health()["thread_alive"] is False
-
-
-def test_stop_drains_active_request_to_completion():
-    sched, _ = make([[5, 6, 7]])
-    sched.start()
-    req = sched.submit(*prompt(), max_new_tokens=3)
-    assert req.done.wait(5)
-    sched.stop(timeout=5)
-    assert req.error is None and req.generated_tokens == [5, 6, 7]
-
-
-def test_stop_with_timeout_force_retires_a_request_that_never_finishes():
-    sched, _ = make(never_ending=True)
-    sched.start()
-    req = sched.submit(*prompt(), max_new_tokens=8000)
-    deadline = time.time() + 5
-    while not req.generated_tokens and time.time() < deadline:
-        time.sleep(0.01)
-    sched.stop(timeout=0.2)
-    assert req.done.is_set() and isinstance(req.error, RuntimeError)
 
 
 def test_engine_failure_surfaces_on_the_request():
@@ -254,3 +160,37 @@ def test_engine_failure_surfaces_on_the_request():
     drive(sched, 1)
     assert req.done.is_set() and "device lost" in str(req.error)
     assert threading.active_count() >= 1
+
+
+def test_background_thread_serves_requests_and_stop_fails_the_rest():
+    sched, _ = make([[5, 6, 7]], never_ending=False)
+    sched.start()
+    req = sched.submit(*prompt(), max_new_tokens=3)
+    assert req.done.wait(5)
+    assert req.error is None and req.generated_tokens == [5, 6, 7]
+    sched.stop()
+    late = sched.submit(*prompt(), max_new_tokens=3)
+    sched.stop()
+    assert late.done.is_set() and isinstance(late.error, RuntimeError)
+
+
+def test_one_argmax_per_round_over_the_batch():
+    """The batched step reads all next tokens with one argmax over [S, V]."""
+    sched, eng = make([[5, 6], [8, 9]], max_concurrent=2)
+    calls = []
+    real = torch.argmax
+
+    def counting(t, *a, **k):
+        calls.append(tuple(t.shape))
+        return real(t, *a, **k)
+
+    a = sched.submit(*prompt(), max_new_tokens=2)
+    b = sched.submit(*prompt(start=10), max_new_tokens=2)
+    drive(sched, 1)
+    torch.argmax = counting
+    try:
+        drive(sched, 1)
+    finally:
+        torch.argmax = real
+    assert calls == [(2, VOCAB)]
+    assert a.generated_tokens == [5, 6] and b.generated_tokens == [8, 9]
