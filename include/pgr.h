@@ -35,7 +35,7 @@ extern "C" {
 
 /* ---- library ------------------------------------------------------------------------- */
 
-/* ABI version of this header (increments when an entry point is added or changed); 5. */
+/* ABI version of this header (increments when an entry point is added or changed); 6. */
 int pgr_abi_version(void);
 /* Message of the last failing call on this thread ("" if none). */
 const char* pgr_last_error(void);
@@ -62,6 +62,19 @@ int pgr_attn_step(const void* q, const void* k, const void* v, const int32_t* va
                   float* l, float* acc, int64_t batch, int64_t num_query_heads, int64_t num_kv_heads, int64_t tokens,
                   int64_t head_dim, int dtype, float scale, float softcap, void* workspace, size_t workspace_bytes,
                   void* stream);
+
+/* No counterpart in the reference. For callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc): the same
+ * fold as pgr_attn_step, same kernels and results, with its split-K partials in a static
+ * device array of the library (8 MiB per GPU, held until the process ends) instead of a
+ * workspace. It calls no allocating routine. A chunk whose partials exceed 8 MiB is
+ * rejected with PGR_ERR_CAPACITY; chunks with batch * num_kv_heads <= 496 always fit
+ * (head_dim <= 128, n_rep <= 16). Calls share their GPU's array: calls that overlap on one
+ * GPU (two streams, two threads) race and must be serialized by the caller. */
+int pgr_attn_step_noalloc(const void* q, const void* k, const void* v, const int32_t* valid, const int32_t* active,
+                          float* m, float* l, float* acc, int64_t batch, int64_t num_query_heads,
+                          int64_t num_kv_heads, int64_t tokens, int64_t head_dim, int dtype, float scale,
+                          float softcap, void* stream);
 
 /* Fold one chunk's K into (m, l) only.
  * Replaces streaming_attention_stats_step, pager_hf/streaming_attention.py:516-560

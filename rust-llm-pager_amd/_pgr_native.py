@@ -33,7 +33,7 @@ MODE_FOLD_FIXED = 3
 STREAM_DIRECT = 0
 STREAM_STAGED = 1
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 c_i32, c_i64, c_u8, c_u32, c_u64 = ctypes.c_int32, ctypes.c_int64, ctypes.c_uint8, ctypes.c_uint32, ctypes.c_uint64
 c_f32, c_f64, c_size, c_vp = ctypes.c_float, ctypes.c_double, ctypes.c_size_t, ctypes.c_void_p
@@ -106,6 +106,11 @@ SIGNATURES: dict[str, tuple] = {
         ctypes.c_int,
         [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_i64, ctypes.c_int, c_f32,
          c_f32, c_vp, c_size, c_vp],
+    ),
+    "pgr_attn_step_noalloc": (
+        ctypes.c_int,
+        [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_i64, ctypes.c_int, c_f32,
+         c_f32, c_vp],
     ),
     "pgr_attn_stats_step": (
         ctypes.c_int,

@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cmath>
+#include <mutex>
 #include <new>
 #include <string>
 
@@ -11,6 +12,13 @@
 #include "pager_core.h"
 #include "pgr_common.h"
 #include "pgr_kernels.h"
+
+// Split-K partials of pgr_attn_step_noalloc: a file-scope device array, one copy per GPU,
+// held until the process ends. In host code `scratch` is a host-side stand-in, not a device
+// address: the device address is looked up once per device (hipGetSymbolAddress with that
+// device current, noalloc_scratch below) and only that address is used afterwards.
+constexpr size_t kNoAllocScratchBytes = (size_t)8 << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 
 namespace {
 
@@ -114,6 +122,27 @@ int run_dense(int mode, const void* q, const void* k, const void* v, const int32
   return pgr::kOk;
 }
 
+// Device address of `scratch` on the current device, looked up on the first call there.
+constexpr int kMaxDevices = 64;
+std::once_flag g_scratch_once[kMaxDevices];
+void* g_scratch_ptr[kMaxDevices];
+hipError_t g_scratch_err[kMaxDevices];
+
+int noalloc_scratch(void** out) {
+  int dev = 0;
+  const hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_err(e, "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) return set_err(pgr::kErrUnsupported, "device index beyond the scratch table");
+  std::call_once(g_scratch_once[dev], [dev] {
+    void* p = nullptr;
+    g_scratch_err[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    g_scratch_ptr[dev] = p;
+  });
+  if (g_scratch_err[dev] != hipSuccess) return hip_err(g_scratch_err[dev], "hipGetSymbolAddress(scratch)");
+  *out = g_scratch_ptr[dev];
+  return pgr::kOk;
+}
+
 pgr::PagedKV* kv_of(void* h) { return static_cast<pgr::PagedKV*>(h); }
 
 int kv_rc(pgr::PagedKV* kv, int rc) {
@@ -125,7 +154,7 @@ int kv_rc(pgr::PagedKV* kv, int rc) {
 
 extern "C" {
 
-int pgr_abi_version(void) { return 5; }
+int pgr_abi_version(void) { return 6; }
 
 const char* pgr_last_error(void) { return g_last_error.c_str(); }
 
@@ -142,6 +171,29 @@ int pgr_attn_step(const void* q, const void* k, const void* v, const int32_t* va
                   void* stream) {
   return run_dense(PGR_MODE_FOLD, q, k, v, valid, active, m, l, acc, nullptr, 0, 0, 16, batch, num_query_heads,
                    num_kv_heads, tokens, head_dim, dtype, scale, softcap, workspace, workspace_bytes, stream);
+}
+
+int pgr_attn_step_noalloc(const void* q, const void* k, const void* v, const int32_t* valid, const int32_t* active,
+                          float* m, float* l, float* acc, int64_t batch, int64_t num_query_heads,
+                          int64_t num_kv_heads, int64_t tokens, int64_t head_dim, int dtype, float scale,
+                          float softcap, void* stream) {
+  int rc = check_dense(batch, num_query_heads, num_kv_heads, tokens, head_dim, dtype, scale);
+  if (rc != pgr::kOk) return rc;
+  if (tokens == 0 || batch == 0) return pgr::kOk;
+  // Every partial slot that the merge reads is written by the fold launch before it (a row
+  // with active = 0 is skipped by both), so nothing left in `scratch` by an earlier call is
+  // read and nothing needs clearing.
+  const size_t need = plan_dense(batch, num_query_heads, num_kv_heads, tokens, head_dim, PGR_MODE_FOLD, 16).bytes;
+  if (need > kNoAllocScratchBytes)
+    return set_err(pgr::kErrCapacity, "pgr_attn_step_noalloc: this chunk needs " + std::to_string(need) +
+                                          " bytes of split-K partials, more than the " +
+                                          std::to_string(kNoAllocScratchBytes) +
+                                          "-byte static scratch; use pgr_attn_step with a workspace");
+  void* ws = nullptr;
+  rc = noalloc_scratch(&ws);
+  if (rc != pgr::kOk) return rc;
+  return run_dense(PGR_MODE_FOLD, q, k, v, valid, active, m, l, acc, nullptr, 0, 0, 16, batch, num_query_heads,
+                   num_kv_heads, tokens, head_dim, dtype, scale, softcap, ws, kNoAllocScratchBytes, stream);
 }
 
 int pgr_attn_stats_step(const void* q, const void* k, const int32_t* valid, const int32_t* active, float* m, float* l,
