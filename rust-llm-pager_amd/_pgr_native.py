@@ -24,6 +24,7 @@ PGR_ERR_BUDGET = -7
 
 DTYPE_F16 = 0
 DTYPE_BF16 = 1
+DTYPE_F32 = 2  # operator API and finalize only
 
 MODE_FOLD = 0
 MODE_STATS = 1

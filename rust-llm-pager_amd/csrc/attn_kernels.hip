@@ -377,6 +377,220 @@ __global__ __launch_bounds__(256) void dense_attn_kernel(DenseArgs a) {
                                    a.pl + slot * a.n_rep, a.pacc + slot * a.n_rep * D);
 }
 
+// l of head r from a per-head register array, with r a per-lane value (no dynamic indexing).
+template <int N>
+__device__ __forceinline__ float l_run_at(const float (&l)[N], int r) {
+  float x = 0.f;
+#pragma unroll
+  for (int q = 0; q < N; ++q)
+    if (q == r) x = l[q];
+  return x;
+}
+
+// ---------------------------------------------------------------------------------------
+// Generic dense chunk kernel: the operator API for the cases the MFMA kernel above does not
+// take -- fp32 q/k/v (any head dim) and 16-bit head dims 8, 16 and 256. The reference pads
+// Q and K with zero columns up to 16 when head_dim < 16 (streaming_attention.py:56-66,
+// :125-133) so that tl.dot applies; zero columns add nothing to a dot product, and this
+// kernel computes the unpadded dot products directly on the VALU.
+//
+// One wave per workgroup, grid (n_split, Hkv, B); the wave folds `wave_tokens` consecutive
+// tokens in tiles of 64, with the same partial layout and e-based (m, l) as
+// dense_attn_kernel, so dense_merge_kernel combines either. Per tile:
+//   1. scores: lane t takes token t0 + t and all n_rep query heads (q in LDS);
+//   2. softmax: per head, a wave max / sum; P (rounded to the K/V type before P.V, as
+//      streaming_attention.py:178 does) goes to LDS;
+//   3. P.V: lane (g, c) takes head dims c, c + 64, ... of tokens g, g + G, ... (G = 64 / min(D, 64)),
+//      so each V row is read by consecutive lanes; the token groups are summed at the end.
+constexpr int kGenTile = 64;
+
+template <class Ty>
+struct GenElem {  // 16-bit K/V/q elements
+  typedef uint16_t T;
+  static __device__ __forceinline__ float ld(const T* p) { return Ty::to_f(*p); }
+  static __device__ __forceinline__ float round_p(float p) { return Ty::to_f(Ty::cvt(p)); }
+};
+struct F32Elem {
+  typedef float T;
+  static __device__ __forceinline__ float ld(const T* p) { return *p; }
+  static __device__ __forceinline__ float round_p(float p) { return p; }
+};
+
+__device__ __forceinline__ float wave_max64(float x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
+  return x;
+}
+__device__ __forceinline__ float wave_sum64(float x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
+  return x;
+}
+
+template <class E, int D, int kMode>
+__global__ __launch_bounds__(64) void dense_generic_kernel(DenseArgs a) {
+  constexpr bool kFold = (kMode == kModeFold || kMode == kModeStats);
+  constexpr bool kWithV = (kMode != kModeStats);
+  constexpr bool kMass = (kMode == kModeAccumulate);
+  constexpr int DL = D < 64 ? D : 64;  // lanes per token group in the P.V pass
+  constexpr int G = 64 / DL;           // token groups
+  constexpr int DPL = D / DL;          // head dims per lane
+  typedef typename E::T T;
+  __shared__ float q_s[kMaxRep][D];
+  __shared__ float p_s[kMaxRep][kGenTile];    // P rounded for P.V
+  __shared__ float praw_s[kMaxRep][kGenTile];  // P unrounded, for the block mass
+  __shared__ float alpha_s[kMaxRep];
+
+  const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  if (a.active != nullptr && a.active[b] == 0) return;  // whole workgroup: uniform exit
+  const int lane = threadIdx.x;
+  const int n_rep = a.n_rep;
+  const size_t kv_base = ((size_t)b * a.hkv + h) * (size_t)a.tc * D;
+  const T* kp = reinterpret_cast<const T*>(a.k) + kv_base;
+  const T* vp = reinterpret_cast<const T*>(a.v) + kv_base;
+  const T* qp = reinterpret_cast<const T*>(a.q) + ((size_t)b * a.hq + (size_t)h * n_rep) * D;
+  for (int i = lane; i < kMaxRep * D; i += 64) {
+    const int r = i / D;
+    q_s[r][i - r * D] = r < n_rep ? E::ld(qp + i) : 0.f;
+  }
+  // Running (m, l) per head: uniform values, kept in registers of every lane.
+  float m_run[kMaxRep], l_run[kMaxRep], blk[kMaxRep];
+#pragma unroll
+  for (int r = 0; r < kMaxRep; ++r) {
+    m_run[r] = kNegInf;
+    l_run[r] = 0.f;
+    blk[r] = 0.f;
+    if constexpr (!kFold) {
+      if (r < n_rep) {
+        m_run[r] = a.m_in[(size_t)b * a.hq + h * n_rep + r];
+        l_run[r] = a.l_in[(size_t)b * a.hq + h * n_rep + r];
+      }
+    }
+  }
+  float acc[kMaxRep][DPL];
+#pragma unroll
+  for (int r = 0; r < kMaxRep; ++r)
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) acc[r][j] = 0.f;
+  __syncthreads();
+
+  const int t_begin = split * a.wave_tokens;
+  const int t_end = min(t_begin + a.wave_tokens, a.tc);
+  const int grp = lane / DL, col = lane - grp * DL;
+  for (int t0 = t_begin; t0 < t_end; t0 += kGenTile) {
+    // 1. Scores of token t0 + lane for every head.
+    const int t = t0 + lane;
+    bool ok = t < t_end;
+    if (ok && a.valid != nullptr) ok = a.valid[(size_t)b * a.tc + t] != 0;
+    float s[kMaxRep];
+#pragma unroll
+    for (int r = 0; r < kMaxRep; ++r) s[r] = 0.f;
+    if (ok) {
+      const T* krow = kp + (size_t)t * D;
+      for (int d = 0; d < D; ++d) {
+        const float kd = E::ld(krow + d);
+#pragma unroll
+        for (int r = 0; r < kMaxRep; ++r) s[r] += q_s[r][d] * kd;
+      }
+    }
+    // 2. Softmax weights per head.
+#pragma unroll
+    for (int r = 0; r < kMaxRep; ++r) {
+      if (r >= n_rep) continue;  // uniform
+      const float x = ok ? transform_score(s[r], a.scale, a.softcap) : kNegInf;
+      float p;
+      if constexpr (kFold) {
+        const float m_new = fmaxf(m_run[r], wave_max64(x));
+        const bool empty = m_new == kNegInf;
+        const float alpha = empty ? 0.f : __expf(m_run[r] - m_new);
+        p = (empty || !ok) ? 0.f : __expf(x - m_new);
+        l_run[r] = l_run[r] * alpha + wave_sum64(p);
+        m_run[r] = m_new;
+        if (lane == 0) alpha_s[r] = alpha;
+      } else {
+        p = ok ? __expf(x - m_run[r]) : 0.f;
+      }
+      p_s[r][lane] = E::round_p(p);
+      if constexpr (kMass) praw_s[r][lane] = p;
+    }
+    __syncthreads();
+    // 3. P.V over this tile.
+    if constexpr (kWithV) {
+      if constexpr (kFold) {
+#pragma unroll
+        for (int r = 0; r < kMaxRep; ++r) {
+          if (r >= n_rep) continue;
+          const float al = alpha_s[r];
+#pragma unroll
+          for (int j = 0; j < DPL; ++j) acc[r][j] *= al;
+        }
+      }
+      const int n_tok = min(kGenTile, t_end - t0);
+      for (int tt = grp; tt < n_tok; tt += G) {
+        const T* vrow = vp + (size_t)(t0 + tt) * D;
+        float vv[DPL];
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) vv[j] = E::ld(vrow + col + j * DL);
+#pragma unroll
+        for (int r = 0; r < kMaxRep; ++r) {
+          if (r >= n_rep) continue;
+          const float pr = p_s[r][tt];
+#pragma unroll
+          for (int j = 0; j < DPL; ++j) acc[r][j] += pr * vv[j];
+        }
+      }
+    }
+    // Block mass (accumulate mode): lane r sums its head's weights token by token, in order,
+    // and writes sum / l at the last token of each block (or of the wave's range).
+    if constexpr (kMass) {
+      if (lane < n_rep) {
+        const int r = lane;
+        const int n_tok = min(kGenTile, t_end - t0);
+        float bs = 0.f;
+#pragma unroll
+        for (int q = 0; q < kMaxRep; ++q)
+          if (q == r) bs = blk[q];
+        const int qh = h * n_rep + r;
+        for (int tt = 0; tt < n_tok; ++tt) {
+          bs += praw_s[r][tt];
+          const int tok = t0 + tt;
+          if ((tok + 1) % a.tokens_per_block == 0 || tok + 1 == t_end) {
+            a.block_mass[((size_t)b * a.hq + qh) * a.max_blocks + a.block_id_offset + tok / a.tokens_per_block] =
+                bs / l_run_at(l_run, r);
+            bs = 0.f;
+          }
+        }
+#pragma unroll
+        for (int q = 0; q < kMaxRep; ++q)
+          if (q == r) blk[q] = bs;
+      }
+    }
+    __syncthreads();
+  }
+
+  // Partials: token groups summed across lanes (xor over the group bits of the lane id).
+  const size_t slot = ((size_t)b * a.hkv + h) * a.n_split + split;
+#pragma unroll
+  for (int r = 0; r < kMaxRep; ++r) {
+    if (r >= n_rep) continue;
+    if constexpr (kWithV) {
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) {
+        float x = acc[r][j];
+#pragma unroll
+        for (int o = DL; o < 64; o <<= 1) x += __shfl_xor(x, o);
+        if (grp == 0) a.pacc[(slot * n_rep + r) * D + col + j * DL] = x;
+      }
+    }
+    if constexpr (kFold) {
+      if (lane == 0) {
+        a.pm[slot * n_rep + r] = m_run[r];
+        a.pl[slot * n_rep + r] = l_run[r];
+      }
+    }
+  }
+}
+
 // Combine the dense partials into the caller's running state, in place.
 template <int kMode>
 __global__ __launch_bounds__(64) void dense_merge_kernel(DenseArgs a, float* m, float* l, float* acc, int d) {
@@ -891,9 +1105,25 @@ __global__ __launch_bounds__(256) void mass_reduce_kernel(const SeqInfo* seqs, c
   }
 }
 
+hipError_t launch_dense_merge(const DenseArgs& a, int mode, int batch, int d, float* m, float* l, float* acc,
+                              hipStream_t stream) {
+  dim3 mgrid(batch * a.hq);
+  switch (mode) {
+    case kModeFold:
+      dense_merge_kernel<kModeFold><<<mgrid, 64, 0, stream>>>(a, m, l, acc, d);
+      break;
+    case kModeStats:
+      dense_merge_kernel<kModeStats><<<mgrid, 64, 0, stream>>>(a, m, l, acc, d);
+      break;
+    default:
+      dense_merge_kernel<kModeAccumulate><<<mgrid, 64, 0, stream>>>(a, m, l, acc, d);
+      break;
+  }
+  return hipGetLastError();
+}
+
 template <class Ty, int D>
-hipError_t launch_dense_t(const DenseArgs& a, int mode, int batch, float* m, float* l, float* acc,
-                          hipStream_t stream) {
+hipError_t launch_dense_t(const DenseArgs& a, int mode, int batch, hipStream_t stream) {
   dim3 grid(a.n_split, a.hkv, batch);
   switch (mode) {
     case kModeFold:
@@ -909,33 +1139,68 @@ hipError_t launch_dense_t(const DenseArgs& a, int mode, int batch, float* m, flo
       dense_attn_kernel<Ty, D, kModeFoldFixed><<<grid, 256, 0, stream>>>(a);
       break;
   }
-  hipError_t err = hipGetLastError();
-  if (err != hipSuccess) return err;
-  dim3 mgrid(batch * a.hq);
+  return hipGetLastError();
+}
+
+template <class Ty>
+hipError_t launch_dense_ty(const DenseArgs& a, int mode, int batch, int d, hipStream_t stream) {
+  switch (d) {
+    case 32:
+      return launch_dense_t<Ty, 32>(a, mode, batch, stream);
+    case 64:
+      return launch_dense_t<Ty, 64>(a, mode, batch, stream);
+    default:
+      return launch_dense_t<Ty, 128>(a, mode, batch, stream);
+  }
+}
+
+template <class E, int D>
+hipError_t launch_generic_t(const DenseArgs& a, int mode, int batch, hipStream_t stream) {
+  dim3 grid(a.n_split, a.hkv, batch);
   switch (mode) {
     case kModeFold:
-      dense_merge_kernel<kModeFold><<<mgrid, 64, 0, stream>>>(a, m, l, acc, D);
+      dense_generic_kernel<E, D, kModeFold><<<grid, 64, 0, stream>>>(a);
       break;
     case kModeStats:
-      dense_merge_kernel<kModeStats><<<mgrid, 64, 0, stream>>>(a, m, l, acc, D);
+      dense_generic_kernel<E, D, kModeStats><<<grid, 64, 0, stream>>>(a);
+      break;
+    case kModeAccumulate:
+      dense_generic_kernel<E, D, kModeAccumulate><<<grid, 64, 0, stream>>>(a);
       break;
     default:
-      dense_merge_kernel<kModeAccumulate><<<mgrid, 64, 0, stream>>>(a, m, l, acc, D);
+      dense_generic_kernel<E, D, kModeFoldFixed><<<grid, 64, 0, stream>>>(a);
       break;
   }
   return hipGetLastError();
 }
 
+// 16-bit q/k/v at the head dims the MFMA kernel does not take.
 template <class Ty>
-hipError_t launch_dense_ty(const DenseArgs& a, int mode, int batch, int d, float* m, float* l, float* acc,
-                           hipStream_t stream) {
+hipError_t launch_generic_16(const DenseArgs& a, int mode, int batch, int d, hipStream_t stream) {
   switch (d) {
-    case 32:
-      return launch_dense_t<Ty, 32>(a, mode, batch, m, l, acc, stream);
-    case 64:
-      return launch_dense_t<Ty, 64>(a, mode, batch, m, l, acc, stream);
+    case 8:
+      return launch_generic_t<GenElem<Ty>, 8>(a, mode, batch, stream);
+    case 16:
+      return launch_generic_t<GenElem<Ty>, 16>(a, mode, batch, stream);
     default:
-      return launch_dense_t<Ty, 128>(a, mode, batch, m, l, acc, stream);
+      return launch_generic_t<GenElem<Ty>, 256>(a, mode, batch, stream);
+  }
+}
+
+hipError_t launch_generic_32(const DenseArgs& a, int mode, int batch, int d, hipStream_t stream) {
+  switch (d) {
+    case 8:
+      return launch_generic_t<F32Elem, 8>(a, mode, batch, stream);
+    case 16:
+      return launch_generic_t<F32Elem, 16>(a, mode, batch, stream);
+    case 32:
+      return launch_generic_t<F32Elem, 32>(a, mode, batch, stream);
+    case 64:
+      return launch_generic_t<F32Elem, 64>(a, mode, batch, stream);
+    case 128:
+      return launch_generic_t<F32Elem, 128>(a, mode, batch, stream);
+    default:
+      return launch_generic_t<F32Elem, 256>(a, mode, batch, stream);
   }
 }
 
@@ -954,13 +1219,24 @@ hipError_t launch_paged_t(const PagedArgs& a, int n_work, bool mass, hipStream_t
 
 bool head_dim_supported(int d) { return d == 32 || d == 64 || d == 128; }
 
-int dense_wave_tokens(int batch, int hkv, int tc, int tokens_per_block, bool mass) {
-  // Aim for about 2048 waves over the grid (8 per CU), each folding at least one tile.
-  const long tiles = (tc + 15) / 16;
+bool dense_head_dim_supported(int d) { return d == 8 || d == 16 || head_dim_supported(d) || d == 256; }
+
+bool dense_generic(int dtype, int d) { return dtype == kF32 || !head_dim_supported(d); }
+
+int dense_waves_per_workgroup(int dtype, int d) { return dense_generic(dtype, d) ? 1 : kWaves; }
+
+int dense_wave_tokens(int dtype, int d, int batch, int hkv, int tc, int tokens_per_block, bool mass) {
+  // Aim for about 2048 waves over the grid (8 per CU; 1024 one-wave workgroups for the
+  // generic kernel), each folding at least one tile (16 tokens in the MFMA kernel, 64 in the
+  // generic one).
+  const bool gen = dense_generic(dtype, d);
+  const long tile = gen ? kGenTile : 16;
+  const long target = gen ? 1024 : 2048;
+  const long tiles = (tc + tile - 1) / tile;
   const long rows = (long)batch * hkv;
-  long per_wave = (tiles * rows + 2047) / 2048;
+  long per_wave = (tiles * rows + target - 1) / target;
   if (per_wave < 1) per_wave = 1;
-  long tokens = per_wave * 16;
+  long tokens = per_wave * tile;
   if (mass) {
     const long tpb = tokens_per_block;
     tokens = (tokens + tpb - 1) / tpb * tpb;
@@ -992,8 +1268,17 @@ hipError_t launch_dense(int dtype, int mode, int d, const DenseLaunch& p, hipStr
   a.block_id_offset = p.block_id_offset;
   a.scale = p.scale;
   a.softcap = p.softcap;
-  if (dtype == kF16) return launch_dense_ty<F16>(a, mode, p.batch, d, p.m, p.l, p.acc, stream);
-  return launch_dense_ty<BF16>(a, mode, p.batch, d, p.m, p.l, p.acc, stream);
+  hipError_t e;
+  if (dtype == kF32)
+    e = launch_generic_32(a, mode, p.batch, d, stream);
+  else if (!head_dim_supported(d))
+    e = dtype == kF16 ? launch_generic_16<F16>(a, mode, p.batch, d, stream)
+                      : launch_generic_16<BF16>(a, mode, p.batch, d, stream);
+  else
+    e = dtype == kF16 ? launch_dense_ty<F16>(a, mode, p.batch, d, stream)
+                      : launch_dense_ty<BF16>(a, mode, p.batch, d, stream);
+  if (e != hipSuccess) return e;
+  return launch_dense_merge(a, mode, p.batch, d, p.m, p.l, p.acc, stream);
 }
 
 hipError_t launch_finalize(int dtype, const float* acc, const float* l, void* out, int rows, int d,

@@ -41,8 +41,10 @@ int check_dense(int64_t batch, int64_t hq, int64_t hkv, int64_t tokens, int64_t 
   if (hq % hkv != 0) return set_err(pgr::kErrInvalid, "num_query_heads must be a multiple of num_kv_heads");
   if (hq / hkv > pgr::kMaxRep)
     return set_err(pgr::kErrUnsupported, "streaming attention's GQA query-head packing supports n_rep up to 16");
-  if (!pgr::head_dim_supported((int)d)) return set_err(pgr::kErrUnsupported, "head_dim must be 32, 64 or 128");
-  if (dtype != pgr::kF16 && dtype != pgr::kBF16) return set_err(pgr::kErrInvalid, "dtype must be fp16 or bf16");
+  if (!pgr::dense_head_dim_supported((int)d))
+    return set_err(pgr::kErrUnsupported, "head_dim must be 8, 16, 32, 64, 128 or 256");
+  if (dtype != pgr::kF16 && dtype != pgr::kBF16 && dtype != pgr::kF32)
+    return set_err(pgr::kErrInvalid, "dtype must be fp16, bf16 or fp32");
   if (!(scale > 0.f) || !std::isfinite(scale)) return set_err(pgr::kErrInvalid, "scale must be positive and finite");
   if (batch > 65535 || hkv > 65535 || tokens > ((int64_t)1 << 30))
     return set_err(pgr::kErrInvalid, "shape exceeds the launch limits");
@@ -54,12 +56,14 @@ struct DensePlan {
   size_t bytes = 0, o_pm = 0, o_pl = 0, o_pacc = 0;
 };
 
-DensePlan plan_dense(int64_t batch, int64_t hq, int64_t hkv, int64_t tokens, int64_t d, int mode, int64_t tpb) {
+DensePlan plan_dense(int64_t batch, int64_t hq, int64_t hkv, int64_t tokens, int64_t d, int mode, int64_t tpb,
+                     int dtype) {
   DensePlan p;
   if (tokens <= 0 || batch <= 0) return p;
   const bool mass = mode == PGR_MODE_ACCUMULATE;
-  p.wave_tokens = pgr::dense_wave_tokens((int)batch, (int)hkv, (int)tokens, (int)(mass ? tpb : 16), mass);
-  const int64_t per_wg = (int64_t)pgr::kWaves * p.wave_tokens;
+  p.wave_tokens =
+      pgr::dense_wave_tokens(dtype, (int)d, (int)batch, (int)hkv, (int)tokens, (int)(mass ? tpb : 16), mass);
+  const int64_t per_wg = (int64_t)pgr::dense_waves_per_workgroup(dtype, (int)d) * p.wave_tokens;
   p.n_split = (int)((tokens + per_wg - 1) / per_wg);
   const size_t slots = (size_t)batch * hkv * p.n_split;
   const size_t n_rep = (size_t)(hq / hkv);
@@ -90,7 +94,7 @@ int run_dense(int mode, const void* q, const void* k, const void* v, const int32
   if (tokens == 0 || batch == 0) return pgr::kOk;  // nothing to fold: the state is unchanged
   if (!q || !k || !m || !l || (mode != PGR_MODE_STATS && (!v || !acc)))
     return set_err(pgr::kErrInvalid, "null tensor pointer");
-  const DensePlan p = plan_dense(batch, hq, hkv, tokens, d, mode, tpb);
+  const DensePlan p = plan_dense(batch, hq, hkv, tokens, d, mode, tpb, dtype);
   if (ws == nullptr || ws_bytes < p.bytes) return set_err(pgr::kErrCapacity, "workspace too small");
   char* w = static_cast<char*>(ws);
   pgr::DenseLaunch L{};
@@ -162,7 +166,13 @@ size_t pgr_attn_workspace_bytes(int64_t batch, int64_t num_query_heads, int64_t 
                                 int64_t head_dim, int mode, int64_t tokens_per_block) {
   if (batch <= 0 || num_kv_heads <= 0 || num_query_heads <= 0 || tokens <= 0 || head_dim <= 0) return 0;
   if (mode == PGR_MODE_ACCUMULATE && (tokens_per_block <= 0 || tokens_per_block % 16 != 0)) return 0;
-  return plan_dense(batch, num_query_heads, num_kv_heads, tokens, head_dim, mode, tokens_per_block).bytes;
+  // The geometry depends on the element type only at head dims 32/64/128 (16-bit there runs the
+  // MFMA kernel, fp32 the generic one): the size covers both.
+  const size_t a = plan_dense(batch, num_query_heads, num_kv_heads, tokens, head_dim, mode, tokens_per_block,
+                              pgr::kF16).bytes;
+  const size_t b = plan_dense(batch, num_query_heads, num_kv_heads, tokens, head_dim, mode, tokens_per_block,
+                              pgr::kF32).bytes;
+  return a > b ? a : b;
 }
 
 int pgr_attn_step(const void* q, const void* k, const void* v, const int32_t* valid, const int32_t* active, float* m,
@@ -183,7 +193,8 @@ int pgr_attn_step_noalloc(const void* q, const void* k, const void* v, const int
   // Every partial slot that the merge reads is written by the fold launch before it (a row
   // with active = 0 is skipped by both), so nothing left in `scratch` by an earlier call is
   // read and nothing needs clearing.
-  const size_t need = plan_dense(batch, num_query_heads, num_kv_heads, tokens, head_dim, PGR_MODE_FOLD, 16).bytes;
+  const size_t need =
+      plan_dense(batch, num_query_heads, num_kv_heads, tokens, head_dim, PGR_MODE_FOLD, 16, dtype).bytes;
   if (need > kNoAllocScratchBytes)
     return set_err(pgr::kErrCapacity, "pgr_attn_step_noalloc: this chunk needs " + std::to_string(need) +
                                           " bytes of split-K partials, more than the " +

@@ -6,8 +6,9 @@
 
 namespace pgr {
 
-// Element types of Q/K/V/output. Matches PGR_DTYPE_* in include/pgr.h.
-enum DType : int { kF16 = 0, kBF16 = 1 };
+// Element types of Q/K/V/output. Matches PGR_DTYPE_* in include/pgr.h. fp32 is taken by the
+// dense operator API and finalize only; the paged store holds 16-bit K/V.
+enum DType : int { kF16 = 0, kBF16 = 1, kF32 = 2 };
 
 // Status codes. Matches PGR_* in include/pgr.h.
 enum Status : int {

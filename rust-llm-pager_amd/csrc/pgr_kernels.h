@@ -62,8 +62,15 @@ struct PagedLaunch {
   uint32_t plan_token = 0;
 };
 
+// Head dims of the paged decode kernels (32, 64, 128).
 bool head_dim_supported(int d);
-int dense_wave_tokens(int batch, int hkv, int tc, int tokens_per_block, bool mass);
+// Head dims of the dense operator kernels: 8, 16, 32, 64, 128, 256 (fp16, bf16 or fp32).
+bool dense_head_dim_supported(int d);
+// Dense launch geometry: the MFMA kernel (4 waves per workgroup, 16-token tiles) takes 16-bit
+// q/k/v at head dims 32/64/128; the generic VALU kernel (1 wave, 64-token tiles) the rest.
+bool dense_generic(int dtype, int d);
+int dense_waves_per_workgroup(int dtype, int d);
+int dense_wave_tokens(int dtype, int d, int batch, int hkv, int tc, int tokens_per_block, bool mass);
 
 hipError_t launch_dense(int dtype, int mode, int d, const DenseLaunch& p, hipStream_t stream);
 hipError_t launch_finalize(int dtype, const float* acc, const float* l, void* out, int rows, int d,

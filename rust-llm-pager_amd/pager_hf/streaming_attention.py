@@ -16,8 +16,11 @@ Conventions kept from the reference:
 
 Differences, by design: p is rounded to the K/V dtype before P.V exactly as the reference
 does, but the chunk is folded by many workgroups in parallel and merged, so fp32 results
-differ from the reference's sequential fold in the last bits. q/k/v must be float16 or
-bfloat16 and head_dim one of 32, 64, 128 (NotImplementedError otherwise). A masked position
+differ from the reference's sequential fold in the last bits. q/k/v may be float16, bfloat16
+or float32, and head_dim one of 8, 16, 32, 64, 128, 256 (NotImplementedError otherwise);
+16-bit inputs at head_dim 32/64/128 run the MFMA kernel, the rest a VALU kernel. The
+reference zero-pads Q and K to 16 columns below head_dim 16 so that tl.dot applies
+(:56-66, :125-133); the dot products are the same without the padding. A masked position
 contributes exactly zero in every kernel, also when the fixed max m is -inf.
 """
 from __future__ import annotations
@@ -27,6 +30,7 @@ import torch
 from . import _native as N
 
 _M_TILE = 16  # streaming_attention.py:55: query heads packed per KV head
+_QKV_CODES = {torch.float16: N.nat.DTYPE_F16, torch.bfloat16: N.nat.DTYPE_BF16, torch.float32: N.nat.DTYPE_F32}
 
 
 def _validate_n_rep(n_rep: int) -> None:
@@ -69,7 +73,9 @@ def _prep(q, k, v, m, l, acc, valid, active, scale):
     _validate_n_rep(n_rep)
     if k.dtype != q.dtype or (v is not None and v.dtype != q.dtype):
         raise TypeError("q, k and v must share one dtype")
-    code = N.dtype_code(q.dtype)
+    if q.dtype not in _QKV_CODES:
+        raise NotImplementedError(f"streaming attention takes float16, bfloat16 or float32 q/k/v, got {q.dtype}")
+    code = _QKV_CODES[q.dtype]
     device = N.require_cuda(q, k, v, m, l, acc, valid, active)
     for t, name in ((m, "m"), (l, "l")):
         _state(t, name)

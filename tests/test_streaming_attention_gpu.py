@@ -291,3 +291,100 @@ def test_fully_masked_row_stays_nan_free():
     streaming_attention_step(q.cuda(), k.cuda(), v.cuda(), m, l, acc, valid=valid.cuda())
     assert torch.isinf(m[0]).all() and (l[0] == 0).all() and (acc[0] == 0).all()
     assert not torch.isnan(acc).any()
+
+
+# -- the envelope beyond the MFMA kernel: head dims 8, 16, 256 and fp32 q/k/v -----------------
+
+
+def _two_pass_with_tail(q, k, v, tpb, group, *, valid=None, out_dtype=None):
+    """stats over every group and the tail, accumulate with mass over full blocks, fold_fixed
+    for the tail (paged_model.py:992-1048); returns (out, mass) on the CPU."""
+    b, hq, d = q.shape
+    total = k.shape[2]
+    full = total // tpb * tpb
+    nbl = full // tpb
+    qd, kd, vd = q.cuda(), k.cuda(), v.cuda()
+    vald = None if valid is None else valid.cuda()
+    sl = lambda t, s, e: None if t is None else t[:, s:e].contiguous()  # noqa: E731
+    m, l, _ = streaming_attention_state_init(b, hq, d, dev())
+    for s in range(0, full, group):
+        e = min(s + group, full)
+        streaming_attention_stats_step(qd, kd[:, :, s:e], m, l, valid=sl(vald, s, e))
+    if total > full:
+        streaming_attention_stats_step(qd, kd[:, :, full:], m, l, valid=sl(vald, full, total))
+    acc = torch.zeros(b, hq, d, dtype=torch.float32, device=dev())
+    mass = torch.zeros(b, hq, max(nbl, 1), dtype=torch.float32, device=dev())
+    for s in range(0, full, group):
+        e = min(s + group, full)
+        streaming_attention_accumulate_step(qd, kd[:, :, s:e], vd[:, :, s:e], m, l, acc, mass, s // tpb, tpb,
+                                            valid=sl(vald, s, e))
+    if total > full:
+        streaming_attention_fold_fixed_step(qd, kd[:, :, full:], vd[:, :, full:], m, l, acc,
+                                            valid=sl(vald, full, total))
+    out = streaming_attention_finalize(acc, l, out_dtype or q.dtype)
+    return out, mass[:, :, :nbl].cpu()
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("hq,hkv,d", [(14, 2, 8), (8, 8, 16), (16, 1, 256), (14, 2, 256), (12, 2, 16)])
+def test_head_dims_outside_the_mfma_kernel(dtype, hq, hkv, d):
+    """Head dims 8 and 16 (the reference zero-pads Q/K to 16 columns below 16, which leaves every
+    dot product unchanged) and 256: one-pass folds and the two-pass-with-tail path with mass,
+    with a padding mask, against the dense oracle."""
+    n_rep = hq // hkv
+    q, k, v = draw(70 + d + hq, (3, hq, d), (3, hkv, 337, d), (3, hkv, 337, d), dtype=dtype, scale=0.5)
+    valid = torch.ones(3, 337, dtype=torch.int32)
+    valid[2, :150] = 0
+    m, l, acc = streaming_attention_state_init(3, hq, d, dev())
+    qd, kd, vd, vald = q.cuda(), k.cuda(), v.cuda(), valid.cuda()
+    for s in range(0, 337, 100):
+        streaming_attention_step(qd, kd[:, :, s:s + 100], vd[:, :, s:s + 100], m, l, acc,
+                                 valid=vald[:, s:s + 100].contiguous())
+    ref, rmass = dense(q, k, v, n_rep, tpb=16, valid=valid)
+    assert max_abs(streaming_attention_finalize(acc, l, dtype), ref) < TOL
+    out, mass = _two_pass_with_tail(q, k, v, 16, 64, valid=valid)
+    assert max_abs(out, ref) < TOL
+    assert max_abs(mass, rmass[:, :, :mass.shape[2]]) < 1e-4
+
+
+def test_fp32_dev_cases_at_1e4():
+    """The reference's fp32 dev cases (bench/streaming_attention_triton_kernel_mvp.py:488 and
+    :557-566): 200 tokens in one fold, and the grouped two-pass with 16-token block mass, at
+    rtol = atol = 1e-4 against the dense fp32 result."""
+    q, k, v = draw(80, (1, HQ, D), (1, HKV, 200, D), (1, HKV, 200, D), dtype=torch.float32)
+    m, l, acc = streaming_attention_state_init(1, HQ, D, dev())
+    streaming_attention_step(q.cuda(), k.cuda(), v.cuda(), m, l, acc)
+    out = streaming_attention_finalize(acc, l, torch.float32)
+    ref, rmass = dense(q, k, v, 7, tpb=16)
+    assert torch.allclose(out.cpu(), ref, rtol=1e-4, atol=1e-4)
+    out2, mass = _two_pass_with_tail(q, k, v, 16, 64)
+    assert torch.allclose(out2.cpu(), ref, rtol=1e-4, atol=1e-4)
+    assert torch.allclose(mass, rmass[:, :, :mass.shape[2]], rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(14, 2, 8), (8, 2, 16), (14, 2, 32), (14, 2, 64), (32, 8, 128), (16, 2, 256)])
+def test_fp32_qkv_every_head_dim(hq, hkv, d):
+    """fp32 q/k/v at every head dim, ragged chunks with a padding mask and an inactive row,
+    softcap, against the oracle at 1e-4; P is not rounded (its dtype is fp32)."""
+    n_rep = hq // hkv
+    q, k, v = draw(90 + d, (3, hq, d), (3, hkv, 411, d), (3, hkv, 411, d), dtype=torch.float32, scale=0.5)
+    valid = torch.ones(3, 411, dtype=torch.int32)
+    valid[0, 300:] = 0
+    active = torch.tensor([1, 1, 0], dtype=torch.int32)
+    m, l, acc = streaming_attention_state_init(3, hq, d, dev())
+    qd, kd, vd = q.cuda(), k.cuda(), v.cuda()
+    for s in range(0, 411, 137):
+        streaming_attention_step(qd, kd[:, :, s:s + 137], vd[:, :, s:s + 137], m, l, acc,
+                                 valid=valid[:, s:s + 137].contiguous().cuda(), active=active.cuda(), softcap=30.0)
+    out = streaming_attention_finalize(acc, l, torch.float32)
+    ref, _ = dense(q, k, v, n_rep, valid=valid, softcap=30.0)
+    assert torch.allclose(out[:2].cpu(), ref[:2], rtol=1e-4, atol=1e-4)
+    assert torch.isinf(m[2]).all() and (l[2] == 0).all() and (acc[2] == 0).all()  # inactive row untouched
+
+
+def test_unsupported_head_dim_is_rejected():
+    q = torch.zeros(1, 8, 48, dtype=torch.float16, device=dev())
+    k = torch.zeros(1, 2, 8, 48, dtype=torch.float16, device=dev())
+    m, l, acc = streaming_attention_state_init(1, 8, 48, dev())
+    with pytest.raises(NotImplementedError):
+        streaming_attention_step(q, k, k, m, l, acc)
