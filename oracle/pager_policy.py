@@ -403,3 +403,40 @@ class Pager:
         ram_used = sum(block.size for block in self.blocks if block.tier == RAM)
         self.metrics.vram_peak = max(self.metrics.vram_peak, vram_used)
         self.metrics.ram_peak = max(self.metrics.ram_peak, ram_used)
+
+
+def selection_margin(pager: Pager) -> dict:
+    """How close the pager's last placement came to a different choice, for reporting.
+
+    sinks_heavy_hitter (core.rs:257-318): after the sinks and the recent budget, the scored
+    blocks are taken best first; returns the EMA score gap between the last block taken and
+    the first block left out (``gap``), with their ids and the number taken by score.
+    heavy_hitter (core.rs:368-400): ``gap`` = promote_margin - (best non-VRAM score - worst
+    unpinned VRAM score), i.e. how far the last comparison was from a swap. Other policies
+    ignore scores: gap None. Computed from the pager's current tiers and scores."""
+    blocks = pager.blocks
+    max_vram = pager.vram // BLOCK_SIZE_BYTES
+    if pager.policy == SINKS_HEAVY_HITTER and max_vram > 0:
+        fixed = set(b.id for b in blocks[:SINK_BLOCKS][:max_vram])
+        remaining = max(max_vram - len(fixed), 0)
+        recent_budget = min(pager.recent_window, max(max_vram // 2, 1), remaining)
+        for b in blocks[max(len(blocks) - recent_budget, 0):]:
+            if len(fixed) >= max_vram:
+                break
+            fixed.add(b.id)
+        scored = _stable_sort([(b.id, b.score) for b in blocks if b.id not in fixed],
+                              lambda a, b: compare_scores(b[1], a[1]))
+        n_taken = min(max(max_vram - len(fixed), 0), len(scored))
+        if 0 < n_taken < len(scored):
+            last, first_out = scored[n_taken - 1], scored[n_taken]
+            return {"gap": float(last[1]) - float(first_out[1]), "taken": n_taken, "last": last[0],
+                    "first_out": first_out[0]}
+        return {"gap": None, "taken": n_taken}
+    if pager.policy == HEAVY_HITTER:
+        vram = [b for b in blocks if b.tier == VRAM and not b.pinned]
+        other = [b for b in blocks if b.tier != VRAM]
+        if vram and other:
+            worst = min(float(b.score) for b in vram)
+            best = max(float(b.score) for b in other)
+            return {"gap": float(pager.promote_margin) - (best - worst)}
+    return {"gap": None}

@@ -177,7 +177,11 @@ class PagedModel:
             self._lock.release()
 
     def _close(self) -> None:
+        # Releasing the last graph of a memory pool releases the pool: the next capture needs
+        # a new pool handle (capturing into the released one fails inside the allocator).
         self._graphs.clear()
+        self._graph_pool = None
+        self._graph_warm = False
         if self._decoder is not None:
             self._decoder.pool.close()
         self._decoder = None
