@@ -88,9 +88,11 @@ class PagedDecodeOracle:
         self.sessions[sid].lo = list(lo)
 
     def prefill(self, sid, keys, values, n_tokens, *, place=True):
-        """keys[layer] [rows, Hkv, n_src, D] arrays (any float dtype holding the stored values)."""
+        """keys[layer] [rows, Hkv, n_src, D] arrays (any float dtype holding the stored values).
+        keys = values = None registers the length only: such a session takes part in
+        placement and gather lists (step with compute=False and no q/k/v), not in attention."""
         s = self.sessions[sid]
-        for layer in range(self.num_layers):
+        for layer in range(self.num_layers if keys is not None else 0):
             for r in range(s.rows):
                 for store, src in ((s.keys, keys), (s.values, values)):
                     buf = np.zeros((self.hkv, n_tokens + 256, self.d), np.float32)
@@ -131,7 +133,8 @@ class PagedDecodeOracle:
         return buf_k[:, : n + 1], buf_v[:, : n + 1]
 
     def step(self, sids, q, k_new, v_new, compute=True):
-        """q[layer] [S, Hq, D]; k_new/v_new[layer] [S, Hkv, D] (float32 arrays of the stored values).
+        """q[layer] [S, Hq, D]; k_new/v_new[layer] [S, Hkv, D] (float32 arrays of the stored values);
+        with compute=False they may be None (placement and gather lists only).
 
         Returns a dict with per-layer outputs, per-sequence gather ids, per-session block
         scores handed to the pager and the moves of apply_tiers. With compute=False the
@@ -147,6 +150,8 @@ class PagedDecodeOracle:
             per_session = {sid: [] for sid in sids}
             for i, (sid, r) in enumerate(seqs):
                 s = self.sessions[sid]
+                if not compute and (k_new is None or s.keys[layer][r] is None):
+                    continue  # placement only
                 k, v = self._append(sid, r, layer, k_new[layer][i], v_new[layer][i])
                 if not compute:
                     continue
