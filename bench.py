@@ -1,5 +1,9 @@
 """Decode-attention throughput of the fused paged path on one MI355X.
 
+By default the line also carries configurations 1, 3, 4 and 5 as sub-records under
+"configs" (each with its own step or token rate, HBM and host-link GB/s against their peaks,
+and the reference's CPU path timed on its K/V); --configs "" leaves them out.
+
 Workload (one "step" = one decode step of one layer over the whole batch): Qwen2.5-0.5B
 attention geometry (14 query heads, 2 KV heads, head_dim 64, fp16, 32-token blocks), batch 8,
 contexts drawn uniform in [1024, 32768] from a seed, each sequence keeping its 64 most recent
@@ -138,15 +142,34 @@ def hbm_all_resident(layers, steps, warmup):
     }
 
 
+KERNEL_SOURCES = ("rust-llm-pager_amd/csrc/attn_kernels.hip", "rust-llm-pager_amd/csrc/pgr_common.h",
+                  "rust-llm-pager_amd/build.py")
+
+
+def kernel_source_hash():
+    """sha256 (first 16 hex digits) of the decode kernel's source and build flags: a counter
+    summary measured on other sources is not reported as this kernel's traffic."""
+    import hashlib
+
+    h = hashlib.sha256()
+    for rel in KERNEL_SOURCES:
+        with open(os.path.join(ROOT, rel), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:16]
+
+
 def committed_traffic(workload_layers):
     """HBM bytes per launch of the all-resident kernel from the committed counter summary
-    (FETCH_SIZE and WRITE_SIZE scaled by a plain copy's readings), or None."""
+    (FETCH_SIZE and WRITE_SIZE scaled by a plain copy's readings), or None when the summary
+    was measured on other kernel sources or another workload."""
     path = os.path.join(ROOT, "profiles", "paged_attn_all_resident_traffic.json")
     if not os.path.exists(path):
         return None
     with open(path) as f:
         t = json.load(f)
     if t.get("layers") != workload_layers or t.get("batch") != CFG["batch"]:
+        return None
+    if t.get("kernel_source_sha256_16") != kernel_source_hash():
         return None
     return t.get("traffic_bytes_per_launch")
 
@@ -189,12 +212,15 @@ def continuous(args):
                          max_new_tokens=m) for n, m in zip(lens, outs)]
     eng = sched.engine()
     host_bytes = [0]
+    hbm_bytes = [0]
     orig_step = eng.step
+    kv_tok = 2 * 2 * 128 * 2 * 28  # K+V bytes of one token over all layers
 
     def step(sessions, tokens):
         out = orig_step(sessions, tokens)
         if len(sessions) > 1:
             host_bytes[0] += eng.host_bytes_per_step()
+            hbm_bytes[0] += eng.decoder.pool.step_stats()["resident_tokens"] * kv_tok
         return out
 
     eng.step = step
@@ -204,8 +230,9 @@ def continuous(args):
     torch.cuda.synchronize()
     t_open = time.perf_counter() - t_open
     tokens0 = sum(len(r.generated_tokens) for r in reqs)
-    host_bytes[0] = 0
+    host_bytes[0] = hbm_bytes[0] = 0
     live = sum(r.context_tokens for r in sched._active)
+    live_lens = [r.context_tokens for r in sched._active]
     t0 = time.perf_counter()
     for _ in range(args.cb_rounds):
         sched._admit_new_requests()
@@ -215,6 +242,7 @@ def continuous(args):
     tokens = sum(len(r.generated_tokens) for r in reqs) - tokens0
     sched.stop()
     link = host_bytes[0] / dt / 1e9
+    hbm = hbm_bytes[0] / dt / 1e9
     return {
         "metric": "continuous-batching decode tokens/s (64 concurrent, Qwen2.5-1.5B arch, 4 GB HBM K/V budget)",
         "value": round(tokens / dt, 2),
@@ -225,7 +253,11 @@ def continuous(args):
         "live_tokens_at_start": live,
         "first_round_s": round(t_open, 2),
         "host_link": {"achieved": round(link, 3), "peak": LINK_PEAK_GBS, "unit": "GB/s",
-                      "frac": round(link / LINK_PEAK_GBS, 4)},
+                      "frac": round(link / LINK_PEAK_GBS, 4),
+                      "bytes_per_round": host_bytes[0] // args.cb_rounds},
+        "hbm": {"achieved": round(hbm, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(hbm / HBM_PEAK_GBS, 4),
+                "bytes_per_round": hbm_bytes[0] // args.cb_rounds},
+        "live_context_lengths": live_lens,
         "dtype": "bf16",
         "data": "synthetic: random-init weights, random token ids",
         "config": {"workload": "continuous batching, Qwen2.5-1.5B architecture, 64 concurrent, prompts lognormal("
@@ -327,92 +359,114 @@ def _cpu_attention_rate(groups, n_rep, d, budget_s):
         torch.set_num_threads(previous)
 
 
-def configs(args):
-    """Configurations 1, 3 and 4 measured the way configurations 2 and 5 are, each with the
-    reference's CPU path (dense fp32 attention and block mass in torch on the host threads)
-    timed on the same in-scope K/V.
+def _rate(bytes_per_step, seconds_per_step, peak):
+    gbs = bytes_per_step / seconds_per_step / 1e9
+    return {"bytes_per_step": int(bytes_per_step), "GBs": round(gbs, 3), "peak": peak, "frac": round(gbs / peak, 4)}
 
-    1: one Qwen2.5-0.5B layer (14q/2kv, D 64, fp16), batch 1, 4096 tokens in 32-token blocks,
-       the 8 most recent blocks in HBM and 120 on host, 128 steps.
-    3: TinyLlama-1.1B architecture (22 layers, 32q/4kv, D 64, fp16, random init), 8192 prompt
-       tokens, 256 greedy tokens, sinks_heavy_hitter with a 41-block budget and 8 recent
-       blocks; decode only (the prompt is registered by a first call).
-    4: one Mistral-7B layer (32q/8kv, D 128, bf16), batch 4, 131072 tokens, window 4096:
-       32 in-window blocks in HBM and 96 on host, 32 steps."""
+
+def _cpu_record(kv_bytes, seconds, tokens, threads, sample):
+    """The reference's CPU path on the same in-scope K/V: GB/s and tokens/s."""
+    return {"value": round(kv_bytes / seconds / 1e9, 3), "unit": "GB/s", "tokens_per_s": round(tokens / seconds, 2),
+            "cores": threads, "kind": "port", "sample": sample}
+
+
+def _layer_config(args, name, *, hq, hkv, d, dtype, batch, ctx, resident, window, steps, warmup):
+    """One decoder layer over `batch` sequences of `ctx` tokens, the `resident` most recent blocks
+    in HBM (recent_only) and the rest on host, optionally a sliding window; `steps` decode steps,
+    each appending one token per sequence."""
     import torch
 
-    from pager_hf import PagedDecoder, PagedModel
+    from pager_hf import PagedDecoder
 
-    rows = {}
+    T = 32
+    nb = ctx // T
+    dec = PagedDecoder(num_layers=1, num_query_heads=hq, num_kv_heads=hkv, head_dim=d, tokens_per_block=T,
+                       dtype=dtype, device="cuda", pool_blocks=batch * (resident + 8),
+                       host_blocks=batch * (nb + 8), staging_blocks=64, staging_buffers=2)
+    g = torch.Generator(device="cuda").manual_seed(ctx)
+    sids, cpu_groups = [], []
+    for _ in range(batch):
+        sid = dec.add_session(capacity_tokens=ctx + steps + warmup + 64, vram_budget=resident * MIB16,
+                              ram_budget=1 << 42, recent_window=resident - 1, policy="recent_only")
+        k = (torch.randn(1, hkv, ctx, d, device="cuda", generator=g) * 0.5).to(dtype)
+        v = (torch.randn(1, hkv, ctx, d, device="cuda", generator=g) * 0.5).to(dtype)
+        dec.prefill(sid, [k], [v], ctx)
+        lo = ctx - (window or ctx)
+        cpu_groups.append((k[0, :, lo:].cpu(), v[0, :, lo:].cpu()))
+        del k, v
+        sids.append(sid)
+    q = (torch.randn(batch, hq, d, device="cuda", generator=g) * 0.5).to(dtype)
+    kn = (torch.randn(batch, hkv, d, device="cuda", generator=g) * 0.5).to(dtype)
+    host = res_tok = 0
 
-    def layer_run(name, *, hq, hkv, d, dtype, batch, ctx, resident, window, steps, warmup):
-        T = 32
-        nb = ctx // T
-        dec = PagedDecoder(num_layers=1, num_query_heads=hq, num_kv_heads=hkv, head_dim=d, tokens_per_block=T,
-                           dtype=dtype, device="cuda", pool_blocks=batch * (resident + 8),
-                           host_blocks=batch * (nb + 8), staging_blocks=64, staging_buffers=2)
-        g = torch.Generator(device="cuda").manual_seed(ctx)
-        sids, cpu_groups = [], []
-        for _ in range(batch):
-            sid = dec.add_session(capacity_tokens=ctx + steps + warmup + 64, vram_budget=resident * MIB16,
-                                  ram_budget=1 << 42, recent_window=resident - 1, policy="recent_only")
-            k = (torch.randn(1, hkv, ctx, d, device="cuda", generator=g) * 0.5).to(dtype)
-            v = (torch.randn(1, hkv, ctx, d, device="cuda", generator=g) * 0.5).to(dtype)
-            dec.prefill(sid, [k], [v], ctx)
-            lo = ctx - (window or ctx)
-            cpu_groups.append((k[0, :, lo:].cpu(), v[0, :, lo:].cpu()))
-            del k, v
-            sids.append(sid)
-        q = (torch.randn(batch, hq, d, device="cuda", generator=g) * 0.5).to(dtype)
-        kn = (torch.randn(batch, hkv, d, device="cuda", generator=g) * 0.5).to(dtype)
-        host = res_tok = 0
+    def one(i):
+        if window:
+            for sid in sids:
+                dec.set_lo(sid, [ctx + i - window + 1])
+        dec.begin_step(sids)
+        st = dec.pool.step_stats()
+        dec.decode_layer(0, q, kn, kn)
+        dec.end_step(collect=False)
+        return st
 
-        def one(i):
-            nonlocal host, res_tok
-            if window:
-                for sid in sids:
-                    dec.set_lo(sid, [ctx + i - window + 1])
-            dec.begin_step(sids)
-            st = dec.pool.step_stats()
-            dec.decode_layer(0, q, kn, kn)
-            dec.end_step(collect=False)
-            return st
+    for i in range(warmup):
+        one(i)
+    torch.cuda.synchronize()
+    dec.pool.sync()
+    t0 = time.perf_counter()
+    for i in range(warmup, warmup + steps):
+        st = one(i)
+        host += st["host_tokens"]
+        res_tok += st["resident_tokens"]
+    torch.cuda.synchronize()
+    dec.pool.sync()
+    dt = (time.perf_counter() - t0) / steps
+    dec.pool.close()
+    tok_bytes = 2 * hkv * d * 2
+    host_b, hbm_b = host / steps * tok_bytes, res_tok / steps * tok_bytes
+    cpu_s, threads = _cpu_attention_rate(cpu_groups, hq // hkv, d, args.cpu_seconds / 3)
+    cpu_bytes = sum(k.numel() * 2 * 2 for k, _ in cpu_groups)
+    return {
+        "workload": name,
+        "steps": steps,
+        "ms_per_step": round(dt * 1e3, 4),
+        "tokens_per_s": round(batch / dt, 1),
+        "kv_GBs": round((host_b + hbm_b) / dt / 1e9, 2),
+        "host_link": _rate(host_b, dt, LINK_PEAK_GBS),
+        "hbm": _rate(hbm_b, dt, HBM_PEAK_GBS),
+        "cpu_baseline": _cpu_record(cpu_bytes, cpu_s, batch, threads,
+                                    f"dense fp32 attention and block mass in torch over the same in-scope K/V of "
+                                    f"all {batch} sequences, repeated for ~{args.cpu_seconds / 3:.0f} s"),
+    }
 
-        for i in range(warmup):
-            one(i)
-        torch.cuda.synchronize()
-        dec.pool.sync()
-        t0 = time.perf_counter()
-        for i in range(warmup, warmup + steps):
-            st = one(i)
-            host += st["host_tokens"]
-            res_tok += st["resident_tokens"]
-        torch.cuda.synchronize()
-        dec.pool.sync()
-        dt = (time.perf_counter() - t0) / steps
-        dec.pool.close()
-        tok_bytes = 2 * hkv * d * 2
-        host_b, hbm_b = host / steps * tok_bytes, res_tok / steps * tok_bytes
-        cpu_s, threads = _cpu_attention_rate(cpu_groups, hq // hkv, d, args.cpu_seconds / 3)
-        cpu_bytes = sum(k.numel() * 2 * 2 for k, _ in cpu_groups)
-        rows[name] = {
-            "ms_per_step": round(dt * 1e3, 4),
-            "tokens_per_s": round(batch / dt, 1),
-            "kv_GBs": round((host_b + hbm_b) / dt / 1e9, 2),
-            "host_link": {"bytes_per_step": int(host_b), "GBs": round(host_b / dt / 1e9, 2),
-                          "frac_of_64": round(host_b / dt / 1e9 / LINK_PEAK_GBS, 4)},
-            "hbm": {"bytes_per_step": int(hbm_b), "GBs": round(hbm_b / dt / 1e9, 2)},
-            "cpu_baseline": {"kv_GBs": round(cpu_bytes / cpu_s / 1e9, 3), "tokens_per_s": round(batch / cpu_s, 1),
-                             "cores": threads, "kind": "port"},
-        }
 
-    layer_run("1", hq=14, hkv=2, d=64, dtype=torch.float16, batch=1, ctx=4096, resident=8, window=None, steps=128,
-              warmup=8)
-    layer_run("4", hq=32, hkv=8, d=128, dtype=torch.bfloat16, batch=4, ctx=131072, resident=32, window=4096,
-              steps=32, warmup=4)
+def config1(args):
+    import torch
 
-    # Configuration 3: the whole model through PagedModel.
+    return _layer_config(args, "one Qwen2.5-0.5B layer (14q/2kv, D 64, fp16), batch 1, 4096 tokens in 32-token "
+                               "blocks: the 8 most recent in HBM, 120 on host (recent_only); 128 steps",
+                         hq=14, hkv=2, d=64, dtype=torch.float16, batch=1, ctx=4096, resident=8, window=None,
+                         steps=128, warmup=8)
+
+
+def config4(args):
+    import torch
+
+    return _layer_config(args, "one Mistral-7B layer (32q/8kv, D 128, bf16), batch 4, 131072 tokens, window 4096: "
+                               "32 in-window blocks in HBM, 96 on host; 32 steps",
+                         hq=32, hkv=8, d=128, dtype=torch.bfloat16, batch=4, ctx=131072, resident=32, window=4096,
+                         steps=32, warmup=4)
+
+
+def config3(args):
+    """TinyLlama-1.1B architecture (22 layers, 32q/4kv, D 64, intermediate 5632, fp16, random
+    init), 8192 random prompt ids, 256 greedy tokens, sinks_heavy_hitter with a 41-block budget
+    (4 sinks + 8 recent + 29 by score) and 32-token blocks; decode steps replayed from HIP
+    graphs (eager for comparison). The prompt is registered by a first generate() call."""
+    import torch
     from transformers import LlamaConfig, LlamaForCausalLM
+
+    from pager_hf import PagedModel
 
     cfg = LlamaConfig(hidden_size=2048, intermediate_size=5632, num_hidden_layers=22, num_attention_heads=32,
                       num_key_value_heads=4, vocab_size=32000, max_position_embeddings=8448 + 64, rms_norm_eps=1e-5)
@@ -437,38 +491,89 @@ def configs(args):
         timed[graphs] = ((time.perf_counter() - t0) / n_new, pm.last_run_stats)
         pm.reset()
     dt, st = timed[True]
-    host_b = st.total_cpu_to_gpu_mb * 1e6 / n_new
-    kv_tok = 2 * 4 * 64 * 2 * 22
-    in_scope = 8192 + n_new // 2
     del model
     torch.cuda.empty_cache()
+    kv_tok = 2 * 4 * 64 * 2 * 22  # K+V bytes of one token over all layers
+    in_scope = 8192 + n_new // 2  # mean context over the timed tokens
+    host_b = st.total_cpu_to_gpu_mb * 1e6 / n_new
+    hbm_b = in_scope * kv_tok - host_b
     # CPU: the attention of one decode step over all 22 layers at the mean context.
     gen = torch.Generator().manual_seed(9)
     groups = [((torch.randn(4, in_scope, 64, generator=gen) * 0.5).half(),
                (torch.randn(4, in_scope, 64, generator=gen) * 0.5).half()) for _ in range(22)]
     cpu_s, threads = _cpu_attention_rate(groups, 8, 64, args.cpu_seconds / 3)
-    rows["3"] = {
+    return {
+        "workload": "TinyLlama-1.1B architecture (22 layers, 32q/4kv, D 64, fp16, random init), 8192-token prompt, "
+                    "256 greedy tokens, sinks_heavy_hitter 41 blocks (4 sinks + 8 recent + 29 scored), 32-token "
+                    "blocks, decode steps from HIP graphs",
+        "tokens": n_new,
         "ms_per_token": round(dt * 1e3, 3),
         "tokens_per_s": round(1 / dt, 1),
         "eager_ms_per_token": round(timed[False][0] * 1e3, 3),
-        "note": "decode steps replayed from captured HIP graphs (use_hip_graphs=True); eager for comparison",
         "kv_GBs": round(in_scope * kv_tok / dt / 1e9, 2),
-        "host_link": {"bytes_per_token": int(host_b), "GBs": round(host_b / dt / 1e9, 2),
-                      "frac_of_64": round(host_b / dt / 1e9 / LINK_PEAK_GBS, 4)},
+        "host_link": _rate(host_b, dt, LINK_PEAK_GBS),
+        "hbm": _rate(hbm_b, dt, HBM_PEAK_GBS),
         "mean_attention_in_gpu": round(st.mean_attention_in_gpu, 4),
-        "cpu_baseline": {"kv_GBs": round(in_scope * kv_tok / cpu_s / 1e9, 3), "tokens_per_s": round(1 / cpu_s, 1),
-                         "cores": threads, "kind": "port", "note": "attention of all 22 layers only"},
+        "cpu_baseline": _cpu_record(in_scope * kv_tok, cpu_s, 1, threads,
+                                    f"dense fp32 attention and block mass in torch for all 22 layers of one decode "
+                                    f"step at the mean context ({in_scope} tokens), repeated for "
+                                    f"~{args.cpu_seconds / 3:.0f} s; attention only, not the model's other layers"),
     }
+
+
+def config5(args):
+    """Continuous batching (see continuous()), as a sub-record with the reference's CPU attention
+    path timed on a bounded sample of the same round."""
+    import numpy as np
+    import torch
+
+    res = continuous(args)
+    lens = res["live_context_lengths"]
+    kv_tok_layer = 2 * 2 * 128 * 2
+    round_bytes = sum(lens) * kv_tok_layer * 28  # every layer's in-scope K/V of one round
+    # CPU sample: 8 sessions drawn from the live ones (contexts capped at 16384), 2 layers each.
+    rng = np.random.default_rng(7)
+    pick = [min(int(n), 16384) for n in rng.choice(lens, 8, replace=False)]
+    gen = torch.Generator().manual_seed(10)
+    groups = [((torch.randn(2, n, 128, generator=gen) * 0.5).bfloat16(),
+               (torch.randn(2, n, 128, generator=gen) * 0.5).bfloat16()) for n in pick for _ in range(2)]
+    cpu_s, threads = _cpu_attention_rate(groups, 6, 128, args.cpu_seconds / 3)
+    sample_bytes = sum(k.numel() * 2 * 2 for k, _ in groups)
+    cpu_gbs = sample_bytes / cpu_s / 1e9
+    round_s = round_bytes / (cpu_gbs * 1e9)
+    dt = res["ms_per_round"] / 1e3
     return {
-        "metric": "per-configuration decode-attention measurements (configurations 1, 3, 4)",
-        "value": rows["4"]["kv_GBs"],
-        "unit": "GB/s",
-        "higher_is_better": True,
-        "configs": rows,
-        "dtype": "fp16 (1, 3), bf16 (4)",
-        "data": "synthetic K/V and random-init weights",
-        "config": {"workload": "configurations 1, 3 and 4 as specified; value is configuration 4's K/V GB/s"},
+        "workload": res["config"]["workload"] + "; 4 GB real HBM K/V bytes = 68 logical blocks per session; "
+                                                "recent_only; staged host streaming with cross-layer prefetch",
+        "rounds": res["rounds"],
+        "ms_per_round": res["ms_per_round"],
+        "tokens_per_s": res["value"],
+        "live_tokens_at_start": res["live_tokens_at_start"],
+        "host_link": {"bytes_per_step": res["host_link"]["bytes_per_round"], "GBs": res["host_link"]["achieved"],
+                      "peak": LINK_PEAK_GBS, "frac": res["host_link"]["frac"]},
+        "hbm": {"bytes_per_step": res["hbm"]["bytes_per_round"], "GBs": res["hbm"]["achieved"],
+                "peak": HBM_PEAK_GBS, "frac": res["hbm"]["frac"]},
+        "kv_GBs": round((res["host_link"]["bytes_per_round"] + res["hbm"]["bytes_per_round"]) / dt / 1e9, 2),
+        "cpu_baseline": {"value": round(cpu_gbs, 3), "unit": "GB/s", "tokens_per_s": round(64 / round_s, 2),
+                         "cores": threads, "kind": "port",
+                         "sample": f"dense bf16->fp32 attention and block mass in torch over 8 of the live sessions "
+                                   f"(contexts {pick}, capped at 16384) x 2 layers for ~{args.cpu_seconds / 3:.0f} s; "
+                                   f"tokens/s = 64 / (one round's {round_bytes / 1e9:.1f} GB of in-scope K/V at "
+                                   f"that rate)"},
     }
+
+
+CONFIG_RUNNERS = {"1": config1, "3": config3, "4": config4, "5": config5}
+
+
+def configs(args):
+    """The other configurations, each as a sub-record (see config1/3/4/5)."""
+    names = [c for c in args.configs.split(",") if c]
+    out = {}
+    for name in names:
+        print(f"[bench] configuration {name}", file=sys.stderr, flush=True)
+        out[name] = CONFIG_RUNNERS[name](args)
+    return out
 
 
 def hbm_scale(args):
@@ -543,6 +648,33 @@ def hbm_scale(args):
     }
 
 
+def calibrate_host_read(mib):
+    """Reads `mib` MiB of host-resident records once with records_to_hf_kernel, which reads the
+    pinned host mirror in place through its device mapping: a known number of bytes over the
+    host link (K and V of every host block of one layer), for the host-link read counters.
+    Returns the bytes read from host memory."""
+    import torch
+
+    from pager_hf import PagedDecoder
+
+    T, hkv, d = 32, 2, 64
+    rec = 2 * hkv * T * d * 2
+    n_blocks = (mib << 20) // rec
+    n = n_blocks * T
+    dec = PagedDecoder(num_layers=1, num_query_heads=14, num_kv_heads=hkv, head_dim=d, tokens_per_block=T,
+                       dtype=torch.float16, device="cuda", pool_blocks=8, host_blocks=n_blocks + 8, staging_blocks=8)
+    sid = dec.add_session(capacity_tokens=n + 64, vram_budget=MIB16, ram_budget=1 << 42, recent_window=0,
+                          policy="recent_only")
+    k = torch.zeros(1, hkv, n, d, dtype=torch.float16, device="cuda")
+    dec.prefill(sid, [k], [k], n)
+    host_blocks = len(dec.pool.block_ids(sid, False))
+    torch.cuda.synchronize()
+    dec.pool.export_tokens(sid, 0, 0, n)  # one launch: host records read in place, resident ones from HBM
+    torch.cuda.synchronize()
+    dec.pool.close()
+    return host_blocks * rec
+
+
 class SimpleTokenizer:
     eos_token_id = None
 
@@ -614,9 +746,12 @@ def main() -> int:
                     help="layers of the all-resident HBM measurement (0 skips it)")
     ap.add_argument("--workload", choices=["batch8", "continuous", "register", "configs", "hbm-scale"],
                     default="batch8",
-                    help="batch8: the headline line; continuous: the 64-request continuous-batching run; "
-                         "register: prompt registration at 8k-64k tokens; configs: configurations 1, 3, 4; "
+                    help="batch8: the headline line (configuration 2, plus the configurations in --configs as "
+                         "sub-records); continuous: the 64-request continuous-batching run alone; register: prompt "
+                         "registration at 8k-64k tokens; configs: only the configurations in --configs; "
                          "hbm-scale: the all-resident kernel against bytes per launch")
+    ap.add_argument("--configs", default="1,3,4,5",
+                    help="other configurations measured into the line (comma list of 1, 3, 4, 5; empty for none)")
     ap.add_argument("--register-reps", type=int, default=3)
     ap.add_argument("--cb-rounds", type=int, default=24)
     ap.add_argument("--cb-extra-requests", type=int, default=64)
@@ -626,7 +761,10 @@ def main() -> int:
     ap.add_argument("--cb-staging-blocks", type=int, default=8192, help="records per staging buffer (staged mode)")
     ap.add_argument("--cb-staging-buffers", type=int, default=2, help="staging buffers (staged mode)")
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
-                    help="after timing, run one device copy of this size (counter calibration)")
+                    help="after timing, run one device copy of this size (HBM counter calibration)")
+    ap.add_argument("--calibration-host-mib", type=int, default=0,
+                    help="after timing, read this many MiB of host-resident records once through the host mirror's "
+                         "device mapping (host-link counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1).", file=sys.stderr)
@@ -643,8 +781,8 @@ def main() -> int:
         print(json.dumps(line), flush=True)
         return 0
     if args.workload == "configs":
-        line = configs(args)
-        line.update({"n_gpus": 1, "steps": None, "warmup": None, "scaling": "weak", "vs_baseline": None})
+        line = {"metric": "per-configuration decode-attention measurements", "configs": configs(args),
+                "n_gpus": 1, "scaling": "weak", "vs_baseline": None, "data": "synthetic K/V and random-init weights"}
         print(json.dumps(line), flush=True)
         return 0
     if args.workload == "register":
@@ -741,6 +879,9 @@ def main() -> int:
         dst.copy_(src)
         torch.cuda.synchronize()
         line["calibration_copy_bytes"] = n
+        del src, dst
+    if args.calibration_host_mib:
+        line["calibration_host_read_bytes"] = calibrate_host_read(args.calibration_host_mib)
     dec.pool.close()
     del dec
     line["roofline"] = None
@@ -757,12 +898,15 @@ def main() -> int:
             "unit": "GB/s",
             "frac": kern["frac"],
             "traffic": committed_traffic(args.resident_layers),
+            "kernel_source_sha256_16": kernel_source_hash(),
             "launches": kern["launches"],
             "avg_launch_us": kern["avg_launch_us"],
             "bytes_per_launch": kern["bytes_per_launch"],
         }
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(ctx, args.cpu_seconds)
+    if args.configs:
+        line["configs"] = configs(args)
     print(json.dumps(line), flush=True)
     return 0
 
