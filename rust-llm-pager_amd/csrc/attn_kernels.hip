@@ -21,9 +21,10 @@
 // contiguous run of D/4 elements of K row n: chunk c, k-slot 4g+i <-> dim (D/4)g + 4c + i.
 // V is read as four token rows of D/16 contiguous elements (dims (D/16)n .. +D/16) and
 // transposed in registers with v_perm_b32 into the A operand of each of the D/16 M-tiles;
-// M-tile j, row r <-> dim (D/16)r + j. All global loads are 16/8/4-byte per lane. One K load
-// instruction covers half of each of the tile's 16 rows. One V load instruction covers four
-// whole rows, or at head_dim 64 a quarter of each of the 16 rows (see load_tile_rs).
+// M-tile j, row r <-> dim (D/16)r + j. In the dense kernel all global loads are 16/8/4-byte
+// per lane and one K load instruction covers half of each of the tile's 16 rows. The paged
+// kernel reads records whose V is stored transposed in groups of four tokens (PTile), so its
+// V operands arrive as 16-byte loads in MFMA order with no permutes.
 //
 // P is rounded to the K/V element type before the P.V product, as the reference does
 // (streaming_attention.py:178, :347, :428).
@@ -143,10 +144,10 @@ __device__ __forceinline__ u32x2 v_tile(const uint32_t (&v)[4][D / 32], int j) {
 
 // S^T tile of 16 tokens x 16 heads.
 template <class Ty, int D>
-__device__ __forceinline__ f32x4 qk_tile(const Tile<D>& t, const u32x4 (&q)[D / 32]) {
+__device__ __forceinline__ f32x4 qk_tile(const u32x4 (&k)[D / 32], const u32x4 (&q)[D / 32]) {
   f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int c = 0; c < D / 16; ++c) s = Ty::mma(k_chunk<D>(t.k, c), k_chunk<D>(q, c), s);
+  for (int c = 0; c < D / 16; ++c) s = Ty::mma(k_chunk<D>(k, c), k_chunk<D>(q, c), s);
   return s;
 }
 
@@ -335,7 +336,7 @@ __global__ __launch_bounds__(256) void dense_attn_kernel(DenseArgs a) {
       for (int i = 0; i < 4; ++i)
         if (!ok[i]) zero_v_row<D>(t, i);
     }
-    const f32x4 s4 = qk_tile<Ty, D>(t, q);
+    const f32x4 s4 = qk_tile<Ty, D>(t.k, q);
     float s[4], p[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) s[i] = ok[i] ? transform_score(s4[i], a.scale, a.softcap) : kNegInf;
@@ -696,59 +697,39 @@ constexpr float kLazyRescale = 8.0f;
 constexpr float kMInit = -1.0e30f;  // running max before any valid score (finite: 2^(-inf - kMInit) = 0)
 
 
-// One 16-token tile through a buffer resource: K row n (bytes k_lane from the K tile) and V
-// rows 4g..4g+3 (v_lane, then +D elements). `r` covers one KV head of one record, `sk` / `sv` are
-// the tile's K and V byte offsets (wave-uniform, in SGPRs). A resource with no records makes
-// every load of the tile return zeros without a memory access.
-//
-// At head_dim 64, V load i of lane (g, n) reads row 4g + (i + n) % 4, so that one instruction
-// touches all 16 rows (cache lines) of the V tile rather than 4. Reads of the host mirror over
-// the host link run about 2% faster that way; unrotate_v puts the rows back in order before
-// the fold. At head_dim 128 (two lines per row) the same rotation read the host link 8%
-// slower, so the other head dims load rows in order.
+// Registers of one 16-token tile in the decode kernel, both read as D/2 contiguous bytes per
+// lane: K row n, dims (D/4)g .. (D/4)g + D/4 - 1 (the chunks of the S^T products), and V in
+// the record's transposed layout (v_record_index, pgr_kernels.h): tokens 4g..4g+3 of dims
+// (D/16)n .. (D/16)n + D/16 - 1, four tokens per dim, which are the A operands of the D/16
+// O^T products as they stand (M-tile j = dwords 2j, 2j + 1).
 template <int D>
-constexpr bool kRotateV = D == 64;
+struct PTile {
+  u32x4 k[D / 32];
+  u32x4 v[D / 32];
+};
 
 constexpr int kBufferFlags = 0x00020000;  // dword 3 of a raw buffer resource on gfx9
 
+// One tile through a buffer resource: `r` covers one KV head of one record, `sk` / `sv` are the
+// tile's K and V byte offsets (wave-uniform, in SGPRs), `k_lane` / `v_lane` the lane's offsets
+// in them. Each load instruction covers every other 16 bytes of the tile's K (or V) bytes, the
+// next instruction the rest. A resource with no records makes every load return zeros without
+// a memory access.
 template <int D>
-__device__ __forceinline__ void load_tile_rs(Tile<D>& t, __amdgpu_buffer_rsrc_t r, uint32_t sk, uint32_t sv,
+__device__ __forceinline__ void load_tile_rs(PTile<D>& t, __amdgpu_buffer_rsrc_t r, uint32_t sk, uint32_t sv,
                                              uint32_t k_lane, uint32_t v_lane) {
 #pragma unroll
-  for (int i = 0; i < Tile<D>::KV4; ++i) t.k[i] = __builtin_amdgcn_raw_buffer_load_b128(r, k_lane + 16u * i, sk, 0);
-  const int rot = kRotateV<D> ? (int)(__lane_id() & 3) : 0;  // n % 4
+  for (int i = 0; i < D / 32; ++i) t.k[i] = __builtin_amdgcn_raw_buffer_load_b128(r, k_lane + 16u * i, sk, 0);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t off = v_lane + (uint32_t)(((i + rot) & 3) * D * 2);
-    if constexpr (D == 32) {
-      t.v[i][0] = __builtin_amdgcn_raw_buffer_load_b32(r, off, sv, 0);
-    } else if constexpr (D == 64) {
-      const u32x2 x = __builtin_amdgcn_raw_buffer_load_b64(r, off, sv, 0);
-      t.v[i][0] = x.x;
-      t.v[i][1] = x.y;
-    } else {
-      const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(r, off, sv, 0);
-      t.v[i][0] = x.x;
-      t.v[i][1] = x.y;
-      t.v[i][2] = x.z;
-      t.v[i][3] = x.w;
-    }
-  }
+  for (int i = 0; i < D / 32; ++i) t.v[i] = __builtin_amdgcn_raw_buffer_load_b128(r, v_lane + 16u * i, sv, 0);
 }
 
-// Undoes the lane rotation of load_tile_rs: slot i holds row (i + r) % 4 with r = n % 4, so
-// row k sits in slot (k - r) % 4. Two select stages shift by r & 1, then by r & 2.
-template <int D>
-__device__ __forceinline__ void unrotate_v(Tile<D>& t, bool r1, bool r2) {
+// O^T[D x 16 heads] += V^T . P^T with the transposed V tile.
+template <class Ty, int D>
+__device__ __forceinline__ void pv_tile_t(f32x4 (&acc)[D / 16], const PTile<D>& t, const float (&p)[4]) {
+  const u32x2 pb = {Ty::pack(p[0], p[1]), Ty::pack(p[2], p[3])};
 #pragma unroll
-  for (int w = 0; w < Tile<D>::VW; ++w) {
-    const uint32_t a0 = t.v[0][w], a1 = t.v[1][w], a2 = t.v[2][w], a3 = t.v[3][w];
-    const uint32_t b0 = r1 ? a3 : a0, b1 = r1 ? a0 : a1, b2 = r1 ? a1 : a2, b3 = r1 ? a2 : a3;
-    t.v[0][w] = r2 ? b2 : b0;
-    t.v[1][w] = r2 ? b3 : b1;
-    t.v[2][w] = r2 ? b0 : b2;
-    t.v[3][w] = r2 ? b1 : b3;
-  }
+  for (int j = 0; j < D / 16; ++j) acc[j] = Ty::mma(k_chunk<D>(t.v, j), pb, acc[j]);
 }
 
 struct TileMeta {
@@ -788,7 +769,7 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(const WorkItem* __restr
   const int count = wi->entry_count, partial = wi->partial;
   const int append_slot = wi->append_slot, append_pos = wi->append_pos;
   const uint32_t k_lane = (uint32_t)(n * D + (D / 4) * g) * 2u;
-  const uint32_t v_lane = (uint32_t)(4 * g * D + (D / 16) * n) * 2u;
+  const uint32_t v_lane = (uint32_t)lane * (D / 2);  // lane (g, n) = 16 g + n: its transposed V run
 
   if (a.work_out != nullptr) {
     // First launch of a step: `work` is the pinned plan buffer. This workgroup's work item
@@ -830,7 +811,7 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(const WorkItem* __restr
   // the loop is unconditional, so the load counter stays in order; a fetch past the wave's
   // last tile goes through an empty buffer resource and returns at once with zeros.
   int nf = 0, fe = 0, ftb = 0;
-  auto fetch = [&](Tile<D>& t, TileMeta& mt) {
+  auto fetch = [&](PTile<D>& t, TileMeta& mt) {
     const int slot = ecur.slot, bid = ecur.block_id;
     const uint16_t* rb = slot >= 0 ? pool + (size_t)slot * rec : stage + (size_t)(-slot - 1) * rec;
     const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
@@ -849,23 +830,30 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(const WorkItem* __restr
     }
   };
 
-  const bool rot1 = (n & 1) != 0, rot2 = (n & 2) != 0;
-  auto fold = [&](Tile<D>& t, const TileMeta& mt) {
-    if constexpr (kRotateV<D>) unrotate_v<D>(t, rot1, rot2);
-    f32x4 s4 = qk_tile<Ty, D>(t, q);
+  auto fold = [&](PTile<D>& t, const TileMeta& mt) {
+    f32x4 s4 = qk_tile<Ty, D>(t.k, q);
     if (capped) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) s4[i] = a.softcap * tanhf(s4[i] * cap_in);
     }
     if (mt.t0 < lo || mt.t0 + 16 > hi) {  // tile straddles the valid range: mask per token
+      // Token 4g + i of the lane's V operands is 16-bit half (i & 1) of dwords x / z (i < 2)
+      // or y / w (i >= 2): a masked token's V is zeroed, so stale record bytes never reach P.V.
+      uint32_t mx = 0xffffffffu, my = 0xffffffffu;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int tok = mt.t0 + 4 * g + i;
         if (tok < lo || tok >= hi) {
           s4[i] = kNegInf;
-          zero_v_row<D>(t, i);
+          const uint32_t keep = (i & 1) ? 0x0000ffffu : 0xffff0000u;
+          if (i < 2)
+            mx &= keep;
+          else
+            my &= keep;
         }
       }
+#pragma unroll
+      for (int w = 0; w < D / 32; ++w) t.v[w] &= u32x4{mx, my, mx, my};
     }
     const float lmax = fmaxf(fmaxf(s4[0], s4[1]), fmaxf(s4[2], s4[3])) * mult;
     if (__builtin_amdgcn_ballot_w64(lmax > m_thr) != 0) {
@@ -883,7 +871,7 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(const WorkItem* __restr
     for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s4[i], mult, -m_run));
     const float psum = (p[0] + p[1]) + (p[2] + p[3]);
     l_run += psum;
-    pv_tile<Ty, D>(acc, t, p);
+    pv_tile_t<Ty, D>(acc, t, p);
     if constexpr (kMass) {
       blk += psum;
       if (mt.last >= 0) {  // block complete: (m_b, s_b) of this block to LDS, stored after the loop
@@ -898,7 +886,7 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(const WorkItem* __restr
   };
 
   if (tiles > 0) {
-    Tile<D> buf[NB];
+    PTile<D> buf[NB];
     TileMeta meta[NB];
     // Tile 0, then q, then the rest of the prologue: q is needed by the first fold, and
     // waiting for it here (which also waits for tile 0, as loads return in order) keeps
@@ -934,9 +922,9 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(const WorkItem* __restr
   // block record. No workgroup of this launch reads that position (work covers [lo, hi)).
   if (append_slot >= 0 && threadIdx.x < D) {
     const size_t src = ((size_t)seq * a.hkv + h) * D + threadIdx.x;
-    uint16_t* dst = pool + (size_t)append_slot * rec + head_off + (size_t)append_pos * D + threadIdx.x;
-    dst[0] = a.k_new[src];
-    dst[v_off] = a.v_new[src];
+    uint16_t* rec_base = pool + (size_t)append_slot * rec;
+    rec_base[head_off + (size_t)append_pos * D + threadIdx.x] = a.k_new[src];
+    rec_base[v_off + v_record_index(h, append_pos, threadIdx.x, T, D)] = a.v_new[src];
   }
 
   const size_t slot = (size_t)partial;

@@ -1,8 +1,9 @@
 // KV block-store data movement kernels: reference block layout <-> pool records.
 // (The decode token is appended by the fused attention kernel.)
 //
-// Pool record layout for one (block, sequence row, layer): K [Hkv][T][D] followed by
-// V [Hkv][T][D]; every element is 16-bit (fp16 or bf16) and moved as raw bits.
+// Pool record layout for one (block, sequence row, layer): K [Hkv][T][D] followed by V in
+// 16-token tiles of four-token transposed groups (v_record_index, pgr_kernels.h); every
+// element is 16-bit (fp16 or bf16) and moved as raw bits.
 #include <hip/hip_runtime.h>
 
 #include "pgr_common.h"
@@ -25,9 +26,8 @@ __global__ void ref_to_records_kernel(const uint16_t* key, const uint16_t* value
     const int h = (int)(r / d);
     const int dd = (int)(r - (size_t)h * d);
     uint16_t* kr = pool + (size_t)slots[b] * rec;
-    const size_t dst = ((size_t)h * tpb + t) * d + dd;
-    kr[dst] = key[i];
-    kr[per_row + dst] = value[i];
+    kr[((size_t)h * tpb + t) * d + dd] = key[i];
+    kr[per_row + v_record_index(h, t, dd, tpb, d)] = value[i];
   }
 }
 
@@ -44,9 +44,8 @@ __global__ void records_to_ref_kernel(const uint16_t* pool, const int32_t* slots
     const int h = (int)(r / d);
     const int dd = (int)(r - (size_t)h * d);
     const uint16_t* kr = pool + (size_t)slots[b] * rec;
-    const size_t src = ((size_t)h * tpb + t) * d + dd;
-    key[i] = kr[src];
-    value[i] = kr[per_row + src];
+    key[i] = kr[((size_t)h * tpb + t) * d + dd];
+    value[i] = kr[per_row + v_record_index(h, t, dd, tpb, d)];
   }
 }
 

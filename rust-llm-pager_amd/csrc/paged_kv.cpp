@@ -20,13 +20,31 @@ namespace pgr {
 
 namespace {
 
+// V chunk c (16 bytes) of a record's V region holds dims d0, d0 + 1 of four consecutive tokens
+// (v_record_index): tile `tile` of head `h`, tokens 16 tile + 4g .. + 3. Maps c to those.
+struct VChunk {
+  int h, tok0, d0;
+};
+__device__ __forceinline__ VChunk v_chunk(int c, int tpb, int d) {
+  const int per_head = tpb * d / 8;  // 16-byte chunks of one head's V
+  const int h = c / per_head;
+  const int rem = c - h * per_head;
+  const int tile = rem / (2 * d);
+  const int q = 2 * (rem - tile * 2 * d);  // first of the chunk's two four-token groups
+  const int dn = d / 16;
+  const int j = q % dn, n = (q / dn) % 16, g = q / (16 * dn);
+  return VChunk{h, tile * 16 + 4 * g, dn * n + j};
+}
+
 // One workgroup per block of records: converts tokens of one (row, layer) from the
 // [Hkv, n_src, D] layout into records at dst + slot[i] * rec (zero past n_tokens), or back.
 __global__ void hf_to_records_kernel(const uint16_t* k, const uint16_t* v, int64_t n_src, int64_t n_tokens,
                                      const int64_t* dst, uint16_t* pool, uint16_t* host, int hkv, int tpb, int d) {
   // Block i of a [Hkv, n_src, D] tensor pair into its record: dst[i] >= 0 is an HBM pool
   // slot, dst[i] < 0 the host mirror record -dst[i] - 1 (written in place over the host
-  // link). 16 bytes per load and store; tokens past n_tokens are zero.
+  // link). 16 bytes per store; tokens past n_tokens are zero. K chunk c is 8 dims of one
+  // token row; V chunk c is 2 dims of 4 tokens (the record's transposed V tiles), gathered
+  // from four 4-byte loads.
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
   const int64_t b = blockIdx.x;
   const int64_t di = dst[b];
@@ -40,22 +58,26 @@ __global__ void hf_to_records_kernel(const uint16_t* k, const uint16_t* v, int64
     const int r = c - h * tpb * cpr;
     const int t = r / cpr, cc = r - t * cpr;
     const int64_t tok = b * tpb + t;
-    u32x4 kx = {0u, 0u, 0u, 0u}, vx = {0u, 0u, 0u, 0u};
-    if (tok < n_tokens) {
-      const size_t src = ((size_t)h * n_src + tok) * d + (size_t)cc * 8;
-      kx = *reinterpret_cast<const u32x4*>(k + src);
-      vx = *reinterpret_cast<const u32x4*>(v + src);
+    u32x4 kx = {0u, 0u, 0u, 0u};
+    if (tok < n_tokens) kx = *reinterpret_cast<const u32x4*>(k + ((size_t)h * n_src + tok) * d + (size_t)cc * 8);
+    *reinterpret_cast<u32x4*>(kr + (size_t)(h * tpb + t) * d + (size_t)cc * 8) = kx;
+    const VChunk vc = v_chunk(c, tpb, d);
+    uint32_t p[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t vt = b * tpb + vc.tok0 + i;
+      p[i] = vt < n_tokens ? *reinterpret_cast<const uint32_t*>(v + ((size_t)vc.h * n_src + vt) * d + vc.d0) : 0u;
     }
-    const size_t o = (size_t)(h * tpb + t) * d + (size_t)cc * 8;
-    *reinterpret_cast<u32x4*>(kr + o) = kx;
-    *reinterpret_cast<u32x4*>(vr + o) = vx;
+    const u32x4 vx = {(p[0] & 0xffffu) | (p[1] << 16), (p[2] & 0xffffu) | (p[3] << 16),
+                      (p[0] >> 16) | (p[1] & 0xffff0000u), (p[2] >> 16) | (p[3] & 0xffff0000u)};
+    *reinterpret_cast<u32x4*>(vr + (size_t)c * 8) = vx;
   }
 }
 
 __global__ void records_to_hf_kernel(const int64_t* src, const uint16_t* pool, const uint16_t* host,
                                      int64_t n_tokens, uint16_t* k, uint16_t* v, int hkv, int tpb, int d) {
   // Record of block i (src[i] >= 0: pool slot; < 0: host mirror record -src[i] - 1, read in
-  // place over the host link) into k, v [Hkv, n_tokens, D]. 16 bytes per load and store.
+  // place over the host link) into k, v [Hkv, n_tokens, D]. 16 bytes per load.
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
   const int64_t b = blockIdx.x;
   const int64_t si = src[b];
@@ -69,11 +91,16 @@ __global__ void records_to_hf_kernel(const int64_t* src, const uint16_t* pool, c
     const int r = c - h * tpb * cpr;
     const int t = r / cpr, cc = r - t * cpr;
     const int64_t tok = b * tpb + t;
-    if (tok < n_tokens) {
-      const size_t o = (size_t)(h * tpb + t) * d + (size_t)cc * 8;
-      const size_t dst = ((size_t)h * n_tokens + tok) * d + (size_t)cc * 8;
-      *reinterpret_cast<u32x4*>(k + dst) = *reinterpret_cast<const u32x4*>(kr + o);
-      *reinterpret_cast<u32x4*>(v + dst) = *reinterpret_cast<const u32x4*>(vr + o);
+    const u32x4 kx = *reinterpret_cast<const u32x4*>(kr + (size_t)(h * tpb + t) * d + (size_t)cc * 8);
+    if (tok < n_tokens) *reinterpret_cast<u32x4*>(k + ((size_t)h * n_tokens + tok) * d + (size_t)cc * 8) = kx;
+    const VChunk vc = v_chunk(c, tpb, d);
+    const u32x4 w = *reinterpret_cast<const u32x4*>(vr + (size_t)c * 8);
+    const uint32_t p[4] = {(w.x & 0xffffu) | (w.z << 16), (w.x >> 16) | (w.z & 0xffff0000u),
+                           (w.y & 0xffffu) | (w.w << 16), (w.y >> 16) | (w.w & 0xffff0000u)};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t vt = b * tpb + vc.tok0 + i;
+      if (vt < n_tokens) *reinterpret_cast<uint32_t*>(v + ((size_t)vc.h * n_tokens + vt) * d + vc.d0) = p[i];
     }
   }
 }

@@ -7,6 +7,24 @@
 
 namespace pgr {
 
+// V layout inside a record. K is stored row by row, [Hkv][T][D]. V is stored in 16-token tiles,
+// [Hkv][T/16][16 * D], and inside a tile in groups of four tokens transposed: element (token r
+// of the tile, dim d) sits at vt_index(r, d, D). With DN = D / 16, the run of 4 * DN elements at
+// ((r / 4) * 16 + n) * 4 * DN holds tokens 4(r/4)..4(r/4)+3 of dims DN*n .. DN*n + DN - 1, four
+// tokens per dim: exactly the V^T operands of the MFMA tiles that decode-kernel lane
+// (g = r / 4, n) feeds, so that lane loads one contiguous run (D/2 bytes, the size of its K run)
+// and uses it as it arrives. D is a multiple of 16.
+__host__ __device__ __forceinline__ int vt_index(int r, int d, int D) {
+  const int dn = D / 16;
+  return (((r >> 2) * 16 + d / dn) * dn + d % dn) * 4 + (r & 3);
+}
+
+// Element offset of V (head h, token t of the block, dim d) from the start of the record's V
+// region (T tokens per block).
+__host__ __device__ __forceinline__ size_t v_record_index(int h, int t, int d, int T, int D) {
+  return ((size_t)h * T + (size_t)(t & ~15)) * D + (size_t)vt_index(t & 15, d, D);
+}
+
 struct DenseLaunch {
   const void* q;
   const void* k;
