@@ -93,12 +93,13 @@ def run_steps(dec, sids, q, kn, vn, out, first, count, stats):
         dec.end_step(collect=False)
 
 
-def hbm_all_resident(layers, steps, warmup):
+def hbm_all_resident(layers, steps, warmup, target_wg=0, blocks_per_wg=32):
     """The same batch with every block resident in HBM, over `layers` layers (one launch pair
     per layer, so the K/V read per step exceeds the 256 MB MALL and comes from HBM)."""
     import torch
 
-    dec, sids, ctx, q, kn, vn, out = build(warmup + 2 * steps, resident_blocks=1100, layers=layers)
+    dec, sids, ctx, q, kn, vn, out = build(warmup + 2 * steps, resident_blocks=1100, layers=layers,
+                                          target_wg=target_wg, blocks_per_wg=blocks_per_wg)
     stats = {"resident_tokens": 0, "host_tokens": 0, "copies": 0, "launches": 0}
     run_steps(dec, sids, q, kn, vn, out, 0, warmup, stats)
     # Pass 1: step rate (no per-launch events).
@@ -886,7 +887,7 @@ def main() -> int:
     del dec
     line["roofline"] = None
     if args.resident_layers > 0:
-        res = hbm_all_resident(args.resident_layers, max(4, min(args.steps, 16)), 2)
+        res = hbm_all_resident(args.resident_layers, max(4, min(args.steps, 16)), 2, args.target_wg, args.blocks_per_wg)
         line["hbm_all_resident"] = res
         kern = res["kernel"]
         line["roofline"] = {
