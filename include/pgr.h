@@ -31,7 +31,7 @@ extern "C" {
 
 #define PGR_DTYPE_F16 0
 #define PGR_DTYPE_BF16 1
-#define PGR_DTYPE_F32 2 /* pgr_attn_finalize output only */
+#define PGR_DTYPE_F32 2 /* operator API only (q/k/v and finalize output); the KV store is 16-bit */
 
 /* ---- library ------------------------------------------------------------------------- */
 
@@ -44,7 +44,9 @@ const char* pgr_last_error(void);
  * Shapes follow pager_hf/streaming_attention.py: q [B, Hq, D]; k, v [B, Hkv, Tc, D]
  * contiguous; valid [B, Tc] int32 0/1 or NULL (all valid); active [B] int32 or NULL (all
  * active); online-softmax state m, l [B, Hq] and acc [B, Hq, D] fp32, updated in place.
- * D in {32, 64, 128}; Hq / Hkv <= 16; scale > 0; softcap <= 0 disables softcapping.
+ * q, k, v share one dtype: fp16, bf16 or fp32. D in {8, 16, 32, 64, 128, 256} (16-bit at
+ * 32/64/128 runs on MFMA, the rest on a VALU kernel); Hq / Hkv <= 16; scale > 0; softcap <= 0
+ * disables softcapping. Anything else returns PGR_ERR_UNSUPPORTED.
  * `workspace` must hold pgr_attn_workspace_bytes(...) bytes of device memory.
  */
 #define PGR_MODE_FOLD 0
