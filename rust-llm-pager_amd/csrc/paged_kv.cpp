@@ -119,13 +119,16 @@ __global__ void copy_records_kernel(void* const* bases, int src_tbl, int dst_tbl
 }
 
 // Staged mode: records of one layer's host mirror (read in place through its device mapping)
-// into a staging buffer, by (host record, staging record) pairs. A fixed grid of a few dozen
+// into a staging buffer, by (host record, staging record) pairs: those of one chunk,
+// [chunk_begin[0], chunk_begin[1]), read from the uploaded plan so that the launch is the
+// same from step to step (a captured graph replays it). A fixed grid of a few dozen
 // workgroups keeps the host link busy while leaving the CUs to concurrent work.
 constexpr int kStageCopyWorkgroups = 96;
-__global__ void stage_copy_kernel(const void* host, void* stage, const int64_t* pairs, int64_t n_pairs,
+__global__ void stage_copy_kernel(const void* host, void* stage, const int64_t* pairs, const int64_t* chunk_begin,
                                   int64_t rec_vec) {
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-  for (int64_t p = blockIdx.x; p < n_pairs; p += gridDim.x) {
+  const int64_t end = chunk_begin[1];
+  for (int64_t p = chunk_begin[0] + blockIdx.x; p < end; p += gridDim.x) {
     const u32x4* src = static_cast<const u32x4*>(host) + (size_t)pairs[2 * p] * rec_vec;
     u32x4* dst = static_cast<u32x4*>(stage) + (size_t)pairs[2 * p + 1] * rec_vec;
     for (int64_t i = threadIdx.x; i < rec_vec; i += blockDim.x) dst[i] = src[i];
@@ -178,6 +181,7 @@ PagedKV::~PagedKV() {
     hipEventDestroy(t.stop);
   }
   if (plan_uploaded_) hipEventDestroy(plan_uploaded_);
+  if (cap_fork_) hipEventDestroy(cap_fork_);
   if (stage_copies_done_) hipEventDestroy(stage_copies_done_);
   if (moves_done_) hipEventDestroy(moves_done_);
   if (decode_done_) hipEventDestroy(decode_done_);
@@ -292,6 +296,8 @@ int PagedKV::init() {
   PGR_HIP(hipStreamCreateWithFlags(&copy_stream_, hipStreamNonBlocking));
   buf_free_.resize(cfg_.staging_buffers);
   chunk_ready_.resize(cfg_.staging_buffers);
+  buf_free_cap_.assign(cfg_.staging_buffers, 0);
+  buf_free_eager_.assign(cfg_.staging_buffers, 0);
   // Ordering events. They order GPU work against GPU work, or tell the host that the GPU has
   // finished reading a pinned buffer; none guards device writes that the host then reads
   // (the mass read-back synchronizes its stream). So none needs the system-scope release
@@ -303,6 +309,7 @@ int PagedKV::init() {
     PGR_HIP(hipEventCreateWithFlags(&chunk_ready_[i], ev_flags));
   }
   PGR_HIP(hipEventCreateWithFlags(&plan_uploaded_, ev_flags));
+  PGR_HIP(hipEventCreateWithFlags(&cap_fork_, ev_flags));
   for (PlanBuf& b : plan_bufs_) PGR_HIP(hipEventCreateWithFlags(&b.read, ev_flags));
   PGR_HIP(hipHostMalloc(reinterpret_cast<void**>(&plan_flags_), 256, hipHostMallocDefault));
   std::memset(plan_flags_, 0, 256);
@@ -931,7 +938,7 @@ int PagedKV::begin_step(const int32_t* sids, int n, hipStream_t stream) {
             used_in_chunk = 0;
           }
           const int64_t take = std::min(e - cur, chunk_cap - used_in_chunk);
-          const int64_t stage_rec = (int64_t)((stage_base_ + chunk) % cfg_.staging_buffers) * chunk_cap + used_in_chunk;
+          const int64_t stage_rec = (int64_t)(chunk % cfg_.staging_buffers) * chunk_cap + used_in_chunk;
           copies_.push_back(CopyCmd{s.row[r].host_off + cur, stage_rec, take, chunk});
           for (int64_t x = 0; x < take; ++x)
             pend.push_back({seq, BlockEntry{(int32_t)(-(stage_rec + x) - 1), (int32_t)(cur + x)}, chunk});
@@ -952,15 +959,15 @@ int PagedKV::begin_step(const int32_t* sids, int n, hipStream_t stream) {
   const bool any_host = !copies_.empty();
   n_chunks_ = any_host ? chunk + 1 : 0;
   // Cross-layer prefetch (staged mode): when the step's host blocks fit one chunk and there
-  // are two or more buffers, layer l reads buffer (base + l) % buffers, and decode_layer(l)
-  // queues layer l+1's copies right after layer l's attention. The copies then run under the
-  // rest of layer l's work (projections, MLP), which leaves the host link idle otherwise.
+  // are two or more buffers, layer l reads buffer l % buffers, and decode_layer(l) queues
+  // layer l+1's copies right after layer l's attention. The copies then run under the rest
+  // of layer l's work (projections, MLP), which leaves the host link idle otherwise. Chunk c
+  // of a step without prefetch uses buffer c % buffers. Every step starts on buffer 0, so
+  // a step's launches are the same as the last step's when its plan has the same shape.
   prefetch_step_ = n_chunks_ == 1 && cfg_.staging_buffers >= 2;
   prefetched_layer_ = -1;
-  // The next step starts on the buffer after this step's last one, so its first copy does
-  // not wait for this step's last reader.
-  step_stage_base_ = stage_base_;
-  stage_base_ = (stage_base_ + (prefetch_step_ ? cfg_.num_layers : n_chunks_)) % cfg_.staging_buffers;
+  cap_forked_ = false;
+  std::fill(buf_free_cap_.begin(), buf_free_cap_.end(), 0);
   const int n_launch = std::max(1, n_chunks_);
   // Work items. A launch is cut into whole rounds of target_wg / Hkv work items of nearly
   // equal size: the fewest rounds whose items hold at most E_max entries each, so that
@@ -1073,10 +1080,13 @@ int PagedKV::begin_step(const int32_t* sids, int n, hipStream_t stream) {
     off = align_up(off + bytes, 256);
     return at;
   };
-  // Plan: the per-sequence and per-session arrays, the staging pairs, then the work items.
+  // Plan: the per-sequence and per-session arrays, the chunks' bounds in the staging pair
+  // list, the work items, then the pairs (ahead of the work items, only the bounds array,
+  // which holds 32 chunks in its 256 bytes, so the work items stay where they were).
   const size_t o_seqs = carve(sizeof(SeqInfo) * S);
   const size_t o_srows = carve(sizeof(int32_t) * std::max(n, 1));
   const size_t o_sfirst = carve(sizeof(int32_t) * std::max(n, 1));
+  const size_t o_cbegin = carve(sizeof(int64_t) * (size_t)(n_chunks_ + 1));
   // Staged mode: (host record, staging record) per record to stream, chunk by chunk.
   stage_pairs_.clear();
   chunk_pair_begin_.assign(n_chunks_ + 1, 0);
@@ -1088,8 +1098,8 @@ int PagedKV::begin_step(const int32_t* sids, int n, hipStream_t stream) {
     chunk_pair_begin_[c.chunk + 1] = (int64_t)stage_pairs_.size() / 2;
   }
   for (int c = 1; c <= n_chunks_; ++c) chunk_pair_begin_[c] = std::max(chunk_pair_begin_[c], chunk_pair_begin_[c - 1]);
-  const size_t o_spairs = carve(sizeof(int64_t) * std::max<size_t>(stage_pairs_.size(), 2));
   const size_t o_work = carve(sizeof(WorkItem) * std::max<size_t>(work_.size(), 1));
+  const size_t o_spairs = carve(sizeof(int64_t) * std::max<size_t>(stage_pairs_.size(), 2));
   const size_t plan_bytes = off;
   const size_t o_pm = carve(sizeof(float) * (size_t)n_partials_ * hq);
   const size_t o_pl = carve(sizeof(float) * (size_t)n_partials_ * hq);
@@ -1132,6 +1142,7 @@ int PagedKV::begin_step(const int32_t* sids, int n, hipStream_t stream) {
   std::memcpy(h + o_work, work_.data(), sizeof(WorkItem) * work_.size());
   std::memcpy(h + o_srows, sess_rows.data(), sizeof(int32_t) * n);
   std::memcpy(h + o_sfirst, sess_first.data(), sizeof(int32_t) * n);
+  std::memcpy(h + o_cbegin, chunk_pair_begin_.data(), sizeof(int64_t) * chunk_pair_begin_.size());
   if (!stage_pairs_.empty()) std::memcpy(h + o_spairs, stage_pairs_.data(), sizeof(int64_t) * stage_pairs_.size());
   char* d = static_cast<char*>(ws_);
   // A staging copy queued for a layer that was never decoded may still read the previous
@@ -1160,6 +1171,7 @@ int PagedKV::begin_step(const int32_t* sids, int n, hipStream_t stream) {
   d_sess_rows_ = reinterpret_cast<int32_t*>(d + o_srows);
   d_sess_first_ = reinterpret_cast<int32_t*>(d + o_sfirst);
   d_stage_pairs_ = reinterpret_cast<int64_t*>(d + o_spairs);
+  d_chunk_begin_ = reinterpret_cast<int64_t*>(d + o_cbegin);
   d_pm_ = reinterpret_cast<float*>(d + o_pm);
   d_pl_ = reinterpret_cast<float*>(d + o_pl);
   d_pacc_ = reinterpret_cast<float*>(d + o_pacc);
@@ -1211,34 +1223,42 @@ int PagedKV::decode_layer(int layer, const void* q, const void* k_new, const voi
   const int nbuf = cfg_.staging_buffers;
   // Side stream: wait until the previous reader of buffer `buf` finished, then stream the
   // host runs of chunk `L` of layer `lay` into it. `shift` moves the plan's records (laid out
-  // for the step's first buffer) to buffer `buf`.
+  // for buffer 0) to buffer `buf`.
   auto issue_copies = [&](int lay, int L, int buf, int64_t shift) -> int {
-    // The pair list is part of the step plan: wait for its upload and for the buffer's last reader.
-    PGR_HIP(hipStreamWaitEvent(copy_stream_, plan_uploaded_, 0));
-    PGR_HIP(hipStreamWaitEvent(copy_stream_, buf_free_[buf], 0));
-    const int64_t p0 = chunk_pair_begin_[L], np = chunk_pair_begin_[L + 1] - p0;
-    if (np > 0) {
-      const unsigned grid = (unsigned)std::min<int64_t>(np, kStageCopyWorkgroups);
-      stage_copy_kernel<<<grid, 256, 0, copy_stream_>>>(host_dev_[lay], static_cast<char*>(stage_) + shift * (int64_t)rec,
-                                                        d_stage_pairs_ + 2 * p0, np, (int64_t)(rec / 16));
-      PGR_HIP(hipGetLastError());
+    if (capturing) {
+      // Everything queued before the graph's launch precedes it: join the capture once, then
+      // wait only for this step's readers of the buffer.
+      if (!cap_forked_) {
+        PGR_HIP(hipEventRecord(cap_fork_, stream));
+        PGR_HIP(hipStreamWaitEvent(copy_stream_, cap_fork_, 0));
+        cap_forked_ = true;
+      }
+      if (buf_free_cap_[buf]) PGR_HIP(hipStreamWaitEvent(copy_stream_, buf_free_[buf], 0));
+    } else {
+      // The pair list is part of the step plan: wait for its upload (which follows every
+      // earlier step, replayed ones included) and for the buffer's last reader.
+      PGR_HIP(hipStreamWaitEvent(copy_stream_, plan_uploaded_, 0));
+      if (buf_free_eager_[buf]) PGR_HIP(hipStreamWaitEvent(copy_stream_, buf_free_[buf], 0));
     }
-    for (const CopyCmd& c : copies_)
-      if (c.chunk == L) stats_.stream_copies += 1;
-    stats_.stream_bytes += (size_t)np * rec;
+    stage_copy_kernel<<<kStageCopyWorkgroups, 256, 0, copy_stream_>>>(
+        host_dev_[lay], static_cast<char*>(stage_) + shift * (int64_t)rec, d_stage_pairs_, d_chunk_begin_ + L,
+        (int64_t)(rec / 16));
+    PGR_HIP(hipGetLastError());
     PGR_HIP(hipEventRecord(chunk_ready_[buf], copy_stream_));
-    PGR_HIP(hipEventRecord(stage_copies_done_, copy_stream_));
-    stage_copy_pending_ = true;
+    if (!capturing) {
+      // A capture is joined back by the launches that wait on chunk_ready_, and a replay ends
+      // with its copies; only eager copies may still run when the next step begins.
+      PGR_HIP(hipEventRecord(stage_copies_done_, copy_stream_));
+      stage_copy_pending_ = true;
+    }
     return kOk;
   };
-  auto layer_buf = [&](int lay) { return (step_stage_base_ + lay) % nbuf; };
-  auto layer_shift = [&](int lay) {
-    return (int64_t)(layer_buf(lay) - step_stage_base_ % nbuf) * cfg_.staging_slots;
-  };
+  auto layer_buf = [&](int lay) { return lay % nbuf; };
+  auto layer_shift = [&](int lay) { return (int64_t)layer_buf(lay) * cfg_.staging_slots; };
   uint32_t* merge_flag = nullptr;  // set when this call makes the step's first (plan-reading) launch
   uint32_t merge_token = 0;
   for (int L = 0; L < n_launch; ++L) {
-    const int buf = prefetch_step_ ? layer_buf(layer) : (step_stage_base_ + L) % nbuf;
+    const int buf = prefetch_step_ ? layer_buf(layer) : L % nbuf;
     if (n_chunks_ > 0) {
       if (!(prefetch_step_ && prefetched_layer_ == layer)) {
         const int rc = issue_copies(layer, L, buf, prefetch_step_ ? layer_shift(layer) : 0);
@@ -1297,7 +1317,11 @@ int PagedKV::decode_layer(int layer, const void* q, const void* k_new, const voi
       t.bytes = ent * (int64_t)T * 2 * cfg_.head_dim * 2 * cfg_.kv_heads;  // K+V bytes read, whole blocks
       timing_pending_.push_back(t);
     }
-    if (n_chunks_ > 0) PGR_HIP(hipEventRecord(buf_free_[buf], stream));
+    if (n_chunks_ > 0) {
+      PGR_HIP(hipEventRecord(buf_free_[buf], stream));
+      buf_free_cap_[buf] = capturing;
+      buf_free_eager_[buf] = !capturing;
+    }
   }
   prefetched_layer_ = -1;
   if (prefetch_step_ && layer + 1 < cfg_.num_layers) {
@@ -1345,7 +1369,9 @@ int PagedKV::step_signature(int64_t* out, int64_t cap) const {
       (int64_t)(uintptr_t)d_pl_, (int64_t)(uintptr_t)d_pacc_, (int64_t)(uintptr_t)d_mass_m_,
       (int64_t)(uintptr_t)d_mass_s_, (int64_t)(uintptr_t)d_mf_, (int64_t)(uintptr_t)d_lf_,
       (int64_t)cfg_.stream_mode, (int64_t)seqs_.size(), (int64_t)step_sids_.size(), (int64_t)mass_stride_,
-      (int64_t)launch_work_begin_.size(), (int64_t)(uintptr_t)plan_bufs_[plan_buf_].dev, (int64_t)plan_on_device_};
+      (int64_t)launch_work_begin_.size(), (int64_t)(uintptr_t)plan_bufs_[plan_buf_].dev, (int64_t)plan_on_device_,
+      (int64_t)n_chunks_, (int64_t)prefetch_step_, (int64_t)(uintptr_t)d_stage_pairs_,
+      (int64_t)(uintptr_t)d_chunk_begin_};
   for (size_t L = 0; L < launch_work_begin_.size(); ++L) {
     v.push_back(launch_work_begin_[L]);
     v.push_back(launch_work_end_[L]);
@@ -1358,9 +1384,11 @@ int PagedKV::step_signature(int64_t* out, int64_t cap) const {
 int PagedKV::end_step(int32_t* completed, int* n_completed) {
   if (!in_step_) return fail(kErrState, "end_step without begin_step");
   const int64_t T = cfg_.tokens_per_block;
-  // Host blocks read in place this step, every layer (counted here rather than per launch,
-  // so that steps replayed from a captured graph are counted too).
-  if (cfg_.stream_mode == 0) stats_.stream_bytes += (uint64_t)step_stats_.host_blocks * rec_bytes() * cfg_.num_layers;
+  // Host blocks read in place (direct mode) or copied to staging (staged mode) this step, every
+  // layer (counted here rather than per launch, so that steps replayed from a captured graph
+  // are counted too).
+  stats_.stream_bytes += (uint64_t)step_stats_.host_blocks * rec_bytes() * cfg_.num_layers;
+  if (cfg_.stream_mode == 1) stats_.stream_copies += (uint64_t)copies_.size() * cfg_.num_layers;
   int c = 0;
   for (size_t i = 0; i < step_sids_.size(); ++i) {
     Session& s = sessions_[step_sids_[i]];

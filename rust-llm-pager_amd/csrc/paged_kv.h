@@ -280,6 +280,15 @@ class PagedKV {
   bool stage_copy_pending_ = false;
   std::vector<hipEvent_t> buf_free_;
   std::vector<hipEvent_t> chunk_ready_;
+  // Staging under stream capture. A capture may wait only on events recorded in it: the copy
+  // stream joins it through cap_fork_, recorded on the capturing stream before the step's
+  // first copy, and a copy waits on buf_free_[b] only where this step recorded it, in the
+  // same mode (buf_free_cap_ under capture, buf_free_eager_ otherwise). Work recorded
+  // before a replay precedes the whole graph on its stream.
+  hipEvent_t cap_fork_ = nullptr;
+  bool cap_forked_ = false;
+  std::vector<char> buf_free_cap_;
+  std::vector<char> buf_free_eager_;
   std::vector<int32_t> free_slots_;
   std::vector<std::pair<int64_t, int64_t>> host_free_;  // (offset, count), sorted by offset
   std::vector<Session> sessions_;
@@ -302,13 +311,12 @@ class PagedKV {
   int n_chunks_ = 0;
   int n_partials_ = 0;
   int mass_stride_ = 0;
-  int stage_base_ = 0;       // staging buffer of the next step's first chunk
   std::vector<int64_t> stage_pairs_;      // staged mode: (host record, staging record) pairs
   std::vector<int64_t> chunk_pair_begin_;  // first pair of each chunk, and the end
   int64_t* d_stage_pairs_ = nullptr;       // the pairs in the uploaded plan
+  int64_t* d_chunk_begin_ = nullptr;       // chunk_pair_begin_ in the uploaded plan
   bool prefetch_step_ = false;  // staged mode, one chunk per layer: prefetch the next layer
   int prefetched_layer_ = -1;   // layer whose copies are already queued in its buffer
-  int step_stage_base_ = 0;  // staging buffer of the open step's first chunk
   // Device views into the workspace for the current step.
   SeqInfo* d_seqs_ = nullptr;
   WorkItem* d_work_ = nullptr;

@@ -111,10 +111,12 @@ class PagedModel:
         (tokens per row the native store is sized for; default: the first session's prompt
         plus max_new_tokens) and ``stream_mode`` ("direct" or "staged"). The group size has
         no effect: the native kernel covers every block in one launch.
-        ``use_hip_graphs=True`` replays decode steps from a captured HIP graph (direct
-        stream mode only): the first decode step runs eagerly, a step whose launch signature
-        differs from the captured one (a new block changes the grids about once per block)
-        is captured and replayed, later steps with the same signature are replayed.
+        ``use_hip_graphs=True`` replays decode steps from a captured HIP graph: the first
+        decode step runs eagerly, a step whose launch signature differs from the captured one
+        (a new block changes the grids about once per block) is captured and replayed, later
+        steps with the same signature are replayed. In the staged stream mode the graph holds
+        the staging copies on the store's copy stream too, each layer's under the layer
+        before it.
         ``use_streaming_attention=False`` selects the reference's reload mode, which copies
         every block back into one HBM cache per step and runs the model's own attention
         (paged_model.py:717-760). For the supported model types it computes the same
@@ -123,8 +125,6 @@ class PagedModel:
             logger.info("use_streaming_attention=False: running the native paged path (same attention, no reload)")
         if tokens_per_block <= 0 or tokens_per_block % 16:
             raise ValueError("tokens_per_block must be a positive multiple of 16 for the native kernels")
-        if use_hip_graphs and stream_mode != "direct":
-            raise ValueError("use_hip_graphs needs stream_mode='direct' (staged copies run on a second stream)")
         self.use_hip_graphs = use_hip_graphs
         self._graphs: OrderedDict = OrderedDict()  # launch signature -> (graph, (ids, pos, logits))
         self._graph_pool = None

@@ -68,7 +68,10 @@ class Pair:
         self.dec.set_lo(sid, lo)
         self.ora.set_lo(sid, lo)
 
-    def step(self, gen, *, compute=True, scale=0.5, sids=None, order=None, end_stream=None):
+    def step(self, gen, *, compute=True, scale=0.5, sids=None, order=None, end_stream=None, graphs=None):
+        """One decode step of `sids` (every session by default), checked against the oracle.
+        With `graphs` (a dict) the layers run from a captured HIP graph, one per launch
+        signature: captured when the signature is new, replayed otherwise."""
         sids = self.sids if sids is None else sids
         order = list(range(self.layers)) if order is None else order
         S = sum(self.dec.sessions[s].rows for s in sids)
@@ -78,9 +81,29 @@ class Pair:
             ks.append((torch.randn(S, self.hkv, self.d, generator=gen) * scale).to(self.dtype))
             vs.append((torch.randn(S, self.hkv, self.d, generator=gen) * scale).to(self.dtype))
         self.dec.begin_step(sids)
-        outs = [None] * self.layers
-        for l in order:
-            outs[l] = self.dec.decode_layer(l, qs[l].cuda(), ks[l].cuda(), vs[l].cuda())
+        if graphs is None:
+            outs = [None] * self.layers
+            for l in order:
+                outs[l] = self.dec.decode_layer(l, qs[l].cuda(), ks[l].cuda(), vs[l].cuda())
+        else:
+            mass = self.dec._mass
+            sig = (self.dec.pool.step_signature(), None if mass is None else mass.data_ptr(), S)
+            entry = graphs.get(sig)
+            if entry is None:
+                ins = [[x.cuda() for x in xs] for xs in (qs, ks, vs)]
+                outs = [None] * self.layers
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph):
+                    for l in order:
+                        outs[l] = self.dec.decode_layer(l, ins[0][l], ins[1][l], ins[2][l])
+                entry = graphs[sig] = (graph, ins, outs)
+            else:
+                for dst, src in zip(entry[1], (qs, ks, vs)):
+                    for d_, s_ in zip(dst, src):
+                        d_.copy_(s_)
+            entry[0].replay()
+            self.dec.pool.step_replayed()
+            outs = entry[2]
         gather = [self.dec.step_host_blocks(i) for i in range(S)]
         if end_stream is None:
             res = self.dec.end_step()
@@ -168,6 +191,38 @@ def test_config4_mistral_layer_window_bf16(mode, staging_blocks):
             st = p.dec.pool.step_stats()
             assert st["host_blocks"] == 4 * 96  # in-window host blocks only
     assert p.ora.host_ids(p.sids[0], 0)[0] == (ctx + 3 - window) // 32
+
+
+@pytest.mark.parametrize("mode,staging_blocks,staging_buffers,policy", [
+    ("staged", 2048, 2, "recent_only"), ("staged", 2048, 3, "sinks_heavy_hitter"), ("staged", 40, 2, "recent_only"),
+    ("staged", 40, 3, "heavy_hitter"), ("direct", 2048, 2, "sinks_heavy_hitter")])
+def test_steps_replayed_from_captured_graphs(mode, staging_blocks, staging_buffers, policy):
+    """Four layers per step captured into HIP graphs (one per launch signature; new blocks
+    change it) and replayed, with eager steps in between. In the staged mode the graph holds
+    the staging copies on the store's copy stream: each layer's copies under the layer before
+    it when one buffer holds a layer's host blocks, chunk by chunk otherwise. Outputs, gather
+    lists, block mass and placement match the oracle at every step."""
+    g = torch.Generator().manual_seed(12)
+    ctx = [1200, 2500, 700]
+    p = Pair(layers=4, hq=8, hkv=2, d=64, tpb=32, dtype=torch.float16, pool_blocks=3 * 16,
+             host_blocks=sum(c // 32 + 8 for c in ctx), staging_blocks=staging_blocks,
+             staging_buffers=staging_buffers, stream_mode=mode)
+    for c in ctx:
+        p.add(ctx=c, capacity=c + 96, gen=g, vram_budget=10 * MIB16, ram_budget=1024 * MIB16, recent_window=7,
+              policy=policy)
+    graphs, errs = {}, []
+    scored = policy != "recent_only"  # the oracle computes every step to score the blocks
+    for step in range(72):
+        eager = step % 24 == 23  # an eager step now and then: the graphs must stay valid around it
+        _, _, err = p.step(g, compute=scored or step % 6 == 0 or step >= 69, graphs=None if eager else graphs)
+        if err is not None:
+            errs.append(err)
+        st = p.dec.pool.step_stats()
+        assert st["host_blocks"] > 100
+        if mode == "staged":
+            assert (st["chunks"] == 1) if staging_blocks >= 2048 else (st["chunks"] > 1)
+    assert len(errs) == (72 if scored else 15) and len(graphs) >= 2
+    print(f"{mode}/{staging_blocks}/{staging_buffers}/{policy}: {len(graphs)} graphs, max err {max(errs):.3g}")
 
 
 @pytest.mark.parametrize("staging_blocks,staging_buffers,order", [

@@ -327,10 +327,12 @@ def test_reload_mode_flag_gives_the_same_tokens():
     assert a == b
 
 
+@pytest.mark.parametrize("stream_mode", ["direct", "staged"])
 @pytest.mark.parametrize("policy", ["sinks_heavy_hitter", "recent_only"])
-def test_hip_graph_steps_match_eager_steps(policy):
+def test_hip_graph_steps_match_eager_steps(policy, stream_mode):
     """Decode steps replayed from captured HIP graphs give the eager steps' logits and tokens,
-    across block boundaries (each new block changes the launch signature: re-capture)."""
+    across block boundaries (each new block changes the launch signature: re-capture). In the
+    staged mode the graphs hold the staging copies too."""
     from pager_hf import PagedModel
 
     model = _model(SMALL, seed=17, init_std=0.05)
@@ -338,7 +340,8 @@ def test_hip_graph_steps_match_eager_steps(policy):
     ids = torch.randint(0, SMALL["vocab_size"], (2, 300), generator=g).cuda()
     mask = torch.ones_like(ids)
     mask[1, :40] = 0
-    kw = dict(vram_budget=4 * MIB16, ram_budget=1 << 40, recent_window=2, policy=policy, tokens_per_block=16)
+    kw = dict(vram_budget=4 * MIB16, ram_budget=1 << 40, recent_window=2, policy=policy, tokens_per_block=16,
+              stream_mode=stream_mode)
     eager = PagedModel(model, **kw)
     graph = PagedModel(model, use_hip_graphs=True, **kw)
     with torch.inference_mode():
@@ -363,7 +366,8 @@ def test_hip_graph_steps_match_eager_steps(policy):
     assert g2.generate(ids, mask, 40) == e2.generate(ids, mask, 40)
 
 
-def test_hip_graphs_continue_a_session_with_fed_tokens():
+@pytest.mark.parametrize("stream_mode", ["direct", "staged"])
+def test_hip_graphs_continue_a_session_with_fed_tokens(stream_mode):
     """A second generate() call with HIP graphs first feeds the tokens the caller appended
     since the first call: those steps run back to back with no host read between them, so
     the host writes the next step's plan while earlier replays are still queued. Each replay
@@ -375,7 +379,7 @@ def test_hip_graphs_continue_a_session_with_fed_tokens():
     ids = torch.randint(0, SMALL["vocab_size"], (1, 300), generator=g).cuda()
     extra = torch.randint(0, SMALL["vocab_size"], (1, 45), generator=g).cuda()
     kw = dict(vram_budget=4 * MIB16, ram_budget=1 << 40, recent_window=2, policy="recent_only", tokens_per_block=16,
-              max_context_tokens=640)
+              max_context_tokens=640, stream_mode=stream_mode)
     runs = []
     for graphs in (False, True):
         pm = PagedModel(model, use_hip_graphs=graphs, **kw)
