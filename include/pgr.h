@@ -35,7 +35,7 @@ extern "C" {
 
 /* ---- library ------------------------------------------------------------------------- */
 
-/* ABI version of this header (increments when an entry point is added or changed); 6. */
+/* ABI version of this header (increments when an entry point is added or changed); 7. */
 int pgr_abi_version(void);
 /* Message of the last failing call on this thread ("" if none). */
 const char* pgr_last_error(void);
@@ -148,7 +148,7 @@ typedef struct pgr_kv_config_s {
   int32_t num_layers;
   int32_t kv_heads;
   int32_t query_heads;
-  int32_t head_dim;
+  int32_t head_dim;         /* 16, 32, 64, 128 or 256 */
   int32_t tokens_per_block; /* multiple of 16 */
   int32_t dtype;
   int64_t pool_slots;       /* HBM records (block x row) per layer */
@@ -239,10 +239,14 @@ int pgr_kv_begin_step(void* kv, const int32_t* sids, int32_t n, void* stream);
  * folds every in-scope block (HBM in place, host blocks streamed), writes out [S, Hq, D]
  * and, if mass_accum != NULL, adds the per-block attention mass (mean over the session's
  * rows and query heads) into mass_accum[session_in_step * accum_stride + block].
+ * window > 0: this layer's own sliding window (alternating-window models); it also masks
+ * the stored positions c <= p - window, p being the current token's position (the rule
+ * col > pos - W of paged_model.py:977-982). Blocks are still read; window <= 0: none.
  * Replaces the patched layer forward's gather + fold loop, paged_model.py:926-1086
  * (gather :878-924, tail append :955, mass :1041-1048). */
 int pgr_kv_decode_layer(void* kv, int32_t layer, const void* q, const void* k_new, const void* v_new, void* out,
-                        float* mass_accum, int64_t accum_stride, float scale, float softcap, void* stream);
+                        float* mass_accum, int64_t accum_stride, float scale, float softcap, int32_t window,
+                        void* stream);
 /* Closes the step: every session grows by one token; sessions whose open block became full
  * are written to completed[] (the new block id is then length / T - 1).
  * Replaces _append_new_full_blocks_from_grown_tail, paged_model.py:1210-1233. */

@@ -11,7 +11,9 @@ Restates, per decode step and session (one session = rows sharing one placement)
     tokens_per_block it becomes block ``num_blocks`` (paged_model.py:1210-1233);
   * attention: dense fp32 softmax over every valid token of the row including the new one
     (tests/test_streaming_attention.py:20-40 form; validity = position >= lo, which folds the
-    left-padding mask and the sliding-window rule col > pos - W of paged_model.py:977-982);
+    left-padding mask and the sliding-window rule col > pos - W of paged_model.py:977-982;
+    a layer with its own window W, as Gemma2's alternating layers have
+    (paged_model.py:153-177), also requires position > pos - W);
   * mass: block mass of the full blocks known before the step, mean over (rows, query
     heads), summed over layers (paged_model.py:1041-1048), then averaged and normalized
     (paged_model.py:865-876); uniform when the policy ignores scores (:788-790);
@@ -132,9 +134,10 @@ class PagedDecodeOracle:
         buf_v[:, n] = np.asarray(v1, np.float32)
         return buf_k[:, : n + 1], buf_v[:, : n + 1]
 
-    def step(self, sids, q, k_new, v_new, compute=True):
+    def step(self, sids, q, k_new, v_new, compute=True, windows=None):
         """q[layer] [S, Hq, D]; k_new/v_new[layer] [S, Hkv, D] (float32 arrays of the stored values);
-        with compute=False they may be None (placement and gather lists only).
+        with compute=False they may be None (placement and gather lists only). windows[layer]:
+        that layer's own sliding window, or None (default: none for every layer).
 
         Returns a dict with per-layer outputs, per-sequence gather ids, per-session block
         scores handed to the pager and the moves of apply_tiers. With compute=False the
@@ -159,7 +162,11 @@ class PagedDecodeOracle:
                 # Tokens before the first block holding a valid position carry zero weight:
                 # compute over [start, total) and place the block masses at their ids.
                 start = (max(s.lo[r], 0) // self.T) * self.T
-                valid = (np.arange(start, total) >= s.lo[r]).astype(np.int32)[None]
+                lo = s.lo[r]
+                window = windows[layer] if windows is not None else None
+                if window:  # col > pos - W with pos = total - 1
+                    lo = max(lo, total - window)
+                valid = (np.arange(start, total) >= lo).astype(np.int32)[None]
                 o, mass = dense_reference(
                     np.asarray(q[layer][i], np.float32)[None], k[None, :, start:], v[None, :, start:],
                     n_rep=self.n_rep, tokens_per_block=self.T, valid=valid, scale=self.scale, softcap=self.softcap,

@@ -34,7 +34,7 @@ MODE_FOLD_FIXED = 3
 STREAM_DIRECT = 0
 STREAM_STAGED = 1
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 c_i32, c_i64, c_u8, c_u32, c_u64 = ctypes.c_int32, ctypes.c_int64, ctypes.c_uint8, ctypes.c_uint32, ctypes.c_uint64
 c_f32, c_f64, c_size, c_vp = ctypes.c_float, ctypes.c_double, ctypes.c_size_t, ctypes.c_void_p
@@ -158,7 +158,7 @@ SIGNATURES: dict[str, tuple] = {
     "pgr_kv_begin_step": (ctypes.c_int, [c_vp, P(c_i32), c_i32, c_vp]),
     "pgr_kv_decode_layer": (
         ctypes.c_int,
-        [c_vp, c_i32, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_f32, c_f32, c_vp],
+        [c_vp, c_i32, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_f32, c_f32, c_i32, c_vp],
     ),
     "pgr_kv_end_step": (ctypes.c_int, [c_vp, P(c_i32), P(c_i32)]),
     "pgr_kv_attach_pager": (ctypes.c_int, [c_vp, c_i32, c_vp, c_i32]),

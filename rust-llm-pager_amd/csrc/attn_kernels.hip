@@ -688,6 +688,7 @@ struct PagedArgs {
   float* lf;
   int hq, hkv, n_rep, tokens_per_block, mass_stride;
   float scale, softcap;
+  int window;             // > 0: the layer's sliding window (see PagedLaunch)
   uint32_t* plan_flag;    // merge: pinned word for plan_token (see PagedLaunch), or null
   uint32_t plan_token;
 };
@@ -701,12 +702,59 @@ constexpr float kMInit = -1.0e30f;  // running max before any valid score (finit
 // lane: K row n, dims (D/4)g .. (D/4)g + D/4 - 1 (the chunks of the S^T products), and V in
 // the record's transposed layout (v_record_index, pgr_kernels.h): tokens 4g..4g+3 of dims
 // (D/16)n .. (D/16)n + D/16 - 1, four tokens per dim, which are the A operands of the D/16
-// O^T products as they stand (M-tile j = dwords 2j, 2j + 1).
+// O^T products as they stand (M-tile j = dwords 2j, 2j + 1). A lane's run is D/32 16-byte
+// vectors, or one 8-byte vector at head dim 16.
+template <int D>
+struct LaneRun {
+  using T = u32x4;
+  static constexpr int N = D / 32;
+};
+template <>
+struct LaneRun<16> {
+  using T = u32x2;
+  static constexpr int N = 1;
+};
+template <int D>
+using RunVec = typename LaneRun<D>::T;
+
 template <int D>
 struct PTile {
-  u32x4 k[D / 32];
-  u32x4 v[D / 32];
+  RunVec<D> k[LaneRun<D>::N];
+  RunVec<D> v[LaneRun<D>::N];
 };
+
+// Dwords 2c, 2c + 1 of a lane's run: the MFMA operand of contraction chunk c (K, q) or of
+// M-tile c (V).
+template <int D>
+__device__ __forceinline__ u32x2 run_chunk(const RunVec<D> (&r)[LaneRun<D>::N], int c) {
+  if constexpr (D == 16) {
+    return r[0];
+  } else {
+    const u32x4 q = r[c >> 1];
+    return (c & 1) ? u32x2{q.z, q.w} : u32x2{q.x, q.y};
+  }
+}
+
+// S^T tile of 16 tokens x 16 heads from the lane's K and q runs.
+template <class Ty, int D>
+__device__ __forceinline__ f32x4 qk_run(const RunVec<D> (&k)[LaneRun<D>::N], const RunVec<D> (&q)[LaneRun<D>::N]) {
+  f32x4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int c = 0; c < D / 16; ++c) s = Ty::mma(run_chunk<D>(k, c), run_chunk<D>(q, c), s);
+  return s;
+}
+
+// Query head row at `qptr`, the lane's run of it (dims (D/4)g .. +D/4); zero for padding heads.
+template <int D>
+__device__ __forceinline__ void load_q_run(RunVec<D> (&q)[LaneRun<D>::N], const uint16_t* qptr, bool real, int g) {
+#pragma unroll
+  for (int i = 0; i < LaneRun<D>::N; ++i) q[i] = RunVec<D>{};
+  if (real) {
+    const RunVec<D>* p = reinterpret_cast<const RunVec<D>*>(qptr + (D / 4) * g);
+#pragma unroll
+    for (int i = 0; i < LaneRun<D>::N; ++i) q[i] = p[i];
+  }
+}
 
 constexpr int kBufferFlags = 0x00020000;  // dword 3 of a raw buffer resource on gfx9
 
@@ -718,10 +766,15 @@ constexpr int kBufferFlags = 0x00020000;  // dword 3 of a raw buffer resource on
 template <int D>
 __device__ __forceinline__ void load_tile_rs(PTile<D>& t, __amdgpu_buffer_rsrc_t r, uint32_t sk, uint32_t sv,
                                              uint32_t k_lane, uint32_t v_lane) {
+  if constexpr (D == 16) {
+    t.k[0] = __builtin_amdgcn_raw_buffer_load_b64(r, k_lane, sk, 0);
+    t.v[0] = __builtin_amdgcn_raw_buffer_load_b64(r, v_lane, sv, 0);
+  } else {
 #pragma unroll
-  for (int i = 0; i < D / 32; ++i) t.k[i] = __builtin_amdgcn_raw_buffer_load_b128(r, k_lane + 16u * i, sk, 0);
+    for (int i = 0; i < D / 32; ++i) t.k[i] = __builtin_amdgcn_raw_buffer_load_b128(r, k_lane + 16u * i, sk, 0);
 #pragma unroll
-  for (int i = 0; i < D / 32; ++i) t.v[i] = __builtin_amdgcn_raw_buffer_load_b128(r, v_lane + 16u * i, sv, 0);
+    for (int i = 0; i < D / 32; ++i) t.v[i] = __builtin_amdgcn_raw_buffer_load_b128(r, v_lane + 16u * i, sv, 0);
+  }
 }
 
 // O^T[D x 16 heads] += V^T . P^T with the transposed V tile.
@@ -729,7 +782,7 @@ template <class Ty, int D>
 __device__ __forceinline__ void pv_tile_t(f32x4 (&acc)[D / 16], const PTile<D>& t, const float (&p)[4]) {
   const u32x2 pb = {Ty::pack(p[0], p[1]), Ty::pack(p[2], p[3])};
 #pragma unroll
-  for (int j = 0; j < D / 16; ++j) acc[j] = Ty::mma(k_chunk<D>(t.v, j), pb, acc[j]);
+  for (int j = 0; j < D / 16; ++j) acc[j] = Ty::mma(run_chunk<D>(t.v, j), pb, acc[j]);
 }
 
 struct TileMeta {
@@ -740,7 +793,9 @@ struct TileMeta {
 
 template <int D>
 struct PagedRing {
-  static constexpr int NB = 3;  // register tiles per wave
+  // Register tiles per wave. At head dim 256 a tile is 64 VGPRs of K and V per lane (next to
+  // 64 of accumulators and 32 of q), so two.
+  static constexpr int NB = D == 256 ? 2 : 3;
 };
 
 // The three pointers the first loads depend on come as separate leading arguments: the build
@@ -765,7 +820,10 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(const WorkItem* __restr
   const size_t rec = (size_t)2 * a.hkv * T * D;  // elements per record
   const size_t head_off = (size_t)h * T * D;
   const size_t v_off = (size_t)a.hkv * T * D;
-  const int seq = wi->seq, lo = wi->lo, hi = wi->hi, n_mass = wi->n_mass;
+  const int seq = wi->seq, hi = wi->hi, n_mass = wi->n_mass;
+  // A layer with its own sliding window masks the stored positions <= hi - window as well
+  // (hi is the current token's position); its blocks are read all the same.
+  const int lo = a.window > 0 ? max(wi->lo, hi - a.window + 1) : wi->lo;
   const int count = wi->entry_count, partial = wi->partial;
   const int append_slot = wi->append_slot, append_pos = wi->append_pos;
   const uint32_t k_lane = (uint32_t)(n * D + (D / 4) * g) * 2u;
@@ -792,7 +850,7 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(const WorkItem* __restr
   // slots exist in every work item).
   BlockEntry ecur = wi->entries[wave], enxt = wi->entries[wave + kWaves];
 
-  u32x4 q[D / 32];  // loaded behind the first tile (below)
+  RunVec<D> q[LaneRun<D>::N];  // loaded behind the first tile (below)
 
   // Score transform: x = mult * s' with s' = s (no softcap) or cap * tanh(s * scale / cap).
   const bool capped = a.softcap > 0.f;
@@ -831,7 +889,7 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(const WorkItem* __restr
   };
 
   auto fold = [&](PTile<D>& t, const TileMeta& mt) {
-    f32x4 s4 = qk_tile<Ty, D>(t.k, q);
+    f32x4 s4 = qk_run<Ty, D>(t.k, q);
     if (capped) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) s4[i] = a.softcap * tanhf(s4[i] * cap_in);
@@ -852,8 +910,12 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(const WorkItem* __restr
             my &= keep;
         }
       }
+      if constexpr (D == 16) {
+        t.v[0] &= u32x2{mx, my};
+      } else {
 #pragma unroll
-      for (int w = 0; w < D / 32; ++w) t.v[w] &= u32x4{mx, my, mx, my};
+        for (int w = 0; w < D / 32; ++w) t.v[w] &= u32x4{mx, my, mx, my};
+      }
     }
     const float lmax = fmaxf(fmaxf(s4[0], s4[1]), fmaxf(s4[2], s4[3])) * mult;
     if (__builtin_amdgcn_ballot_w64(lmax > m_thr) != 0) {
@@ -892,11 +954,11 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(const WorkItem* __restr
     // waiting for it here (which also waits for tile 0, as loads return in order) keeps
     // the loop's wait counts independent of it while tiles 1 .. NB-2 stay in flight.
     fetch(buf[0], meta[0]);
-    load_q<D>(q, a.q + ((size_t)seq * a.hq + qh) * D, real, g);
+    load_q_run<D>(q, a.q + ((size_t)seq * a.hq + qh) * D, real, g);
 #pragma unroll
     for (int j = 1; j < NB - 1; ++j) fetch(buf[j], meta[j]);
 #pragma unroll
-    for (int i = 0; i < D / 32; ++i) asm volatile("" ::"v"(q[i]));
+    for (int i = 0; i < LaneRun<D>::N; ++i) asm volatile("" ::"v"(q[i]));
     for (int ti = 0; ti < tiles; ti += NB) {
 #pragma unroll
       for (int j = 0; j < NB; ++j) {
@@ -948,8 +1010,10 @@ __global__ __launch_bounds__(256) void paged_merge_kernel(const SeqInfo* __restr
   constexpr int kLanes = D / 2;          // threads per partial group (two dims each)
   constexpr int G = 256 / kLanes;        // partial groups
   constexpr int kU = kMergeBatch;
+  constexpr int kRed = kLanes < kWaveSize ? kLanes : kWaveSize;  // lanes of group 0 per wave
   __shared__ float m_s[G], l_s[G];
   __shared__ float acc_s[G][D];
+  __shared__ float dot_s[kLanes / kRed];
   const int seq = blockIdx.x, qh = blockIdx.y;
   const int tid = threadIdx.x;
   const int c = tid % kLanes, grp = tid / kLanes;
@@ -1007,6 +1071,15 @@ __global__ __launch_bounds__(256) void paged_merge_kernel(const SeqInfo* __restr
     }
     m = m_new;
   }
+  // q . k_new: group 0's two-dim products, summed over its lanes in each wave (every lane
+  // takes part in the shuffles; group 0 is aligned to kRed lanes), then over its waves.
+  float dot = 0.f;
+  if (grp == 0)
+    dot = Ty::to_f((uint16_t)(qd & 0xffffu)) * Ty::to_f((uint16_t)(kd & 0xffffu)) +
+          Ty::to_f((uint16_t)(qd >> 16)) * Ty::to_f((uint16_t)(kd >> 16));
+#pragma unroll
+  for (int o = kRed / 2; o > 0; o >>= 1) dot += __shfl_xor(dot, o);
+  if (grp == 0 && c % kRed == 0) dot_s[c / kRed] = dot;
   if (c == 0) {
     m_s[grp] = m;
     l_s[grp] = l;
@@ -1016,10 +1089,9 @@ __global__ __launch_bounds__(256) void paged_merge_kernel(const SeqInfo* __restr
   __syncthreads();
   if (grp != 0) return;
 
-  float dot = Ty::to_f((uint16_t)(qd & 0xffffu)) * Ty::to_f((uint16_t)(kd & 0xffffu)) +
-              Ty::to_f((uint16_t)(qd >> 16)) * Ty::to_f((uint16_t)(kd >> 16));
+  dot = dot_s[0];
 #pragma unroll
-  for (int o = kLanes / 2; o > 0; o >>= 1) dot += __shfl_xor(dot, o);
+  for (int w = 1; w < kLanes / kRed; ++w) dot += dot_s[w];
   float x_cur;
   if (a.softcap > 0.f)
     x_cur = a.softcap * tanhf(dot * (a.scale / a.softcap)) * kLog2e;
@@ -1203,9 +1275,47 @@ hipError_t launch_paged_t(const PagedArgs& a, int n_work, bool mass, hipStream_t
   return hipGetLastError();
 }
 
+template <class Ty>
+hipError_t launch_paged_d(const PagedArgs& a, int d, int n_work, bool mass, hipStream_t stream) {
+  switch (d) {
+    case 16:
+      return launch_paged_t<Ty, 16>(a, n_work, mass, stream);
+    case 32:
+      return launch_paged_t<Ty, 32>(a, n_work, mass, stream);
+    case 64:
+      return launch_paged_t<Ty, 64>(a, n_work, mass, stream);
+    case 128:
+      return launch_paged_t<Ty, 128>(a, n_work, mass, stream);
+    default:
+      return launch_paged_t<Ty, 256>(a, n_work, mass, stream);
+  }
+}
+
+template <class Ty>
+void launch_merge_d(const PagedArgs& a, int d, dim3 grid, hipStream_t stream) {
+  switch (d) {
+    case 16:
+      paged_merge_kernel<Ty, 16><<<grid, 256, 0, stream>>>(a.seqs, a);
+      break;
+    case 32:
+      paged_merge_kernel<Ty, 32><<<grid, 256, 0, stream>>>(a.seqs, a);
+      break;
+    case 64:
+      paged_merge_kernel<Ty, 64><<<grid, 256, 0, stream>>>(a.seqs, a);
+      break;
+    case 128:
+      paged_merge_kernel<Ty, 128><<<grid, 256, 0, stream>>>(a.seqs, a);
+      break;
+    default:
+      paged_merge_kernel<Ty, 256><<<grid, 256, 0, stream>>>(a.seqs, a);
+  }
+}
+
 }  // namespace
 
 bool head_dim_supported(int d) { return d == 32 || d == 64 || d == 128; }
+
+bool paged_head_dim_supported(int d) { return d == 16 || head_dim_supported(d) || d == 256; }
 
 bool dense_head_dim_supported(int d) { return d == 8 || d == 16 || head_dim_supported(d) || d == 256; }
 
@@ -1313,25 +1423,10 @@ hipError_t launch_paged(int dtype, int d, const PagedLaunch& p, hipStream_t stre
   a.mass_stride = p.mass_stride;
   a.scale = p.scale;
   a.softcap = p.softcap;
+  a.window = p.window;
   const bool mass = p.mass_m != nullptr;
-  if (dtype == kF16) {
-    switch (d) {
-      case 32:
-        return launch_paged_t<F16, 32>(a, p.n_work, mass, stream);
-      case 64:
-        return launch_paged_t<F16, 64>(a, p.n_work, mass, stream);
-      default:
-        return launch_paged_t<F16, 128>(a, p.n_work, mass, stream);
-    }
-  }
-  switch (d) {
-    case 32:
-      return launch_paged_t<BF16, 32>(a, p.n_work, mass, stream);
-    case 64:
-      return launch_paged_t<BF16, 64>(a, p.n_work, mass, stream);
-    default:
-      return launch_paged_t<BF16, 128>(a, p.n_work, mass, stream);
-  }
+  return dtype == kF16 ? launch_paged_d<F16>(a, d, p.n_work, mass, stream)
+                       : launch_paged_d<BF16>(a, d, p.n_work, mass, stream);
 }
 
 hipError_t launch_paged_merge(int dtype, int d, const PagedLaunch& p, int n_seq, hipStream_t stream) {
@@ -1355,17 +1450,10 @@ hipError_t launch_paged_merge(int dtype, int d, const PagedLaunch& p, int n_seq,
   a.plan_flag = p.plan_flag;
   a.plan_token = p.plan_token;
   dim3 grid(n_seq, p.hq);
-#define PGR_MERGE(TY, DD) paged_merge_kernel<TY, DD><<<grid, 256, 0, stream>>>(a.seqs, a)
-  if (dtype == kF16) {
-    if (d == 32) PGR_MERGE(F16, 32);
-    else if (d == 64) PGR_MERGE(F16, 64);
-    else PGR_MERGE(F16, 128);
-  } else {
-    if (d == 32) PGR_MERGE(BF16, 32);
-    else if (d == 64) PGR_MERGE(BF16, 64);
-    else PGR_MERGE(BF16, 128);
-  }
-#undef PGR_MERGE
+  if (dtype == kF16)
+    launch_merge_d<F16>(a, d, grid, stream);
+  else
+    launch_merge_d<BF16>(a, d, grid, stream);
   return hipGetLastError();
 }
 

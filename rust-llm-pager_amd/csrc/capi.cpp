@@ -158,7 +158,7 @@ int kv_rc(pgr::PagedKV* kv, int rc) {
 
 extern "C" {
 
-int pgr_abi_version(void) { return 6; }
+int pgr_abi_version(void) { return 7; }
 
 const char* pgr_last_error(void) { return g_last_error.c_str(); }
 
@@ -409,11 +409,13 @@ int pgr_kv_begin_step(void* kv, const int32_t* sids, int32_t n, void* stream) {
 }
 
 int pgr_kv_decode_layer(void* kv, int32_t layer, const void* q, const void* k_new, const void* v_new, void* out,
-                        float* mass_accum, int64_t accum_stride, float scale, float softcap, void* stream) {
+                        float* mass_accum, int64_t accum_stride, float scale, float softcap, int32_t window,
+                        void* stream) {
   if (!kv || !q || !k_new || !v_new || !out) return set_err(pgr::kErrInvalid, "null pointer");
   if (!(scale > 0.f) || !std::isfinite(scale)) return set_err(pgr::kErrInvalid, "scale must be positive and finite");
   return kv_rc(kv_of(kv), kv_of(kv)->decode_layer(layer, q, k_new, v_new, out, mass_accum, accum_stride, scale,
-                                                  softcap > 0.f ? softcap : 0.f, as_stream(stream)));
+                                                  softcap > 0.f ? softcap : 0.f, window > 0 ? window : 0,
+                                                  as_stream(stream)));
 }
 
 int pgr_kv_step_signature(void* kv, int64_t* out, int64_t cap) {

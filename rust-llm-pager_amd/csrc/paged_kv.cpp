@@ -264,7 +264,8 @@ size_t PagedKV::rec_bytes() const {
 int PagedKV::init() {
   if (cfg_.num_layers <= 0 || cfg_.kv_heads <= 0 || cfg_.tokens_per_block <= 0 || cfg_.tokens_per_block % 16 != 0)
     return fail(kErrInvalid, "num_layers, kv_heads > 0 and tokens_per_block a positive multiple of 16 required");
-  if (!head_dim_supported(cfg_.head_dim)) return fail(kErrUnsupported, "head_dim must be 32, 64 or 128");
+  if (!paged_head_dim_supported(cfg_.head_dim))
+    return fail(kErrUnsupported, "head_dim must be 16, 32, 64, 128 or 256");
   if (cfg_.query_heads <= 0 || cfg_.query_heads % cfg_.kv_heads != 0)
     return fail(kErrInvalid, "query_heads must be a positive multiple of kv_heads");
   if (cfg_.query_heads / cfg_.kv_heads > kMaxRep) return fail(kErrUnsupported, "n_rep above 16 is not supported");
@@ -1184,7 +1185,8 @@ int PagedKV::begin_step(const int32_t* sids, int n, hipStream_t stream) {
 }
 
 int PagedKV::decode_layer(int layer, const void* q, const void* k_new, const void* v_new, void* out,
-                          float* mass_accum, int64_t accum_stride, float scale, float softcap, hipStream_t stream) {
+                          float* mass_accum, int64_t accum_stride, float scale, float softcap, int window,
+                          hipStream_t stream) {
   if (!in_step_) return fail(kErrState, "decode_layer outside begin_step/end_step");
   if (layer < 0 || layer >= cfg_.num_layers) return fail(kErrInvalid, "layer out of range");
   // Under stream capture nothing runs now: no cross-stream wait is recorded (the capture
@@ -1219,6 +1221,7 @@ int PagedKV::decode_layer(int layer, const void* q, const void* k_new, const voi
   pl.mass_stride = mass_stride_;
   pl.scale = scale;
   pl.softcap = softcap;
+  pl.window = window;
   const int n_launch = (int)launch_work_begin_.size();
   const int nbuf = cfg_.staging_buffers;
   // Side stream: wait until the previous reader of buffer `buf` finished, then stream the

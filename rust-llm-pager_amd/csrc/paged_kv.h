@@ -111,8 +111,9 @@ class PagedKV {
 
   // Decode step over `sids` (their rows, in order, are the sequences of q/out).
   int begin_step(const int32_t* sids, int n, hipStream_t stream);
+  // window > 0: this layer also masks stored positions <= current - window.
   int decode_layer(int layer, const void* q, const void* k_new, const void* v_new, void* out, float* mass_accum,
-                   int64_t accum_stride, float scale, float softcap, hipStream_t stream);
+                   int64_t accum_stride, float scale, float softcap, int window, hipStream_t stream);
   int end_step(int32_t* completed_sessions, int* n_completed);
   // Everything the open step's launches take as arguments besides the caller's tensors:
   // plan buffer and workspace pointers, grid sizes, the mass stride. Launches captured in a

@@ -73,6 +73,7 @@ struct PagedLaunch {
   float* lf;
   int n_work, hq, hkv, tokens_per_block, mass_stride;
   float scale, softcap;
+  int window = 0;  // > 0: the layer's own sliding window (positions <= current - window masked)
   // Merge launch only: when set, the merge stores plan_token to *plan_flag (pinned host memory)
   // as it starts, telling the host that the attention launches before it, and so their read of
   // the step's plan buffer, have finished.
@@ -80,8 +81,10 @@ struct PagedLaunch {
   uint32_t plan_token = 0;
 };
 
-// Head dims of the paged decode kernels (32, 64, 128).
+// Head dims of the MFMA dense kernel (32, 64, 128).
 bool head_dim_supported(int d);
+// Head dims of the paged decode kernels: 16, 32, 64, 128, 256.
+bool paged_head_dim_supported(int d);
 // Head dims of the dense operator kernels: 8, 16, 32, 64, 128, 256 (fp16, bf16 or fp32).
 bool dense_head_dim_supported(int d);
 // Dense launch geometry: the MFMA kernel (4 waves per workgroup, 16-token tiles) takes 16-bit

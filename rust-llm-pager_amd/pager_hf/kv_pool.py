@@ -213,13 +213,15 @@ class NativeKVPool:
         arr = (ctypes.c_int32 * max(len(sids), 1))(*sids)
         self._call("begin_step", self.lib.pgr_kv_begin_step, arr, len(sids), self._stream())
 
-    def decode_layer(self, layer: int, q, k_new, v_new, out, mass_accum=None, scale=None, softcap=None) -> None:
+    def decode_layer(self, layer: int, q, k_new, v_new, out, mass_accum=None, scale=None, softcap=None,
+                     window=None) -> None:
         if scale is None:
             scale = 1.0 / (self.head_dim**0.5)
         stride = mass_accum.shape[1] if mass_accum is not None else 0
         self._call(
             "decode_layer", self.lib.pgr_kv_decode_layer, layer, q.data_ptr(), k_new.data_ptr(), v_new.data_ptr(),
-            out.data_ptr(), N.ptr(mass_accum), stride, float(scale), float(softcap or 0.0), self._stream(),
+            out.data_ptr(), N.ptr(mass_accum), stride, float(scale), float(softcap or 0.0), int(window or 0),
+            self._stream(),
         )
 
     def attach_pager(self, sid: int, pager_handle: int, scores_from_mass: bool) -> None:

@@ -232,9 +232,12 @@ class PagedDecoder:
 
     def decode_layer(self, layer: int, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor,
                      out: torch.Tensor | None = None, *, scale: float | None = None,
-                     softcap: float | None = None) -> torch.Tensor:
+                     softcap: float | None = None, window: int | None = None) -> torch.Tensor:
         """Append k_new/v_new, attend q over every valid stored token plus the new one, and
-        accumulate this layer's block mass. scale/softcap override the decoder's defaults."""
+        accumulate this layer's block mass. scale/softcap override the decoder's defaults.
+        window: this layer's own sliding window (models whose layers alternate between
+        windowed and global attention): stored positions <= current - window are masked as
+        well, by the rule col > pos - W of paged_model.py:977-982."""
         if self._step is None:
             raise RuntimeError("decode_layer outside begin_step/end_step")
         S = self.num_sequences()
@@ -249,7 +252,7 @@ class PagedDecoder:
         if out is None:
             out = torch.empty(exp_q, dtype=self.dtype, device=self.device)
         self.pool.decode_layer(layer, q, k_new, v_new, out, self._mass, self.scale if scale is None else scale,
-                               self.softcap if softcap is None else softcap)
+                               self.softcap if softcap is None else softcap, window)
         return out
 
     def step_host_blocks(self, seq: int) -> list[int]:

@@ -19,11 +19,14 @@ one-call-at-a-time lock. What runs underneath is the native path:
 ``generate_beam_search`` (paged_model.py:409-634) moves beam rows inside the native store.
 
 Differences: ``use_streaming_attention=False`` (the reference's reload-everything mode)
-runs the same native path, since it computes the same attention; supported model types are the ones
-whose attention is the plain q/k/v + RoPE + o_proj layout in transformers 5.x (llama,
-mistral, qwen2, qwen2_moe, qwen3, starcoder2). Mistral's and Starcoder2's sliding window
-is applied per step through the sequences' first valid position. The Gemma family is not
-supported (head_dim 256, and Gemma2's per-layer windows).
+runs the same native path, since it computes the same attention. Supported model types: the
+reference's (paged_model.py:82-86: qwen2, qwen2_moe, starcoder2, llama, mistral, gemma, phi3,
+gemma2) and qwen3, all of which call transformers 5.x's attention interface with post-RoPE
+q/k/v. Head dims 16, 32, 64, 128 and 256. Mistral's and Starcoder2's sliding window is applied
+per step through the sequences' first valid position; a layer that passes its own window
+(Gemma2's alternating sliding layers) masks by it in the kernel, and its softcap and scale
+(Gemma2's attn_logit_softcapping and query_pre_attn_scalar) come with each call
+(paged_model.py:143-177).
 """
 from __future__ import annotations
 
@@ -43,14 +46,19 @@ logger = logging.getLogger(__name__)
 
 _ATTN_IMPL = "pgr_paged_decode"
 _POLICIES_WITHOUT_ATTENTION_SIGNAL = frozenset({"recent_only", "sinks_recent"})  # paged_model.py:40
-_SUPPORTED_MODEL_TYPES = frozenset({"llama", "mistral", "qwen2", "qwen2_moe", "qwen3", "starcoder2"})
-# Model types whose every layer attends within config.sliding_window (when set).
-_WINDOWED_MODEL_TYPES = frozenset({"mistral", "starcoder2"})
+_SUPPORTED_MODEL_TYPES = frozenset({"llama", "mistral", "qwen2", "qwen2_moe", "qwen3", "starcoder2", "gemma", "gemma2",
+                                    "phi3"})
+# Model types whose every layer attends within config.sliding_window (when set): the blocks
+# below the window are left out of the step altogether. Layers that pass their own window
+# with each call (Gemma2's alternating layers) mask by it in the kernel.
+_WINDOWED_MODEL_TYPES = frozenset({"mistral", "starcoder2", "phi3"})
 
 
 def _paged_attention(module, query, key, value, attention_mask, scaling=None, dropout=0.0, **kwargs):
     """Attention interface of a decode step: query [B, Hq, 1, D], key/value [B, Hkv, 1, D]
-    (post-RoPE, the current token only). Returns ([B, 1, Hq, D], None)."""
+    (post-RoPE, the current token only). The layer's scale, softcap (Gemma2) and sliding
+    window (None for global layers) come as arguments of the call. Returns ([B, 1, Hq, D],
+    None)."""
     ctx = getattr(module, "_pgr_ctx", None)
     if ctx is None:
         raise RuntimeError(f"attention implementation {_ATTN_IMPL!r} is only usable inside PagedModel.generate()")
@@ -59,7 +67,10 @@ def _paged_attention(module, query, key, value, attention_mask, scaling=None, dr
     q = query[:, :, 0, :]
     k = key[:, :, 0, :]
     v = value[:, :, 0, :]
-    out = ctx.decoder.decode_layer(module.layer_idx, q, k, v, scale=scaling, softcap=ctx.softcap)
+    softcap = kwargs.get("softcap")
+    out = ctx.decoder.decode_layer(module.layer_idx, q, k, v, scale=scaling,
+                                   softcap=ctx.softcap if softcap is None else softcap,
+                                   window=kwargs.get("sliding_window"))
     return out.unsqueeze(1), None
 
 

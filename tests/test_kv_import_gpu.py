@@ -31,7 +31,8 @@ def _check(dec, sid, ks, vs, n, row_src):
 
 
 @pytest.mark.parametrize("d,dtype,place", [(64, torch.float16, True), (128, torch.bfloat16, True),
-                                           (64, torch.float16, False)])
+                                           (64, torch.float16, False), (16, torch.bfloat16, True),
+                                           (256, torch.float16, True)])
 def test_import_moves_and_reorder_read_back_exactly(d, dtype, place):
     layers, hkv, T, rows, n = 3, 2, 32, 3, 2000
     g = torch.Generator(device="cuda").manual_seed(d)

@@ -143,6 +143,47 @@ def test_window_lo_skips_blocks_below_it():
     np.testing.assert_allclose(scores, mass / mass.sum(), rtol=0, atol=1e-6)
 
 
+def test_per_layer_window_against_brute_force():
+    """A layer with its own sliding window (Gemma2's alternating layers) attends to the
+    positions c > pos - W only (paged_model.py:977-982), on top of the row's first valid
+    position; the other layer attends to everything. Outputs and scores against float64
+    brute force, the valid set of each (row, layer) enumerated position by position."""
+    rng = np.random.default_rng(13)
+    L, hq, hkv, d, T, n0, W = 2, 4, 2, 8, 16, 70, 24
+    n_rep = hq // hkv
+    lo = [0, 5]
+    o = PagedDecodeOracle(num_layers=L, num_query_heads=hq, num_kv_heads=hkv, head_dim=d, tokens_per_block=T)
+    o.add_session(1, rows=2, vram_budget=1 * MIB16, ram_budget=1 << 40, recent_window=1, policy="sinks_heavy_hitter",
+                  lo=lo)
+    keys = [rng.standard_normal((2, hkv, n0, d)).astype(np.float32) for _ in range(L)]
+    vals = [rng.standard_normal((2, hkv, n0, d)).astype(np.float32) for _ in range(L)]
+    o.prefill(1, keys, vals, n0)
+    q = [rng.standard_normal((2, hq, d)).astype(np.float32) for _ in range(L)]
+    kn = [rng.standard_normal((2, hkv, d)).astype(np.float32) for _ in range(L)]
+    vn = [rng.standard_normal((2, hkv, d)).astype(np.float32) for _ in range(L)]
+    windows = [None, W]
+    r = o.step([1], q, kn, vn, windows=windows)
+    pos = n0  # the new token's position
+    n_mass = n0 // T
+    per_layer = []
+    for layer in range(L):
+        masses = []
+        for row in range(2):
+            valid = [c for c in range(pos + 1) if c >= lo[row] and (windows[layer] is None or c > pos - W)]
+            first = min(valid)
+            assert valid == list(range(first, pos + 1))  # one contiguous range
+            k_all = np.concatenate([keys[layer][row], kn[layer][row][:, None]], axis=1)
+            v_all = np.concatenate([vals[layer][row], vn[layer][row][:, None]], axis=1)
+            out, w = _brute_force_layer(q[layer][row], k_all, v_all, first, n_rep, 1.0 / math.sqrt(d))
+            np.testing.assert_allclose(r["out"][layer][row], out, rtol=0, atol=2e-6)
+            masses.append([[w[h, b * T:(b + 1) * T].sum() for b in range(n_mass)] for h in range(hq)])
+        per_layer.append(np.mean(np.array(masses), axis=(0, 1)))
+    # The windowed layer gives no mass to blocks wholly at or before pos - W.
+    assert per_layer[1][0] == 0.0 and per_layer[1][1] == 0.0 and per_layer[0][0] > 0
+    averaged = np.sum(per_layer, axis=0) / L
+    np.testing.assert_allclose(r["placement"][1]["scores"], averaged / averaged.sum(), rtol=0, atol=1e-6)
+
+
 @pytest.mark.parametrize("policy", ["recent_only", "sinks_recent"])
 def test_score_free_policies_pass_uniform_scores(policy):
     o = PagedDecodeOracle(num_layers=1, num_query_heads=1, num_kv_heads=1, head_dim=8, tokens_per_block=16)

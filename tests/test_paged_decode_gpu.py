@@ -68,10 +68,13 @@ class Pair:
         self.dec.set_lo(sid, lo)
         self.ora.set_lo(sid, lo)
 
-    def step(self, gen, *, compute=True, scale=0.5, sids=None, order=None, end_stream=None, graphs=None):
+    def step(self, gen, *, compute=True, scale=0.5, sids=None, order=None, end_stream=None, graphs=None,
+             windows=None):
         """One decode step of `sids` (every session by default), checked against the oracle.
         With `graphs` (a dict) the layers run from a captured HIP graph, one per launch
-        signature: captured when the signature is new, replayed otherwise."""
+        signature: captured when the signature is new, replayed otherwise. windows[layer]:
+        that layer's own sliding window (None: none)."""
+        win = windows if windows is not None else [None] * self.layers
         sids = self.sids if sids is None else sids
         order = list(range(self.layers)) if order is None else order
         S = sum(self.dec.sessions[s].rows for s in sids)
@@ -84,7 +87,7 @@ class Pair:
         if graphs is None:
             outs = [None] * self.layers
             for l in order:
-                outs[l] = self.dec.decode_layer(l, qs[l].cuda(), ks[l].cuda(), vs[l].cuda())
+                outs[l] = self.dec.decode_layer(l, qs[l].cuda(), ks[l].cuda(), vs[l].cuda(), window=win[l])
         else:
             mass = self.dec._mass
             sig = (self.dec.pool.step_signature(), None if mass is None else mass.data_ptr(), S)
@@ -95,7 +98,7 @@ class Pair:
                 graph = torch.cuda.CUDAGraph()
                 with torch.cuda.graph(graph):
                     for l in order:
-                        outs[l] = self.dec.decode_layer(l, ins[0][l], ins[1][l], ins[2][l])
+                        outs[l] = self.dec.decode_layer(l, ins[0][l], ins[1][l], ins[2][l], window=win[l])
                 entry = graphs[sig] = (graph, ins, outs)
             else:
                 for dst, src in zip(entry[1], (qs, ks, vs)):
@@ -111,7 +114,7 @@ class Pair:
             with torch.cuda.stream(end_stream):
                 res = self.dec.end_step()
         ref = self.ora.step(sids, [np32(x) for x in qs], [np32(x) for x in ks], [np32(x) for x in vs],
-                            compute=compute)
+                            compute=compute, windows=windows)
         assert gather == ref["gather"], "gather index lists differ"
         for sid in sids:
             got, want = res[sid], ref["placement"][sid]
@@ -451,7 +454,38 @@ GRID = [
     (32, 2, 128, 32, torch.bfloat16, 0.07, 30.0, "sinks_heavy_hitter", "staged"),
     (16, 1, 64, 16, torch.float16, None, 50.0, "recent_only", "staged"),
     (8, 8, 128, 64, torch.float16, None, None, "sinks_recent", "direct"),
+    # Head dims 16 and 256 (Gemma / Gemma2 geometries: 8q/1kv and 16q/8kv at 256, with
+    # Gemma2's query_pre_attn_scalar scale and attn-logit softcap).
+    (4, 2, 16, 16, torch.float16, 16**-0.5, 50.0, "sinks_heavy_hitter", "direct"),
+    (8, 4, 16, 32, torch.bfloat16, None, None, "heavy_hitter", "staged"),
+    (8, 1, 256, 16, torch.bfloat16, None, None, "sinks_heavy_hitter", "direct"),
+    (16, 8, 256, 32, torch.float16, 256**-0.5, 50.0, "recent_only", "staged"),
 ]
+
+
+@pytest.mark.parametrize("mode", ["direct", "staged"])
+@pytest.mark.parametrize("d,tpb,window", [(16, 16, 24), (64, 32, 100), (256, 16, 40)])
+def test_per_layer_sliding_windows(d, tpb, window, mode):
+    """Layers alternating between a sliding window and global attention (Gemma2): the windowed
+    layers mask the stored positions <= current - window in the kernel while the global ones
+    read everything, over steps that move the window across block boundaries, with a padded
+    row. Outputs, block mass (scores), gather lists and placement against the oracle."""
+    g = torch.Generator().manual_seed(d + window)
+    p = Pair(layers=4, hq=8, hkv=4, d=d, tpb=tpb, dtype=torch.bfloat16, pool_blocks=64, host_blocks=160,
+             stream_mode=mode, scale=d**-0.5, softcap=50.0, staging_blocks=128)
+    ctx = 14 * tpb + 7
+    sid = p.add(ctx=ctx, rows=2, capacity=ctx + 3 * tpb, gen=g, vram_budget=8 * MIB16, ram_budget=512 * MIB16,
+                recent_window=1, rebalance_interval=2, policy="sinks_heavy_hitter", lo=[0, 9])
+    windows = [window, None, window, None]
+    errs = []
+    for _ in range(2 * tpb + 3):
+        res, ref, err = p.step(g, windows=windows)
+        errs.append(err)
+        got = np.array(res[sid]["block_attention"])
+        want = np.array(ref["placement"][sid]["scores"])
+        assert np.abs(got - want).max() < 2e-5
+    assert max(errs) < TOL
+    assert p.dec.pool.step_stats()["host_blocks"] > 0
 
 
 @pytest.mark.parametrize("hq,hkv,d,tpb,dtype,scale,softcap,policy,mode", GRID)

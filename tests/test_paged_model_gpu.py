@@ -288,16 +288,36 @@ def _family_model(family):
         cfg = tr.Qwen2MoeConfig(moe_intermediate_size=256, shared_expert_intermediate_size=512, num_experts=4,
                                 num_experts_per_tok=2, **common)
         cls = tr.Qwen2MoeForCausalLM
-    else:
+    elif family == "starcoder2":
         cfg = tr.Starcoder2Config(sliding_window=96, **common)  # every layer windowed
         cls = tr.Starcoder2ForCausalLM
+    elif family == "gemma":  # head_dim 256 with one KV head, as Gemma-2B
+        common.update(num_key_value_heads=1, head_dim=256)
+        cfg = tr.GemmaConfig(**common)
+        cls = tr.GemmaForCausalLM
+    elif family.startswith("gemma2"):
+        # Sliding window on alternating layers, query_pre_attn_scalar scale, attn-logit and
+        # final-logit softcapping. gemma2: the reference's own tiny verification geometry
+        # (bench/streaming_paged_model_verify_sliding_window_mvp.py:42-55: head_dim 16,
+        # query_pre_attn_scalar 16); gemma2_256: head_dim 256 as the released models.
+        d = 16 if family == "gemma2" else 256
+        common.update(num_hidden_layers=4, head_dim=d)
+        cfg = tr.Gemma2Config(sliding_window=96, query_pre_attn_scalar=d, attn_logit_softcapping=50.0,
+                              final_logit_softcapping=30.0, attn_implementation="eager", **common)
+        cls = tr.Gemma2ForCausalLM
+    else:  # phi3: fused qkv_proj; every layer windowed
+        cfg = tr.Phi3Config(sliding_window=160, pad_token_id=0, **common)
+        cls = tr.Phi3ForCausalLM
     torch.manual_seed(41)
     return cls(cfg).to(dtype=torch.float16, device="cuda").eval()
 
 
-@pytest.mark.parametrize("family", ["qwen2_moe", "starcoder2"])
+@pytest.mark.parametrize("family", ["qwen2_moe", "starcoder2", "gemma", "gemma2", "gemma2_256", "phi3"])
 def test_other_model_families_greedy_match_unpaged(family):
-    """Qwen2-MoE and Starcoder2 (sliding window 96) through the same attention entry."""
+    """Qwen2-MoE, Starcoder2 (sliding window 96), Gemma (head_dim 256), Gemma2 (alternating
+    sliding window 96, softcaps; head_dim 16 and 256) and Phi3 (sliding window 160) through the
+    same attention entry, against the unpaged model: the reference's architecture list
+    (paged_model.py:82-86, bench/streaming_paged_model_verify_new_archs_mvp.py)."""
     from pager_hf import PagedModel
 
     model = _family_model(family)
