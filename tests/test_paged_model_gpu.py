@@ -333,6 +333,25 @@ def test_other_model_families_greedy_match_unpaged(family):
     assert pm.last_run_stats.total_cpu_to_gpu_mb > 0
 
 
+@pytest.mark.parametrize("family,stream_mode", [("gemma2", "direct"), ("gemma2_256", "staged"), ("phi3", "direct")])
+def test_model_families_under_hip_graphs(family, stream_mode):
+    """Decode steps replayed from HIP graphs for models whose layers pass their own window,
+    scale and softcap (Gemma2) or share one window (Phi3): the same tokens as eager steps.
+    The per-layer window is a launch argument of each captured layer."""
+    from pager_hf import PagedModel
+
+    model = _family_model(family)
+    g = torch.Generator().manual_seed(43)
+    ids = torch.randint(3, 2048, (1, 300), generator=g).cuda()
+    mask = torch.ones_like(ids)
+    kw = dict(vram_budget=4 * MIB16, ram_budget=1 << 40, recent_window=2, policy="sinks_heavy_hitter",
+              tokens_per_block=16, stream_mode=stream_mode)
+    eager = PagedModel(model, **kw).generate(ids, mask, 40)
+    graphs = PagedModel(model, use_hip_graphs=True, **kw)
+    assert graphs.generate(ids, mask, 40) == eager
+    assert len(graphs._graphs) > 0
+
+
 def test_reload_mode_flag_gives_the_same_tokens():
     """use_streaming_attention=False (the reference's reload mode) computes the same attention."""
     from pager_hf import PagedModel
