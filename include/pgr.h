@@ -157,7 +157,7 @@ typedef struct pgr_kv_config_s {
   int32_t staging_buffers;  /* ring depth, >= 1 (2 = double buffering) */
   int32_t blocks_per_workgroup; /* most block entries per workgroup (4..32; 0 = 32) */
   int32_t target_workgroups;    /* workgroups a launch aims for (0 = a multiple of the CU count) */
-  int32_t stream_mode;          /* PGR_STREAM_DIRECT (0) or PGR_STREAM_STAGED (1), see below */
+  int32_t stream_mode;          /* PGR_STREAM_DIRECT (0), _STAGED (1) or _MIRROR (2), see below */
 } pgr_kv_config_t;
 
 /* How decode reads host-resident blocks. DIRECT: the attention kernel reads them in place from
@@ -167,8 +167,17 @@ typedef struct pgr_kv_config_s {
  * step's host blocks fit one buffer and staging_buffers >= 2, pgr_kv_decode_layer(l) also
  * queues layer l+1's copies right after layer l's attention, so that they run under the
  * caller's work between the two layers. */
+/* MIRROR: every layer has an HBM mirror of its host records (HBM: host_records records per
+ * layer). pgr_kv_begin_step queues, on the store's side stream, DMA copies of each layer's
+ * span of the step's host records into that layer's mirror, and after each layer's copies a
+ * word that the layer's attention launch checks as it starts: once set, its workgroups read
+ * host blocks from the mirror, before that from the host in place (same data). The copies
+ * run beside whatever the caller runs between the step's layers, including a replayed graph
+ * of the layers; the next begin_step waits for them. For one long-context session whose
+ * host share fits in HBM as a mirror (a model between layers, e.g. a captured decode step). */
 #define PGR_STREAM_DIRECT 0
 #define PGR_STREAM_STAGED 1
+#define PGR_STREAM_MIRROR 2
 
 typedef struct pgr_kv_stats_s {
   uint64_t gpu_to_cpu_bytes, cpu_to_gpu_bytes, gpu_to_cpu_copies, cpu_to_gpu_copies;

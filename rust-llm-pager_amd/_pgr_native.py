@@ -33,6 +33,7 @@ MODE_FOLD_FIXED = 3
 
 STREAM_DIRECT = 0
 STREAM_STAGED = 1
+STREAM_MIRROR = 2
 
 ABI_VERSION = 7
 

@@ -689,6 +689,8 @@ struct PagedArgs {
   int hq, hkv, n_rep, tokens_per_block, mass_stride;
   float scale, softcap;
   int window;             // > 0: the layer's sliding window (see PagedLaunch)
+  const uint16_t* mirror;       // mirror mode: HBM copy of `stage` (the host mirror), or null
+  const uint32_t* mirror_flag;  // set once this layer's copies into `mirror` have landed
   uint32_t* plan_flag;    // merge: pinned word for plan_token (see PagedLaunch), or null
   uint32_t plan_token;
 };
@@ -791,6 +793,10 @@ struct TileMeta {
   int last;      // last tile of its block
 };
 
+// Mirror mode: most reads of a layer's "mirror filled" word before a workgroup reads the host
+// in place instead (s_sleep 127 between reads: ~8k cycles each, ~20 ms in all).
+constexpr int kMirrorPolls = 6000;
+
 template <int D>
 struct PagedRing {
   // Register tiles per wave. At head dim 256 a tile is 64 VGPRs of K and V per lane (next to
@@ -850,6 +856,28 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(const WorkItem* __restr
   // slots exist in every work item).
   BlockEntry ecur = wi->entries[wave], enxt = wi->entries[wave + kWaves];
 
+  // Mirror mode: host records come from the layer's HBM mirror, filled by DMA on the store's
+  // copy stream, which sets the word after the layer's copies. One lane per workgroup polls
+  // the word past the caches, sleeping between reads, for at most kMirrorPolls reads (~20 ms);
+  // if it is still clear then, the workgroup reads the host in place (same data). The copies
+  // do not depend on this launch, so the wait ends with them. A host record's data never
+  // change while its session holds it, and the mirror is refilled only after the launches
+  // of the step before have finished.
+  const uint16_t* host_src = stage;
+  if (a.mirror_flag != nullptr) {
+    __shared__ uint32_t mirror_ready;
+    if (threadIdx.x == 0) {
+      uint32_t f = __hip_atomic_load(a.mirror_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      for (int i = 0; f == 0u && i < kMirrorPolls; ++i) {
+        __builtin_amdgcn_s_sleep(127);
+        f = __hip_atomic_load(a.mirror_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      }
+      mirror_ready = f;
+    }
+    __syncthreads();
+    if (__builtin_amdgcn_readfirstlane(mirror_ready) != 0u) host_src = a.mirror;
+  }
+
   RunVec<D> q[LaneRun<D>::N];  // loaded behind the first tile (below)
 
   // Score transform: x = mult * s' with s' = s (no softcap) or cap * tanh(s * scale / cap).
@@ -871,7 +899,7 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(const WorkItem* __restr
   int nf = 0, fe = 0, ftb = 0;
   auto fetch = [&](PTile<D>& t, TileMeta& mt) {
     const int slot = ecur.slot, bid = ecur.block_id;
-    const uint16_t* rb = slot >= 0 ? pool + (size_t)slot * rec : stage + (size_t)(-slot - 1) * rec;
+    const uint16_t* rb = slot >= 0 ? pool + (size_t)slot * rec : host_src + (size_t)(-slot - 1) * rec;
     const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(rb + head_off), (short)0, nf < tiles ? 0x7fffffff : 0, kBufferFlags);
     const uint32_t sk = (uint32_t)(ftb * 16 * D * 2);
@@ -1424,6 +1452,8 @@ hipError_t launch_paged(int dtype, int d, const PagedLaunch& p, hipStream_t stre
   a.scale = p.scale;
   a.softcap = p.softcap;
   a.window = p.window;
+  a.mirror = static_cast<const uint16_t*>(p.mirror);
+  a.mirror_flag = p.mirror_flag;
   const bool mass = p.mass_m != nullptr;
   return dtype == kF16 ? launch_paged_d<F16>(a, d, p.n_work, mass, stream)
                        : launch_paged_d<BF16>(a, d, p.n_work, mass, stream);

@@ -135,6 +135,12 @@ __global__ void stage_copy_kernel(const void* host, void* stage, const int64_t* 
   }
 }
 
+// Mirror mode: resets the per-layer "mirror filled" words on the step's stream: 0 when the
+// step's copies follow, 1 when there is nothing to copy (no launch then waits).
+__global__ void mirror_flags_reset_kernel(uint32_t* flags, int n, uint32_t value) {
+  if ((int)threadIdx.x < n) flags[threadIdx.x] = value;
+}
+
 // Staged mode: the step plan, copied from the pinned plan buffer (read in place through its
 // device mapping) into the workspace; in direct mode the step's first attention launch does
 // this copy itself. A copy kernel on the compute stream, rather than an SDMA copy, keeps the
@@ -182,6 +188,11 @@ PagedKV::~PagedKV() {
   }
   if (plan_uploaded_) hipEventDestroy(plan_uploaded_);
   if (cap_fork_) hipEventDestroy(cap_fork_);
+  if (mirror_go_) hipEventDestroy(mirror_go_);
+  if (mirror_done_) hipEventDestroy(mirror_done_);
+  for (void* p : mirror_)
+    if (p) hipFree(p);
+  if (mirror_flags_) hipFree(mirror_flags_);
   if (stage_copies_done_) hipEventDestroy(stage_copies_done_);
   if (moves_done_) hipEventDestroy(moves_done_);
   if (decode_done_) hipEventDestroy(decode_done_);
@@ -272,7 +283,8 @@ int PagedKV::init() {
   if (cfg_.dtype != kF16 && cfg_.dtype != kBF16) return fail(kErrInvalid, "dtype must be fp16 or bf16");
   if (cfg_.pool_slots <= 0 || cfg_.host_records < 0 || cfg_.staging_slots <= 0 || cfg_.staging_buffers < 1)
     return fail(kErrInvalid, "pool_slots, staging_slots > 0 and staging_buffers >= 1 required");
-  if (cfg_.stream_mode != 0 && cfg_.stream_mode != 1) return fail(kErrInvalid, "stream_mode must be 0 or 1");
+  if (cfg_.stream_mode < 0 || cfg_.stream_mode > 2) return fail(kErrInvalid, "stream_mode must be 0, 1 or 2");
+  if (cfg_.stream_mode == 2 && cfg_.num_layers > 256) return fail(kErrInvalid, "mirror mode takes at most 256 layers");
   if (cfg_.host_records > INT32_MAX / 2) return fail(kErrInvalid, "host_records too large for 32-bit record indices");
   if (cfg_.pool_slots > INT32_MAX / 2 || cfg_.staging_slots * cfg_.staging_buffers > INT32_MAX / 2)
     return fail(kErrInvalid, "pool or staging too large for 32-bit record indices");
@@ -294,6 +306,13 @@ int PagedKV::init() {
   // The staging ring exists for the staged stream mode only: in the direct mode the kernels
   // and the copy kernels read and write the host mirror in place.
   if (cfg_.stream_mode == 1) PGR_HIP(hipMalloc(&stage_, rec * (size_t)cfg_.staging_slots * cfg_.staging_buffers));
+  if (cfg_.stream_mode == 2) {
+    mirror_.assign(cfg_.num_layers, nullptr);
+    for (int l = 0; l < cfg_.num_layers; ++l)
+      if (cfg_.host_records > 0) PGR_HIP(hipMalloc(&mirror_[l], rec * (size_t)cfg_.host_records));
+    PGR_HIP(hipMalloc(reinterpret_cast<void**>(&mirror_flags_), 256 * sizeof(uint32_t)));
+    PGR_HIP(hipMemset(mirror_flags_, 0, 256 * sizeof(uint32_t)));
+  }
   PGR_HIP(hipStreamCreateWithFlags(&copy_stream_, hipStreamNonBlocking));
   buf_free_.resize(cfg_.staging_buffers);
   chunk_ready_.resize(cfg_.staging_buffers);
@@ -311,6 +330,8 @@ int PagedKV::init() {
   }
   PGR_HIP(hipEventCreateWithFlags(&plan_uploaded_, ev_flags));
   PGR_HIP(hipEventCreateWithFlags(&cap_fork_, ev_flags));
+  PGR_HIP(hipEventCreateWithFlags(&mirror_go_, ev_flags));
+  PGR_HIP(hipEventCreateWithFlags(&mirror_done_, ev_flags));
   for (PlanBuf& b : plan_bufs_) PGR_HIP(hipEventCreateWithFlags(&b.read, ev_flags));
   PGR_HIP(hipHostMalloc(reinterpret_cast<void**>(&plan_flags_), 256, hipHostMallocDefault));
   std::memset(plan_flags_, 0, 256);
@@ -855,6 +876,7 @@ int PagedKV::begin_step(const int32_t* sids, int n, hipStream_t stream) {
   seqs_.clear();
   work_.clear();
   copies_.clear();
+  mirror_spans_.clear();
   step_host_ids_.clear();
   step_stats_ = StepStats();
   // Validate and open a block where the new token starts one.
@@ -909,6 +931,7 @@ int PagedKV::begin_step(const int32_t* sids, int n, hipStream_t stream) {
       append_pos.push_back((int32_t)(p % T));
       max_mass = std::max<int>(max_mass, (int)n_full);
       std::vector<int64_t> host_ids;
+      int64_t span_lo = -1, span_hi = -1;  // mirror mode: this row's host records to copy
       int64_t b = first_blk;
       while (b < n_full) {
         const int32_t sl = s.slot[b * s.rows + r];
@@ -924,9 +947,13 @@ int PagedKV::begin_step(const int32_t* sids, int n, hipStream_t stream) {
           if (!s.host_valid[x * s.rows + r]) return fail(kErrState, "host block without data (not imported)");
           host_ids.push_back(x);
         }
-        if (cfg_.stream_mode == 0) {  // direct: the kernel reads the host records in place
+        if (cfg_.stream_mode != 1) {  // direct and mirror: the kernel reads host record indices
           for (int64_t x = b; x < e; ++x)
             pend.push_back({seq, BlockEntry{(int32_t)(-(s.row[r].host_off + x) - 1), (int32_t)x}, 0});
+          if (cfg_.stream_mode == 2) {  // one span per row: its first to last host record
+            if (span_lo < 0) span_lo = s.row[r].host_off + b;
+            span_hi = s.row[r].host_off + e;
+          }
           step_stats_.host_blocks += e - b;
           step_stats_.host_tokens += (e - b) * T;
           b = e;
@@ -955,6 +982,7 @@ int PagedKV::begin_step(const int32_t* sids, int n, hipStream_t stream) {
         pend.push_back({seq, BlockEntry{s.slot[(p / T) * s.rows + r], (int32_t)(p / T)}, 0});
       step_stats_.resident_tokens += p % T + 1;  // stored part of the open block + the current token
       step_host_ids_.push_back(std::move(host_ids));
+      if (span_lo >= 0) mirror_spans_.push_back({span_lo, span_hi - span_lo});
     }
   }
   const bool any_host = !copies_.empty();
@@ -1180,7 +1208,42 @@ int PagedKV::begin_step(const int32_t* sids, int n, hipStream_t stream) {
   d_mass_s_ = reinterpret_cast<float*>(d + o_ms);
   d_mf_ = reinterpret_cast<float*>(d + o_mf);
   d_lf_ = reinterpret_cast<float*>(d + o_lf);
+  if (cfg_.stream_mode == 2)
+    if (int rc = issue_mirror_copies(stream); rc != kOk) return rc;
   in_step_ = true;
+  return kOk;
+}
+
+// Mirror mode (end of begin_step). The layers' "mirror filled" words are reset on the step's
+// stream once the previous step's copies have finished (a word set late by one of them
+// would announce that step's data); this step's copies then start on the copy stream behind
+// that point, so after the previous step's launches, which read the mirrors, and after tier
+// moves queued on `stream`. Per layer: one DMA copy per row span (its first to last host
+// record of the step), then the layer's word, written by the copy stream itself
+// (hipStreamWriteValue32: no kernel, so a launch waiting for the word cannot hold it up).
+int PagedKV::issue_mirror_copies(hipStream_t stream) {
+  if (int rc = order_after_decode(stream); rc != kOk) return rc;
+  if (mirror_pending_) {
+    PGR_HIP(hipStreamWaitEvent(stream, mirror_done_, 0));
+    mirror_pending_ = false;
+  }
+  mirror_flags_reset_kernel<<<1, 256, 0, stream>>>(mirror_flags_, cfg_.num_layers, mirror_spans_.empty() ? 1u : 0u);
+  PGR_HIP(hipGetLastError());
+  mirror_step_bytes_ = 0;
+  if (mirror_spans_.empty()) return kOk;
+  PGR_HIP(hipEventRecord(mirror_go_, stream));
+  PGR_HIP(hipStreamWaitEvent(copy_stream_, mirror_go_, 0));
+  const size_t rec = rec_bytes();
+  for (int l = 0; l < cfg_.num_layers; ++l) {
+    for (const auto& sp : mirror_spans_)
+      PGR_HIP(hipMemcpyHtoDAsync(static_cast<char*>(mirror_[l]) + (size_t)sp.first * rec,
+                                 static_cast<char*>(host_[l]) + (size_t)sp.first * rec, (size_t)sp.second * rec,
+                                 copy_stream_));
+    PGR_HIP(hipStreamWriteValue32(copy_stream_, mirror_flags_ + l, 1u, 0));
+  }
+  for (const auto& sp : mirror_spans_) mirror_step_bytes_ += (uint64_t)sp.second * rec;
+  PGR_HIP(hipEventRecord(mirror_done_, copy_stream_));
+  mirror_pending_ = true;
   return kOk;
 }
 
@@ -1205,7 +1268,11 @@ int PagedKV::decode_layer(int layer, const void* q, const void* k_new, const voi
   pl.k_new = k_new;
   pl.v_new = v_new;
   pl.pool = pool_[layer];
-  pl.stage = cfg_.stream_mode == 0 ? host_dev_[layer] : stage_;
+  pl.stage = cfg_.stream_mode == 1 ? stage_ : host_dev_[layer];
+  if (cfg_.stream_mode == 2) {
+    pl.mirror = mirror_[layer];
+    pl.mirror_flag = mirror_flags_ + layer;
+  }
   pl.seqs = d_seqs_;
   pl.pm = d_pm_;
   pl.pl = d_pl_;
@@ -1391,6 +1458,7 @@ int PagedKV::end_step(int32_t* completed, int* n_completed) {
   // layer (counted here rather than per launch, so that steps replayed from a captured graph
   // are counted too).
   stats_.stream_bytes += (uint64_t)step_stats_.host_blocks * rec_bytes() * cfg_.num_layers;
+  if (cfg_.stream_mode == 2) stats_.stream_copies += (uint64_t)mirror_spans_.size() * cfg_.num_layers;
   if (cfg_.stream_mode == 1) stats_.stream_copies += (uint64_t)copies_.size() * cfg_.num_layers;
   int c = 0;
   for (size_t i = 0; i < step_sids_.size(); ++i) {

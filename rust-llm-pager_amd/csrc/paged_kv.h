@@ -43,7 +43,7 @@ struct PagedKVConfig {
   int staging_buffers = 2;       // ring depth
   int blocks_per_workgroup = 32; // most block entries folded by one workgroup (4 waves)
   int target_workgroups = 0;     // workgroups a launch aims for (0: a multiple of the CU count)
-  int stream_mode = 0;           // 0: kernels read host blocks in place; 1: staged copies
+  int stream_mode = 0;           // 0: kernels read host blocks in place; 1: staged copies; 2: HBM mirror
 };
 
 struct StoreStats {
@@ -277,6 +277,7 @@ class PagedKV {
   hipEvent_t decode_done_ = nullptr;
   std::vector<hipStream_t> decode_waited_;
   int order_after_decode(hipStream_t stream);
+  int issue_mirror_copies(hipStream_t stream);
   void forget_streams();  // after a device-wide synchronization
   bool stage_copy_pending_ = false;
   std::vector<hipEvent_t> buf_free_;
@@ -288,6 +289,15 @@ class PagedKV {
   // before a replay precedes the whole graph on its stream.
   hipEvent_t cap_fork_ = nullptr;
   bool cap_forked_ = false;
+  // Mirror mode: per layer an HBM copy of the host records, filled by DMA on copy_stream_ at
+  // begin_step; mirror_flags_[l] (device words) is set once layer l's copies have landed.
+  std::vector<void*> mirror_;
+  uint32_t* mirror_flags_ = nullptr;
+  hipEvent_t mirror_go_ = nullptr;    // on the step's stream, after the flags are cleared
+  hipEvent_t mirror_done_ = nullptr;  // on copy_stream_, after the step's copies
+  bool mirror_pending_ = false;
+  std::vector<std::pair<int64_t, int64_t>> mirror_spans_;  // (first host record, count) per row
+  uint64_t mirror_step_bytes_ = 0;                         // bytes copied per layer this step
   std::vector<char> buf_free_cap_;
   std::vector<char> buf_free_eager_;
   std::vector<int32_t> free_slots_;

@@ -74,6 +74,9 @@ struct PagedLaunch {
   int n_work, hq, hkv, tokens_per_block, mass_stride;
   float scale, softcap;
   int window = 0;  // > 0: the layer's own sliding window (positions <= current - window masked)
+  // Mirror mode: the layer's HBM mirror of `stage` (the host mirror) and its "filled" word.
+  const void* mirror = nullptr;
+  const uint32_t* mirror_flag = nullptr;
   // Merge launch only: when set, the merge stores plan_token to *plan_flag (pinned host memory)
   // as it starts, telling the host that the attention launches before it, and so their read of
   // the step's plan buffer, have finished.

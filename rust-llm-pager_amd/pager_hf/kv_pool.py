@@ -4,7 +4,10 @@ One NativeKVPool owns, for every layer, an HBM slot pool, a pinned host mirror a
 staging ring, plus the per-session block tables. ``stream_mode="direct"`` (default) has the
 decode kernel read host-resident blocks in place over the host link; ``"staged"`` copies
 them into the staging ring first (and, when one buffer holds a layer's host blocks, queues
-the next layer's copies under the current layer). Sessions are groups of rows that share one
+the next layer's copies under the current layer); ``"mirror"`` keeps an HBM mirror of every
+layer's host records, refilled by DMA copies that begin_step queues on a side stream for the
+whole step, and the decode kernel of a layer reads the mirror once that layer's copies have
+landed (the host in place before). Sessions are groups of rows that share one
 placement (the reference's one-PagedModel-per-session model, kv_block_store.py:36-56).
 """
 from __future__ import annotations
@@ -68,7 +71,7 @@ class NativeKVPool:
         self.tokens_per_block = tokens_per_block
         self.dtype = dtype
         self.lib = N.lib()
-        modes = {"direct": nat.STREAM_DIRECT, "staged": nat.STREAM_STAGED}
+        modes = {"direct": nat.STREAM_DIRECT, "staged": nat.STREAM_STAGED, "mirror": nat.STREAM_MIRROR}
         if stream_mode not in modes:
             raise ValueError(f"stream_mode must be one of {sorted(modes)}, got {stream_mode!r}")
         self.stream_mode = stream_mode

@@ -120,14 +120,16 @@ class PagedModel:
     ):
         """Arguments and defaults of paged_model.py:200-215. Added: ``max_context_tokens``
         (tokens per row the native store is sized for; default: the first session's prompt
-        plus max_new_tokens) and ``stream_mode`` ("direct" or "staged"). The group size has
-        no effect: the native kernel covers every block in one launch.
+        plus max_new_tokens) and ``stream_mode`` ("direct", "staged" or "mirror"; see
+        NativeKVPool). The group size has no effect: the native kernel covers every block in
+        one launch.
         ``use_hip_graphs=True`` replays decode steps from a captured HIP graph: the first
         decode step runs eagerly, a step whose launch signature differs from the captured one
         (a new block changes the grids about once per block) is captured and replayed, later
         steps with the same signature are replayed. In the staged stream mode the graph holds
         the staging copies on the store's copy stream too, each layer's under the layer
-        before it.
+        before it. In the mirror mode the copies stay outside the graph: begin_step queues
+        them on the store's copy stream, where they run beside the replay.
         ``use_streaming_attention=False`` selects the reference's reload mode, which copies
         every block back into one HBM cache per step and runs the model's own attention
         (paged_model.py:717-760). For the supported model types it computes the same

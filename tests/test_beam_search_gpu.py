@@ -154,7 +154,7 @@ def _paged(model, **kw):
     return PagedModel(model, **args)
 
 
-@pytest.mark.parametrize("mode", ["direct", "staged"])
+@pytest.mark.parametrize("mode", ["direct", "staged", "mirror"])
 def test_lockstep_with_the_oracles_choices(mode):
     model = _model(SMALL, seed=31, init_std=0.05)
     ids, mask = _prompts(12, [300, 237], SMALL["vocab_size"])

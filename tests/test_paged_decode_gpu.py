@@ -69,11 +69,12 @@ class Pair:
         self.ora.set_lo(sid, lo)
 
     def step(self, gen, *, compute=True, scale=0.5, sids=None, order=None, end_stream=None, graphs=None,
-             windows=None):
+             windows=None, settle=False):
         """One decode step of `sids` (every session by default), checked against the oracle.
         With `graphs` (a dict) the layers run from a captured HIP graph, one per launch
         signature: captured when the signature is new, replayed otherwise. windows[layer]:
-        that layer's own sliding window (None: none)."""
+        that layer's own sliding window (None: none). settle: wait for the store's side-stream
+        work after begin_step (in the mirror mode every layer then reads its mirror)."""
         win = windows if windows is not None else [None] * self.layers
         sids = self.sids if sids is None else sids
         order = list(range(self.layers)) if order is None else order
@@ -84,6 +85,8 @@ class Pair:
             ks.append((torch.randn(S, self.hkv, self.d, generator=gen) * scale).to(self.dtype))
             vs.append((torch.randn(S, self.hkv, self.d, generator=gen) * scale).to(self.dtype))
         self.dec.begin_step(sids)
+        if settle:
+            self.dec.pool.sync()
         if graphs is None:
             outs = [None] * self.layers
             for l in order:
@@ -136,7 +139,7 @@ class Pair:
         return res, ref, err
 
 
-@pytest.mark.parametrize("mode", ["direct", "staged"])
+@pytest.mark.parametrize("mode", ["direct", "staged", "mirror"])
 def test_config1_single_layer_4096_ctx_8_resident(mode):
     g = torch.Generator().manual_seed(1)
     p = Pair(layers=1, hq=14, hkv=2, d=64, tpb=32, dtype=torch.float16, pool_blocks=32, host_blocks=256,
@@ -153,7 +156,7 @@ def test_config1_single_layer_4096_ctx_8_resident(mode):
     assert p.dec.pool.block_ids(sid, True) == list(range(121, 129))
 
 
-@pytest.mark.parametrize("mode", ["direct", "staged"])
+@pytest.mark.parametrize("mode", ["direct", "staged", "mirror"])
 def test_config2_batch8_ragged_contexts_128_steps(mode):
     g = torch.Generator().manual_seed(2)
     ctx = torch.randint(1024, 32769, (8,), generator=g).tolist()
@@ -198,7 +201,8 @@ def test_config4_mistral_layer_window_bf16(mode, staging_blocks):
 
 @pytest.mark.parametrize("mode,staging_blocks,staging_buffers,policy", [
     ("staged", 2048, 2, "recent_only"), ("staged", 2048, 3, "sinks_heavy_hitter"), ("staged", 40, 2, "recent_only"),
-    ("staged", 40, 3, "heavy_hitter"), ("direct", 2048, 2, "sinks_heavy_hitter")])
+    ("staged", 40, 3, "heavy_hitter"), ("direct", 2048, 2, "sinks_heavy_hitter"),
+    ("mirror", 2048, 2, "sinks_heavy_hitter"), ("mirror", 2048, 2, "recent_only")])
 def test_steps_replayed_from_captured_graphs(mode, staging_blocks, staging_buffers, policy):
     """Four layers per step captured into HIP graphs (one per launch signature; new blocks
     change it) and replayed, with eager steps in between. In the staged mode the graph holds
@@ -287,7 +291,7 @@ def test_sessions_join_and_leave_between_steps(mode, layers):
     assert reused  # a freed session id was handed out again
 
 
-@pytest.mark.parametrize("mode", ["direct", "staged"])
+@pytest.mark.parametrize("mode", ["direct", "staged", "mirror"])
 def test_tier_moves_on_another_stream(mode):
     """end_step (and with it the eviction copies) runs on a side stream on alternate steps,
     while begin_step and the attention launches run on the default stream. The evictions run
@@ -308,7 +312,7 @@ def test_tier_moves_on_another_stream(mode):
     assert evicted >= 8  # blocks complete and leave HBM on many steps
 
 
-@pytest.mark.parametrize("mode", ["direct", "staged"])
+@pytest.mark.parametrize("mode", ["direct", "staged", "mirror"])
 def test_scoring_placement_on_another_stream(mode):
     """A scoring policy with no recent window, placement on a side stream every other step:
     the mass read-back and the eviction of the block that completed in this very step (its
@@ -364,7 +368,7 @@ def test_back_to_back_steps_without_host_sync(mode, layers):
         assert err < TOL, f"step {i}: max-abs error {err}"
 
 
-@pytest.mark.parametrize("mode", ["direct", "staged"])
+@pytest.mark.parametrize("mode", ["direct", "staged", "mirror"])
 def test_work_items_of_many_blocks(mode):
     """Work items of more than 16 blocks: 16-token blocks, batch 12 at 7k-14k tokens (about
     8,000 in-scope blocks for one round of work items, 3 workgroups per CU), so a wave folds
@@ -389,7 +393,7 @@ def test_work_items_of_many_blocks(mode):
             assert np.abs(got - want).max() < 2e-5
 
 
-@pytest.mark.parametrize("mode", ["direct", "staged"])
+@pytest.mark.parametrize("mode", ["direct", "staged", "mirror"])
 def test_scoring_policy_mass_drives_placement(mode):
     """sinks_heavy_hitter over two layers: the per-block mass handed to the pager matches the
     oracle's within float tolerance and, where score gaps are clear, placement is identical."""
@@ -460,10 +464,37 @@ GRID = [
     (8, 4, 16, 32, torch.bfloat16, None, None, "heavy_hitter", "staged"),
     (8, 1, 256, 16, torch.bfloat16, None, None, "sinks_heavy_hitter", "direct"),
     (16, 8, 256, 32, torch.float16, 256**-0.5, 50.0, "recent_only", "staged"),
+    (14, 2, 64, 32, torch.bfloat16, None, 30.0, "sinks_heavy_hitter", "mirror"),
+    (8, 1, 256, 16, torch.float16, None, None, "heavy_hitter", "mirror"),
 ]
 
 
-@pytest.mark.parametrize("mode", ["direct", "staged"])
+@pytest.mark.parametrize("policy", ["recent_only", "sinks_heavy_hitter"])
+def test_mirror_mode_with_and_without_landed_copies(policy):
+    """Mirror mode over four layers: on settled steps the side stream's copies have landed
+    before the launches (every layer reads its HBM mirror), on the others the launches race
+    them (a layer reads the mirror or the host in place, whichever its word says). Outputs,
+    gather lists, scores and placement match the oracle on both, with blocks evicted to the
+    host and re-read through the mirror on later steps."""
+    g = torch.Generator().manual_seed(61)
+    ctx = [1500, 2600, 800]
+    p = Pair(layers=4, hq=8, hkv=2, d=64, tpb=32, dtype=torch.float16, pool_blocks=3 * 16,
+             host_blocks=sum(c // 32 + 8 for c in ctx), stream_mode="mirror")
+    for c in ctx:
+        p.add(ctx=c, capacity=c + 96, gen=g, vram_budget=10 * MIB16, ram_budget=1024 * MIB16, recent_window=3,
+              rebalance_interval=2, policy=policy)
+    scored = policy != "recent_only"
+    errs = []
+    for step in range(72):
+        _, _, err = p.step(g, compute=scored or step % 5 == 0, settle=step % 3 == 0)
+        if err is not None:
+            errs.append(err)
+        assert p.dec.pool.step_stats()["host_blocks"] > 100
+    assert max(errs) < TOL
+    assert p.dec.pool.stats()["stream_bytes"] > 0
+
+
+@pytest.mark.parametrize("mode", ["direct", "staged", "mirror"])
 @pytest.mark.parametrize("d,tpb,window", [(16, 16, 24), (64, 32, 100), (256, 16, 40)])
 def test_per_layer_sliding_windows(d, tpb, window, mode):
     """Layers alternating between a sliding window and global attention (Gemma2): the windowed

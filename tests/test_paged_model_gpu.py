@@ -366,7 +366,7 @@ def test_reload_mode_flag_gives_the_same_tokens():
     assert a == b
 
 
-@pytest.mark.parametrize("stream_mode", ["direct", "staged"])
+@pytest.mark.parametrize("stream_mode", ["direct", "staged", "mirror"])
 @pytest.mark.parametrize("policy", ["sinks_heavy_hitter", "recent_only"])
 def test_hip_graph_steps_match_eager_steps(policy, stream_mode):
     """Decode steps replayed from captured HIP graphs give the eager steps' logits and tokens,
@@ -405,7 +405,7 @@ def test_hip_graph_steps_match_eager_steps(policy, stream_mode):
     assert g2.generate(ids, mask, 40) == e2.generate(ids, mask, 40)
 
 
-@pytest.mark.parametrize("stream_mode", ["direct", "staged"])
+@pytest.mark.parametrize("stream_mode", ["direct", "staged", "mirror"])
 def test_hip_graphs_continue_a_session_with_fed_tokens(stream_mode):
     """A second generate() call with HIP graphs first feeds the tokens the caller appended
     since the first call: those steps run back to back with no host read between them, so
