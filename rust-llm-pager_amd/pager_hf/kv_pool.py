@@ -1,13 +1,15 @@
 """Python handle of the native paged KV store (``pgr_kv_*`` in include/pgr.h).
 
-One NativeKVPool owns, for every layer, an HBM slot pool, a pinned host mirror and an HBM
-staging ring, plus the per-session block tables. ``stream_mode="direct"`` (default) has the
+One NativeKVPool owns, for every layer, an HBM slot pool and a pinned host mirror (plus an HBM
+staging ring in the staged mode, or an HBM copy of the host mirror per layer in the mirror
+mode), and the per-session block tables. ``stream_mode="direct"`` (default) has the
 decode kernel read host-resident blocks in place over the host link; ``"staged"`` copies
 them into the staging ring first (and, when one buffer holds a layer's host blocks, queues
 the next layer's copies under the current layer); ``"mirror"`` keeps an HBM mirror of every
 layer's host records, refilled by DMA copies that begin_step queues on a side stream for the
-whole step, and the decode kernel of a layer reads the mirror once that layer's copies have
-landed (the host in place before). Sessions are groups of rows that share one
+whole step, and the decode kernel of a layer waits for that layer's copies and reads the
+mirror (or the host in place, if they have not landed within its bounded wait). Sessions are
+groups of rows that share one
 placement (the reference's one-PagedModel-per-session model, kv_block_store.py:36-56).
 """
 from __future__ import annotations
