@@ -15,8 +15,9 @@ host part against PCIe Gen5 x16.
 
 The HBM roofline is measured on the same batch with every block resident, over 24 layers
 (1.45 GB of K/V per step, beyond the 256 MB MALL): `roofline` is paged_attn_kernel's K/V
-bytes per launch over its HIP-event launch time there. Synthetic N(0,1)*0.5 data. Prints one
-JSON line.
+bytes per launch over its HIP-event launch time there. `roofline_by_launch_size` repeats that
+measurement at batch 16, 32 and 64 and for a Mistral-7B layer (--no-launch-scale leaves it
+out). Synthetic N(0,1)*0.5 data. Prints one JSON line.
 """
 from __future__ import annotations
 
@@ -585,11 +586,11 @@ def configs(args):
     return out
 
 
-def hbm_scale(args):
+def hbm_scale_rows(batches=(8, 16, 32, 64), mistral=True):
     """The all-resident attention kernel as the bytes per launch grow: Qwen2.5-0.5B geometry
-    (14q/2kv, D 64, fp16) at batch 8, 16, 32 and 64 with contexts U[1024, 32768], and a
-    Mistral-7B layer (32q/8kv, D 128, bf16) at batch 4 x 32768 tokens. Every block resident,
-    several layers so the K/V read per step exceeds the MALL; event-timed launches."""
+    (14q/2kv, D 64, fp16) at the given batches with contexts U[1024, 32768], and a Mistral-7B
+    layer (32q/8kv, D 128, bf16) at batch 4 x 32768 tokens. Every block resident, several
+    layers so the K/V read per step exceeds the MALL; event-timed launches."""
     import torch
 
     from pager_hf import PagedDecoder
@@ -637,13 +638,20 @@ def hbm_scale(args):
         out.append({"workload": name, "bytes_per_launch": by // n, "avg_launch_us": round(us, 2),
                     "achieved": round(by / n / us / 1e3, 1), "frac": round(by / n / us / 1e3 / HBM_PEAK_GBS, 4)})
 
-    for batch in (8, 16, 32, 64):
+    for batch in batches:
         ctxs = draw_contexts(CFG["seed"], batch, CFG["ctx_lo"], CFG["ctx_hi"])
         layers = max(2, int(1.6e9 // (sum(ctxs) * 512)))  # > 1.5 GB per step: past the MALL
         measure(f"0.5B layer, batch {batch}, contexts U[1024,32768], {layers} layers", 14, 2, 64, torch.float16,
                 ctxs, layers)
-    measure("Mistral-7B layer (32q/8kv, D 128, bf16), batch 4 x 32768, 4 layers", 32, 8, 128, torch.bfloat16,
-            [32768] * 4, 4)
+    if mistral:
+        measure("Mistral-7B layer (32q/8kv, D 128, bf16), batch 4 x 32768, 4 layers", 32, 8, 128, torch.bfloat16,
+                [32768] * 4, 4)
+    return out
+
+
+def hbm_scale(args):
+    """--workload hbm-scale: hbm_scale_rows() at batch 8 to 64 and the Mistral-7B layer."""
+    out = hbm_scale_rows()
     return {
         "metric": "all-resident paged attention HBM GB/s against bytes per launch",
         "value": out[-1]["achieved"],
@@ -742,6 +750,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=128)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-launch-scale", action="store_true",
+                    help="leave out roofline_by_launch_size (the all-resident kernel at batch 16 to 64)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--staging-blocks", type=int, default=2048, help="records per staging buffer")
     ap.add_argument("--staging-buffers", type=int, default=3)
@@ -916,6 +926,14 @@ def main() -> int:
         line["cpu_baseline"] = cpu_baseline(ctx, args.cpu_seconds)
     if args.configs:
         line["configs"] = configs(args)
+    if not args.no_launch_scale:
+        # The same kernel, every block resident, as a launch carries more bytes: batch 8 is the
+        # roofline above; a launch of several rounds of workgroups amortizes each workgroup's
+        # fixed start, query wait and partial store.
+        line["roofline_by_launch_size"] = {
+            "kernel": "paged_attn_kernel", "bound": "hbm", "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "rows": hbm_scale_rows(batches=(16, 32, 64), mistral=True),
+        }
     print(json.dumps(line), flush=True)
     return 0
 
