@@ -182,6 +182,7 @@ PagedKV::~PagedKV() {
     hipEventDestroy(t.start);
     hipEventDestroy(t.stop);
   }
+  for (hipEvent_t e : timing_events_) hipEventDestroy(e);
   for (auto& t : move_timing_) {
     hipEventDestroy(t.start);
     hipEventDestroy(t.stop);
@@ -1362,10 +1363,11 @@ int PagedKV::decode_layer(int layer, const void* q, const void* k_new, const voi
       // Timing-only events recorded on the stream right before and after the launch. Without
       // a system-scope fence at record time they do not write back and invalidate the caches
       // around the launch they stamp. (Events handed to the launch itself read 15 to 18 us on
-      // the same launches, varying from process to process; these read a steady ~1 us above
-      // the kernel trace.)
-      PGR_HIP(hipEventCreateWithFlags(&t.start, hipEventDisableSystemFence));
-      PGR_HIP(hipEventCreateWithFlags(&t.stop, hipEventDisableSystemFence));
+      // the same launches, varying from process to process.) They come from a pool: creating
+      // two events per launch made a timed pass host-bound, and then a launch's interval also
+      // held the host's time between recording its start and submitting it.
+      PGR_HIP(timing_event(&t.start));
+      PGR_HIP(timing_event(&t.stop));
       PGR_HIP(hipEventRecord(t.start, stream));
     }
     PGR_HIP(launch_paged(cfg_.dtype, cfg_.head_dim, pl, stream));
@@ -1655,11 +1657,21 @@ int PagedKV::resolve_timing() {
     timing_ms_ += ms;
     timing_launches_ += 1;
     timing_bytes_ += t.bytes;
-    hipEventDestroy(t.start);
-    hipEventDestroy(t.stop);
+    timing_events_.push_back(t.start);
+    timing_events_.push_back(t.stop);
   }
   timing_pending_.clear();
   return kOk;
+}
+
+// An event for launch timing: a resolved one from the pool, or a new one.
+hipError_t PagedKV::timing_event(hipEvent_t* ev) {
+  if (!timing_events_.empty()) {
+    *ev = timing_events_.back();
+    timing_events_.pop_back();
+    return hipSuccess;
+  }
+  return hipEventCreateWithFlags(ev, hipEventDisableSystemFence);
 }
 
 int PagedKV::kernel_time(double* ms, int64_t* launches, int64_t* bytes) {

@@ -339,6 +339,8 @@ class PagedKV {
 
   bool timing_ = false;
   std::vector<PendingTiming> timing_pending_;
+  std::vector<hipEvent_t> timing_events_;  // resolved launch-timing events, reused
+  hipError_t timing_event(hipEvent_t* ev);
   double timing_ms_ = 0.0;
   int64_t timing_launches_ = 0;
   int64_t timing_bytes_ = 0;
