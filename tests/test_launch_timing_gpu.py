@@ -1,0 +1,56 @@
+"""Launch timing of the paged attention kernel (pgr_kv_set_timing / pgr_kv_kernel_time), which
+bench.py's roofline figure is built on: counts, bytes and durations over passes that reuse the
+store's timing events, and no effect on the decode results."""
+import numpy as np
+import pytest
+import torch
+
+from oracle.paged_decode import PagedDecodeOracle
+from pager_hf import PagedDecoder
+
+MIB16 = 16 * 1024 * 1024
+
+
+@pytest.mark.gpu
+def test_kernel_time_counts_and_bytes_over_reused_events():
+    layers, hq, hkv, d, T = 3, 14, 2, 64, 32
+    g = torch.Generator().manual_seed(11)
+    dec = PagedDecoder(num_layers=layers, num_query_heads=hq, num_kv_heads=hkv, head_dim=d, tokens_per_block=T,
+                       dtype=torch.float16, device="cuda:0", pool_blocks=64, host_blocks=64, staging_blocks=64)
+    ora = PagedDecodeOracle(num_layers=layers, num_query_heads=hq, num_kv_heads=hkv, head_dim=d, tokens_per_block=T)
+    kw = dict(vram_budget=4 * MIB16, ram_budget=64 * MIB16, recent_window=3, policy="recent_only")
+    n = 300
+    sid = dec.add_session(capacity_tokens=n + 64, **kw)
+    ora.add_session(sid, **kw)
+    ks = [(torch.randn(1, hkv, n, d, generator=g) * 0.5).half() for _ in range(layers)]
+    vs = [(torch.randn(1, hkv, n, d, generator=g) * 0.5).half() for _ in range(layers)]
+    dec.prefill(sid, [k.cuda() for k in ks], [v.cuda() for v in vs], n)
+    ora.prefill(sid, [k.float().numpy() for k in ks], [v.float().numpy() for v in vs], n)
+    dec.pool.kernel_time()  # clear
+    dec.pool.set_timing(True)
+    try:
+        for rnd in range(3):  # later rounds take their events from the pool the first one filled
+            steps = 2 + rnd
+            for _ in range(steps):
+                q = [(torch.randn(1, hq, d, generator=g) * 0.5).half() for _ in range(layers)]
+                kn = [(torch.randn(1, hkv, d, generator=g) * 0.5).half() for _ in range(layers)]
+                vn = [(torch.randn(1, hkv, d, generator=g) * 0.5).half() for _ in range(layers)]
+                dec.begin_step([sid])
+                st = dec.pool.step_stats()
+                outs = [dec.decode_layer(l, q[l].cuda(), kn[l].cuda(), vn[l].cuda()).float().cpu().numpy()
+                        for l in range(layers)]
+                dec.end_step()
+                ref = ora.step([sid], [x.float().numpy() for x in q], [x.float().numpy() for x in kn],
+                               [x.float().numpy() for x in vn])
+                for l in range(layers):
+                    assert float(np.abs(outs[l] - ref["out"][l]).max()) < 2e-3
+            torch.cuda.synchronize()
+            ms, launches, nbytes = dec.pool.kernel_time()
+            per_launch = st["launches"]
+            assert launches == steps * layers * per_launch, (launches, steps, layers, per_launch)
+            # K/V bytes read per launch: every in-scope stored block, whole blocks.
+            assert nbytes > 0 and nbytes % (2 * hkv * T * d * 2) == 0
+            assert ms > 0.0 and ms / launches < 5.0, ms  # milliseconds per launch: microseconds here
+    finally:
+        dec.pool.set_timing(False)
+        dec.pool.close()
