@@ -486,6 +486,9 @@ def config3(args):
     # layer before it ("staged"), or copied by DMA into per-layer HBM mirrors beside the
     # whole replayed step ("mirror"). --c3-runs selects some of them (for traces).
     runs = [r for r in args.c3_runs.split(",") if r]
+    known = ("eager_direct", "graphs_direct", "graphs_staged", "graphs_mirror")
+    if not runs or any(r not in known for r in runs):
+        raise SystemExit(f"--c3-runs takes a comma list of {', '.join(known)}; got {args.c3_runs!r}")
     for graphs, mode in ((False, "direct"), (True, "direct"), (True, "staged"), (True, "mirror")):
         if ("graphs_" if graphs else "eager_") + mode not in runs:
             continue
