@@ -17,7 +17,8 @@ The HBM roofline is measured on the same batch with every block resident, over 2
 (1.45 GB of K/V per step, beyond the 256 MB MALL): `roofline` is paged_attn_kernel's K/V
 bytes per launch over its HIP-event launch time there. `roofline_by_launch_size` repeats that
 measurement at batch 16, 32 and 64 and for a Mistral-7B layer (--no-launch-scale leaves it
-out). Synthetic N(0,1)*0.5 data. Prints one JSON line.
+out). `operator_api` times the six-function operator API at the shapes of the reference's
+kernel probe (--no-operator leaves it out). Synthetic N(0,1)*0.5 data. Prints one JSON line.
 """
 from __future__ import annotations
 
@@ -671,6 +672,78 @@ def hbm_scale(args):
     }
 
 
+def operator_api(dtype_name="float16"):
+    """The six-function operator API (streaming_attention_state_init, _step, _finalize) on one
+    contiguous K/V chunk, the way the reference's own kernel probe times it
+    (bench/streaming_attention_kernel_scaling_probe.py:42-53, 56-65: Qwen2.5-7B shape, 28
+    query heads, 4 KV heads, head_dim 128, batch 1, 3 warmup calls, 20 timed between two
+    events, state init + step + finalize per call), at the probe's chunk sizes and at 32768
+    tokens, with torch's eager attention (matmul, softmax, matmul over repeated KV heads) on
+    the same inputs beside it as the probe does. K/V GB/s counts the chunk's K and V bytes."""
+    import torch
+
+    from pager_hf.streaming_attention import (streaming_attention_finalize, streaming_attention_state_init,
+                                              streaming_attention_step)
+
+    dtype = getattr(torch, dtype_name)
+    hq, hkv, d = 28, 4, 128
+    n_rep = hq // hkv
+    g = torch.Generator(device="cuda").manual_seed(3)
+
+    def time_cuda(fn, warmup=3, reps=20):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(reps):
+            fn()
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / reps
+
+    rows = []
+    for tokens in (64, 256, 1024, 2048, 4096, 32768):
+        q = (torch.randn(1, hq, d, device="cuda", generator=g) * 0.5).to(dtype)
+        k = (torch.randn(1, hkv, tokens, d, device="cuda", generator=g) * 0.5).to(dtype)
+        v = (torch.randn(1, hkv, tokens, d, device="cuda", generator=g) * 0.5).to(dtype)
+
+        def ours():
+            m, l, acc = streaming_attention_state_init(1, hq, d, q.device)
+            streaming_attention_step(q, k, v, m, l, acc)
+            streaming_attention_finalize(acc, l, q.dtype)
+
+        def eager():
+            kd = k.repeat_interleave(n_rep, dim=1)
+            vd = v.repeat_interleave(n_rep, dim=1)
+            scores = torch.matmul(kd, q.unsqueeze(3)) * (1.0 / d ** 0.5)  # [1, Hq, T, 1]
+            probs = torch.softmax(scores.float(), dim=2).to(dtype)
+            torch.matmul(probs.transpose(2, 3).contiguous(), vd)  # [1, Hq, 1, D]
+
+        ms = time_cuda(ours)
+        ms_eager = time_cuda(eager)
+        # The same call captured once and replayed: the device's own time per call, without the
+        # host's launch overhead (an eager call is host-bound below a few thousand tokens).
+        ours()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            ours()
+        ms_graph = time_cuda(graph.replay)
+        del graph
+        kv = 2 * hkv * tokens * d * k.element_size()
+        rows.append({"tokens": tokens, "ms_per_call": round(ms, 4), "torch_eager_ms": round(ms_eager, 4),
+                     "ms_per_call_graph": round(ms_graph, 4), "kv_GBs_graph": round(kv / ms_graph / 1e6, 1),
+                     "hbm_frac_graph": round(kv / ms_graph / 1e6 / HBM_PEAK_GBS, 4)})
+    return {
+        "workload": "operator API, Qwen2.5-7B shape (28q/4kv, D 128), batch 1, one contiguous chunk per call; "
+                    "state_init + step + finalize per call, 20 calls between two events (ms_per_call: eager calls, "
+                    "as the reference's probe times them; ms_per_call_graph: replays of the call captured in a HIP "
+                    "graph)",
+        "dtype": dtype_name, "rows": rows,
+    }
+
+
 def calibrate_host_read(mib):
     """Reads `mib` MiB of host-resident records once with records_to_hf_kernel, which reads the
     pinned host mirror in place through its device mapping: a known number of bytes over the
@@ -756,6 +829,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=128)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-operator", action="store_true",
+                    help="leave out operator_api (the streaming_attention_* operators at the reference probe's shapes)")
     ap.add_argument("--no-launch-scale", action="store_true",
                     help="leave out roofline_by_launch_size (the all-resident kernel at batch 16 to 64)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
@@ -936,6 +1011,8 @@ def main() -> int:
         line["cpu_baseline"] = cpu_baseline(ctx, args.cpu_seconds)
     if args.configs:
         line["configs"] = configs(args)
+    if not args.no_operator:
+        line["operator_api"] = operator_api()
     if not args.no_launch_scale:
         # The same kernel, every block resident, as a launch carries more bytes: batch 8 is the
         # roofline above; a launch of several rounds of workgroups amortizes each workgroup's

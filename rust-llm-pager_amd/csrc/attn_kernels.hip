@@ -593,46 +593,115 @@ __global__ __launch_bounds__(64) void dense_generic_kernel(DenseArgs a) {
 }
 
 // Combine the dense partials into the caller's running state, in place.
+// Split-K merge of the operator kernels: one 256-thread workgroup per (batch row, query head).
+// Thread (g, c) owns dims 2c, 2c+1 (D/2 columns) and merges the partial slots g, g+G, g+2G, ...
+// (G = 512/D groups) online, with kDenseMergeBatch slots' loads in flight before it uses any:
+// a running max and sums rescaled under it (e-based units, as the operator state). The groups
+// then combine through LDS with the state already in (m, l, acc). Stats mode merges (m, l)
+// only; the fixed-max modes add the partial sums as they are. A slot whose split held no valid
+// token carries m = -inf and adds nothing; if nothing is valid anywhere the state is left as
+// it was.
+constexpr int kDenseMergeThreads = 256;
+constexpr int kDenseMergeBatch = 8;
+
 template <int kMode>
-__global__ __launch_bounds__(64) void dense_merge_kernel(DenseArgs a, float* m, float* l, float* acc, int d) {
+__global__ __launch_bounds__(kDenseMergeThreads) void dense_merge_kernel(DenseArgs a, float* m, float* l, float* acc,
+                                                                         int d) {
+  __shared__ float sm_m[kDenseMergeThreads];
+  __shared__ float sm_l[kDenseMergeThreads];
+  __shared__ float sm_a[2 * kDenseMergeThreads];
   const int row = blockIdx.x;  // b * hq + qh
   const int b = row / a.hq, qh = row - b * a.hq;
-  if (a.active != nullptr && a.active[b] == 0) return;
+  if (a.active != nullptr && a.active[b] == 0) return;  // whole workgroup: uniform exit
   const int h = qh / a.n_rep, r = qh - h * a.n_rep;
   const size_t slot0 = ((size_t)b * a.hkv + h) * a.n_split;
-  const int lane = threadIdx.x;
-  if constexpr (kMode == kModeFold || kMode == kModeStats) {
+  const int cols = d / 2;                          // d is even (8 .. 256)
+  const int groups = kDenseMergeThreads / cols;    // 1 .. 64
+  const int g = threadIdx.x / cols, c = threadIdx.x - g * cols;
+  constexpr bool kOnline = kMode == kModeFold || kMode == kModeStats;
+  constexpr bool kAcc = kMode != kModeStats;
+  float mx = kNegInf, ls = 0.f, a0 = 0.f, a1 = 0.f;
+  const int n = a.n_split;
+  for (int s0 = g; s0 < n; s0 += groups * kDenseMergeBatch) {
+    float pmv[kDenseMergeBatch], plv[kDenseMergeBatch], p0[kDenseMergeBatch], p1[kDenseMergeBatch];
+#pragma unroll
+    for (int j = 0; j < kDenseMergeBatch; ++j) {
+      const int sj = s0 + j * groups;
+      const size_t slot = (slot0 + (sj < n ? sj : s0)) * a.n_rep + r;  // past the last slot: re-read s0, weight 0
+      pmv[j] = kOnline ? (sj < n ? a.pm[slot] : kNegInf) : 0.f;
+      plv[j] = kOnline ? a.pl[slot] : 0.f;
+      if constexpr (kAcc) {
+        const float2 v2 = *reinterpret_cast<const float2*>(a.pacc + slot * d + 2 * c);
+        p0[j] = sj < n ? v2.x : 0.f;
+        p1[j] = sj < n ? v2.y : 0.f;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kDenseMergeBatch; ++j) {
+      if constexpr (kOnline) {
+        const float mn = fmaxf(mx, pmv[j]);
+        if (mn != kNegInf) {
+          const float so = __expf(mx - mn), ss = __expf(pmv[j] - mn);
+          ls = ls * so + plv[j] * ss;
+          if constexpr (kAcc) {
+            a0 = a0 * so + p0[j] * ss;
+            a1 = a1 * so + p1[j] * ss;
+          }
+          mx = mn;
+        }
+      } else {
+        a0 += p0[j];
+        a1 += p1[j];
+      }
+    }
+  }
+  if (c == 0) {
+    sm_m[g] = mx;
+    sm_l[g] = ls;
+  }
+  if constexpr (kAcc) {
+    sm_a[g * d + 2 * c] = a0;
+    sm_a[g * d + 2 * c + 1] = a1;
+  }
+  __syncthreads();
+  if (g != 0) return;
+  if constexpr (kOnline) {
     const float m0 = m[row];
     float mf = m0;
-    for (int s = 0; s < a.n_split; ++s) mf = fmaxf(mf, a.pm[(slot0 + s) * a.n_rep + r]);
+    for (int gg = 0; gg < groups; ++gg) mf = fmaxf(mf, sm_m[gg]);
     if (mf == kNegInf) return;  // nothing valid anywhere yet: the state stays as it is
     const float w0 = __expf(m0 - mf);
     float lf = l[row] * w0;
-    for (int s = 0; s < a.n_split; ++s) {
-      const float ms = a.pm[(slot0 + s) * a.n_rep + r];
-      lf += a.pl[(slot0 + s) * a.n_rep + r] * __expf(ms - mf);
+    float x0 = 0.f, x1 = 0.f;
+    if constexpr (kAcc) {
+      x0 = acc[(size_t)row * d + 2 * c] * w0;
+      x1 = acc[(size_t)row * d + 2 * c + 1] * w0;
     }
-    if constexpr (kMode == kModeFold) {
-      for (int dd = lane; dd < d; dd += 64) {
-        float x = acc[(size_t)row * d + dd] * w0;
-        for (int s = 0; s < a.n_split; ++s) {
-          const float ms = a.pm[(slot0 + s) * a.n_rep + r];
-          x += a.pacc[((slot0 + s) * a.n_rep + r) * d + dd] * __expf(ms - mf);
-        }
-        acc[(size_t)row * d + dd] = x;
+    for (int gg = 0; gg < groups; ++gg) {
+      if (sm_m[gg] == kNegInf) continue;
+      const float wg = __expf(sm_m[gg] - mf);
+      lf += sm_l[gg] * wg;
+      if constexpr (kAcc) {
+        x0 += sm_a[gg * d + 2 * c] * wg;
+        x1 += sm_a[gg * d + 2 * c + 1] * wg;
       }
     }
-    __syncthreads();
-    if (lane == 0) {
+    if constexpr (kAcc) {
+      acc[(size_t)row * d + 2 * c] = x0;
+      acc[(size_t)row * d + 2 * c + 1] = x1;
+    }
+    if (c == 0) {
       m[row] = mf;
       l[row] = lf;
     }
   } else {
-    for (int dd = lane; dd < d; dd += 64) {
-      float x = acc[(size_t)row * d + dd];
-      for (int s = 0; s < a.n_split; ++s) x += a.pacc[((slot0 + s) * a.n_rep + r) * d + dd];
-      acc[(size_t)row * d + dd] = x;
+    float x0 = acc[(size_t)row * d + 2 * c], x1 = acc[(size_t)row * d + 2 * c + 1];
+    for (int gg = 0; gg < groups; ++gg) {
+      x0 += sm_a[gg * d + 2 * c];
+      x1 += sm_a[gg * d + 2 * c + 1];
     }
+    acc[(size_t)row * d + 2 * c] = x0;
+    acc[(size_t)row * d + 2 * c + 1] = x1;
   }
 }
 
@@ -1198,13 +1267,13 @@ hipError_t launch_dense_merge(const DenseArgs& a, int mode, int batch, int d, fl
   dim3 mgrid(batch * a.hq);
   switch (mode) {
     case kModeFold:
-      dense_merge_kernel<kModeFold><<<mgrid, 64, 0, stream>>>(a, m, l, acc, d);
+      dense_merge_kernel<kModeFold><<<mgrid, kDenseMergeThreads, 0, stream>>>(a, m, l, acc, d);
       break;
     case kModeStats:
-      dense_merge_kernel<kModeStats><<<mgrid, 64, 0, stream>>>(a, m, l, acc, d);
+      dense_merge_kernel<kModeStats><<<mgrid, kDenseMergeThreads, 0, stream>>>(a, m, l, acc, d);
       break;
     default:
-      dense_merge_kernel<kModeAccumulate><<<mgrid, 64, 0, stream>>>(a, m, l, acc, d);
+      dense_merge_kernel<kModeAccumulate><<<mgrid, kDenseMergeThreads, 0, stream>>>(a, m, l, acc, d);
       break;
   }
   return hipGetLastError();
