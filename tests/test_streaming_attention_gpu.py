@@ -388,3 +388,48 @@ def test_unsupported_head_dim_is_rejected():
     m, l, acc = streaming_attention_state_init(1, 8, 48, dev())
     with pytest.raises(NotImplementedError):
         streaming_attention_step(q, k, k, m, l, acc)
+
+
+# -- long chunks: many split-K slots per merge group ------------------------------------------
+
+
+@pytest.mark.parametrize("b, hq, hkv, d, tokens, dtype", [
+    (2, 28, 4, 128, 32768, torch.float16),    # 64 splits per (row, KV head), 4 merge groups
+    (1, 14, 2, 64, 65536, torch.bfloat16),    # 256 splits, 8 groups: four batches of slots per group
+    (1, 8, 1, 256, 16384, torch.float16),     # head dim 256 (VALU kernel), 2 groups
+    (1, 8, 2, 32, 8192, torch.float32),       # fp32 q/k/v
+])
+def test_long_chunk_merges_many_split_slots(b, hq, hkv, d, tokens, dtype):
+    """A chunk long enough that each merge thread group combines several batches of split-K
+    slots, folded after a first short chunk (so the merge also rescales an existing state),
+    with a masked stretch longer than a split (slots with m = -inf)."""
+    q, k, v = draw(40 + d, (b, hq, d), (b, hkv, 64 + tokens, d), (b, hkv, 64 + tokens, d), dtype=dtype, scale=0.5)
+    valid = torch.ones(b, 64 + tokens, dtype=torch.int32)
+    valid[:, 64 + tokens // 3: 64 + tokens // 3 + tokens // 4] = 0
+    qd, kd, vd, vald = q.cuda(), k.cuda(), v.cuda(), valid.cuda()
+    m, l, acc = streaming_attention_state_init(b, hq, d, dev())
+    streaming_attention_step(qd, kd[:, :, :64], vd[:, :, :64], m, l, acc, valid=vald[:, :64])
+    streaming_attention_step(qd, kd[:, :, 64:], vd[:, :, 64:], m, l, acc, valid=vald[:, 64:])
+    out = streaming_attention_finalize(acc, l, torch.float32)
+    ref, _ = dense(q, k, v, hq // hkv, valid=valid)
+    tol = 1e-4 if dtype == torch.float32 else TOL
+    assert max_abs(out, ref) < tol
+
+
+def test_long_two_pass_with_mass_merges_many_split_slots():
+    """Stats then accumulate over one 32768-token chunk (128 splits per KV head at this shape),
+    with 32-token block mass: output and mass against the dense oracle."""
+    hq, hkv, d, tokens, tpb = 28, 4, 128, 32768, 32
+    q, k, v = draw(77, (1, hq, d), (1, hkv, tokens, d), (1, hkv, tokens, d), scale=0.5)
+    qd, kd, vd = q.cuda(), k.cuda(), v.cuda()
+    m = torch.full((1, hq), float("-inf"), dtype=torch.float32, device=dev())
+    l = torch.zeros(1, hq, dtype=torch.float32, device=dev())
+    streaming_attention_stats_step(qd, kd, m, l)
+    acc = torch.zeros(1, hq, d, dtype=torch.float32, device=dev())
+    nbl = tokens // tpb
+    mass = torch.zeros(1, hq, nbl, dtype=torch.float32, device=dev())
+    streaming_attention_accumulate_step(qd, kd, vd, m, l, acc, mass, 0, tpb)
+    out = streaming_attention_finalize(acc, l, torch.float32)
+    ref, rmass = dense(q, k, v, hq // hkv, tpb)
+    assert max_abs(out, ref) < TOL
+    assert max_abs(mass, rmass) < 1e-4
