@@ -20,8 +20,12 @@
 
 #include <hip/hip_runtime.h>
 
+#include <condition_variable>
 #include <cstdint>
+#include <functional>
+#include <mutex>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "pgr_common.h"
@@ -66,6 +70,32 @@ struct StepStats {
   int64_t chunks = 0;
   int64_t launches = 0;         // attention kernel launches per layer
   int64_t work_items = 0;
+};
+
+// One host thread that runs submitted jobs one at a time: here, the HIP calls that queue a
+// step's mirror-mode copies, so that the caller's thread goes on to launch the step while
+// they are issued. Started by the first submit.
+class HostWorker {
+ public:
+  HostWorker() = default;
+  HostWorker(const HostWorker&) = delete;
+  HostWorker& operator=(const HostWorker&) = delete;
+  ~HostWorker() { stop(); }
+  // Runs `job` on the worker thread. A job submitted before must have been waited for.
+  void submit(std::function<hipError_t()> job);
+  // Returns once the submitted job (if any) has run, with its result; hipSuccess if none.
+  hipError_t wait();
+  void stop();  // runs a submitted job to its end, then ends the thread
+
+ private:
+  void run();
+  std::thread thread_;
+  std::mutex mu_;
+  std::condition_variable cv_;
+  std::function<hipError_t()> job_;
+  bool pending_ = false;
+  bool stop_ = false;
+  hipError_t result_ = hipSuccess;
 };
 
 class PagedKV {
@@ -225,6 +255,7 @@ class PagedKV {
   void* ws_ = nullptr;
   size_t ws_bytes_ = 0;
   int n_cu_ = 0;                  // compute units of the device
+  int device_ = 0;                // the device current at init
   void** bases_dev_ = nullptr;  // [pool_0 .. pool_{L-1}, host_dev_0 .. host_dev_{L-1}] on the device
   IndexBuf index_bufs_[kIndexBufs];
   int next_index_buf_ = 0;
@@ -296,6 +327,11 @@ class PagedKV {
   hipEvent_t mirror_go_ = nullptr;    // on the step's stream, after the flags are cleared
   hipEvent_t mirror_done_ = nullptr;  // on copy_stream_, after the step's copies
   bool mirror_pending_ = false;
+  // Issues the mirror copies and word writes of a step (about 0.25 ms of HIP calls for 22
+  // layers) while begin_step returns. issue_mirror_copies waits for its previous job before
+  // it records or waits on mirror_go_ / mirror_done_ again, and so do sync() and the
+  // destructor before they drain the copy stream.
+  HostWorker mirror_issuer_;
   std::vector<std::pair<int64_t, int64_t>> mirror_spans_;  // (first host record, count) per row
   uint64_t mirror_step_bytes_ = 0;                         // bytes copied per layer this step
   std::vector<char> buf_free_cap_;
