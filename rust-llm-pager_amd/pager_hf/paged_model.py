@@ -239,19 +239,30 @@ class PagedModel:
                 self._extend_session(input_ids, attention_mask, max_new_tokens)
 
             next_input_id = input_ids[:, -1:]
-            current_attention_mask = attention_mask
-            generated_per_row: list[list[int]] = [[] for _ in range(batch_size)]
+            # The mask only grows by a real column per generated token, so the current token's
+            # position is the last one's plus 1 and each row's left padding stays the same
+            # (paged_model.py:373-385 rebuilds both from the grown mask every step). Token ids
+            # stay on the device until the loop ends: no host synchronization between steps
+            # besides the placement's.
+            _, _, _, _, window = self._model_geometry()
+            position_ids = self._position_ids_from_mask(attention_mask)[:, -1:]
+            n_cols = attention_mask.shape[1]
+            pads = (n_cols - attention_mask.long().sum(dim=1)).tolist() if window is not None else None
+            token_ids: list[torch.Tensor] = []
             stats = GenerationStats()
             in_gpu: list[float] = []
-            for _ in range(max_new_tokens):
-                logits, step = self._forward_step(next_input_id, current_attention_mask)
+            for t in range(max_new_tokens):
+                lo = None
+                if window is not None:
+                    col = n_cols - 1 + t
+                    lo = [max(p, col - window + 1) for p in pads]
+                logits, step = self._forward_step(next_input_id, None, position_ids=position_ids, lo=lo)
                 if do_sample:
                     next_token_id = self._sample_next_token(logits, temperature=temperature, top_k=top_k, top_p=top_p,
                                                             generator=generator)
                 else:
                     next_token_id = torch.argmax(logits, dim=-1, keepdim=True)
-                for row_tokens, token_id in zip(generated_per_row, next_token_id[:, 0].tolist()):
-                    row_tokens.append(token_id)
+                token_ids.append(next_token_id)
                 stats.total_new_blocks += step["new_blocks"]
                 stats.total_gpu_to_cpu_mb += step["gpu_to_cpu_mb"]
                 stats.total_cpu_to_gpu_mb += step["cpu_to_gpu_mb"]
@@ -259,9 +270,11 @@ class PagedModel:
                 stats.total_cpu_to_gpu_copies += step["cpu_to_gpu_copies"]
                 in_gpu.append(step["attention_in_gpu"])
                 next_input_id = next_token_id
-                current_attention_mask = torch.cat(
-                    [current_attention_mask, current_attention_mask.new_ones((batch_size, 1))], dim=1
-                )
+                position_ids = position_ids + 1
+            if token_ids:
+                generated_per_row: list[list[int]] = torch.cat(token_ids, dim=1).tolist()
+            else:
+                generated_per_row = [[] for _ in range(batch_size)]
             full_sequence = torch.cat(
                 [input_ids, torch.tensor(generated_per_row, dtype=input_ids.dtype, device=input_ids.device)], dim=1
             )
@@ -522,18 +535,28 @@ class PagedModel:
             for m in modules:
                 m._pgr_ctx = None
 
-    def _forward_step(self, input_id_tensor: torch.Tensor, current_attention_mask: torch.Tensor):
+    def _forward_step(self, input_id_tensor: torch.Tensor, current_attention_mask: torch.Tensor | None, *,
+                      position_ids: torch.Tensor | None = None, lo: list[int] | None = None):
         """One token per row through the model over the paged store, then the placement glue
-        (paged_model.py:715-823). Returns (last-position logits [B, V], step stats)."""
+        (paged_model.py:715-823). Returns (last-position logits [B, V], step stats).
+
+        The current token's position ids [B, 1] and, for sliding-window models, each row's
+        first valid column come from current_attention_mask, or from `position_ids` / `lo`
+        when the caller tracks them (generate's loop, which then needs no mask). The step is
+        opened before the position ids are computed: in the mirror stream mode begin_step
+        starts the step's host-to-device copies."""
         dec, sid = self._decoder, self._sid
         _, _, _, _, window = self._model_geometry()
-        position_ids = self._position_ids_from_mask(current_attention_mask)[:, -1:]
         if window is not None:
-            # Valid columns c > current_column - window (the causal mask's sliding-window rule).
-            col = current_attention_mask.shape[1] - 1
-            pads = (current_attention_mask.shape[1] - current_attention_mask.long().sum(dim=1)).tolist()
-            dec.set_lo(sid, [max(p, col - window + 1) for p in pads])
+            if lo is None:
+                # Valid columns c > current_column - window (the causal mask's sliding-window rule).
+                col = current_attention_mask.shape[1] - 1
+                pads = (current_attention_mask.shape[1] - current_attention_mask.long().sum(dim=1)).tolist()
+                lo = [max(p, col - window + 1) for p in pads]
+            dec.set_lo(sid, lo)
         dec.begin_step([sid])
+        if position_ids is None:
+            position_ids = self._position_ids_from_mask(current_attention_mask)[:, -1:]
         host_blocks = dec.pool.step_stats()["host_blocks"]
         try:
             if self.use_hip_graphs:
