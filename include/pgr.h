@@ -168,13 +168,15 @@ typedef struct pgr_kv_config_s {
  * queues layer l+1's copies right after layer l's attention, so that they run under the
  * caller's work between the two layers. */
 /* MIRROR: every layer has an HBM mirror of its host records (HBM: host_records records per
- * layer). pgr_kv_begin_step queues, on the store's side stream, DMA copies of each layer's
- * span of the step's host records into that layer's mirror, and after each layer's copies a
- * word that the layer's attention launch waits for (one lane per workgroup, a bounded wait of
- * ~20 ms): its workgroups then read host blocks from the mirror, or from the host in place if
- * the word is still clear when the wait ends (same data). The copies run beside whatever the
- * caller runs between the step's layers, including a replayed graph of the layers; the next
- * begin_step waits for them. For one long-context session whose host share fits in HBM as a
+ * layer). pgr_kv_begin_step has a host thread of the store queue, on the store's side stream
+ * and behind the work queued on `stream` before begin_step: DMA copies of each layer's span of
+ * the step's host records into that layer's mirror, and after each layer's copies a word that
+ * the layer's attention launch waits for (one lane per workgroup, a bounded wait of ~20 ms).
+ * Its workgroups then read host blocks from the mirror, or from the host in place if the word
+ * is still clear when the wait ends (same data). The copies run beside whatever the caller
+ * runs between the step's layers, including a replayed graph of the layers; the next
+ * begin_step waits for them. pgr_kv_sync and pgr_kv_destroy wait for the thread's queueing
+ * (destroy ends the thread). For one long-context session whose host share fits in HBM as a
  * mirror (a model between layers, e.g. a captured decode step). */
 #define PGR_STREAM_DIRECT 0
 #define PGR_STREAM_STAGED 1
