@@ -494,6 +494,29 @@ def test_mirror_mode_with_and_without_landed_copies(policy):
     assert p.dec.pool.stats()["stream_bytes"] > 0
 
 
+def test_mirror_store_destroyed_while_its_copies_are_queued():
+    """Mirror mode: a store's host thread queues each step's copies after begin_step returns.
+    Stores destroyed right after begin_step (the step left open, its copies possibly still
+    being queued) and right after decode_layer release cleanly, and every store that follows
+    in the process steps in agreement with the oracle."""
+    g = torch.Generator().manual_seed(67)
+    for rnd in range(4):
+        p = Pair(layers=3, hq=8, hkv=2, d=64, tpb=32, dtype=torch.float16, pool_blocks=32, host_blocks=160,
+                 stream_mode="mirror")
+        p.add(ctx=2900 + 37 * rnd, capacity=3100, gen=g, vram_budget=4 * MIB16, ram_budget=1024 * MIB16,
+              recent_window=2, policy="recent_only")
+        for step in range(4):
+            p.step(g, settle=step == 1)
+        assert p.dec.pool.step_stats()["host_blocks"] > 70
+        p.dec.begin_step(p.sids)
+        if rnd % 2:
+            q = (torch.randn(1, 8, 64, generator=g) * 0.5).half().cuda()
+            kv = (torch.randn(1, 2, 64, generator=g) * 0.5).half().cuda()
+            p.dec.decode_layer(0, q, kv, kv)
+        p.dec.pool.close()
+    torch.cuda.synchronize()
+
+
 @pytest.mark.parametrize("mode", ["direct", "staged", "mirror"])
 @pytest.mark.parametrize("d,tpb,window", [(16, 16, 24), (64, 32, 100), (256, 16, 40)])
 def test_per_layer_sliding_windows(d, tpb, window, mode):
