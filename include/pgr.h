@@ -35,7 +35,7 @@ extern "C" {
 
 /* ---- library ------------------------------------------------------------------------- */
 
-/* ABI version of this header (increments when an entry point is added or changed); 7. */
+/* ABI version of this header (increments when an entry point is added or changed); 8. */
 int pgr_abi_version(void);
 /* Message of the last failing call on this thread ("" if none). */
 const char* pgr_last_error(void);
@@ -103,6 +103,11 @@ int pgr_attn_fold_fixed_step(const void* q, const void* k, const void* v, const 
                              const float* l, float* acc, int64_t batch, int64_t num_query_heads, int64_t num_kv_heads,
                              int64_t tokens, int64_t head_dim, int dtype, float scale, float softcap, void* workspace,
                              size_t workspace_bytes, void* stream);
+
+/* Fresh state for rows = B * Hq: m[r] = -inf, l[r] = 0, acc[r, :] = 0 (fp32, contiguous), in
+ * one launch. Replaces streaming_attention_state_init, pager_hf/streaming_attention.py:444-449
+ * (three fills there). */
+int pgr_attn_state_init(float* m, float* l, float* acc, int64_t rows, int64_t head_dim, void* stream);
 
 /* out[r, :] = (acc[r, :] / l[r]) rounded to dtype, for rows = B * Hq.
  * Replaces streaming_attention_finalize, pager_hf/streaming_attention.py:668-670. */

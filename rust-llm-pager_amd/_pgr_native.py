@@ -35,7 +35,7 @@ STREAM_DIRECT = 0
 STREAM_STAGED = 1
 STREAM_MIRROR = 2
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 c_i32, c_i64, c_u8, c_u32, c_u64 = ctypes.c_int32, ctypes.c_int64, ctypes.c_uint8, ctypes.c_uint32, ctypes.c_uint64
 c_f32, c_f64, c_size, c_vp = ctypes.c_float, ctypes.c_double, ctypes.c_size_t, ctypes.c_void_p
@@ -129,6 +129,7 @@ SIGNATURES: dict[str, tuple] = {
         [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_i64, ctypes.c_int, c_f32, c_f32,
          c_vp, c_size, c_vp],
     ),
+    "pgr_attn_state_init": (ctypes.c_int, [c_vp, c_vp, c_vp, c_i64, c_i64, c_vp]),
     "pgr_attn_finalize": (ctypes.c_int, [c_vp, c_vp, c_vp, c_i64, c_i64, ctypes.c_int, c_vp]),
     "pgr_pager_new": (c_vp, [c_u64, c_u64, c_u64, c_u64, c_f32, c_f32, ctypes.c_char_p]),
     "pgr_pager_free": (None, [c_vp]),

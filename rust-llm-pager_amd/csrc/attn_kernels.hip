@@ -718,6 +718,18 @@ __global__ void finalize_f32_kernel(const float* acc, const float* l, float* out
   out[i] = acc[i] / l[i / d];
 }
 
+// Fresh operator state in one launch: m = -inf, l = 0 for `rows` rows, acc = 0 for rows * d.
+__global__ void state_init_kernel(float* m, float* l, float* acc, int64_t rows, int64_t n_acc) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n_acc; i += stride) {
+    acc[i] = 0.f;
+    if (i < rows) {
+      m[i] = kNegInf;
+      l[i] = 0.f;
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------------------
 // Paged kernel: the fused decode path. Blocks are read in place from the layer's HBM
 // pool, from the mapped pinned host mirror, or from a staging buffer filled by
@@ -1488,6 +1500,16 @@ hipError_t launch_finalize(int dtype, const float* acc, const float* l, void* ou
     finalize_kernel<BF16><<<blocks, threads, 0, stream>>>(acc, l, static_cast<uint16_t*>(out), rows, d);
   else
     finalize_f32_kernel<<<blocks, threads, 0, stream>>>(acc, l, static_cast<float*>(out), rows, d);
+  return hipGetLastError();
+}
+
+hipError_t launch_state_init(float* m, float* l, float* acc, int64_t rows, int64_t d, hipStream_t stream) {
+  const int64_t n_acc = rows * d;  // >= rows: d >= 1
+  if (n_acc == 0) return hipSuccess;
+  const int threads = 256;
+  const int64_t want = (n_acc + threads - 1) / threads;
+  const unsigned blocks = (unsigned)(want < 4096 ? want : 4096);
+  state_init_kernel<<<blocks, threads, 0, stream>>>(m, l, acc, rows, n_acc);
   return hipGetLastError();
 }
 

@@ -158,7 +158,7 @@ int kv_rc(pgr::PagedKV* kv, int rc) {
 
 extern "C" {
 
-int pgr_abi_version(void) { return 7; }
+int pgr_abi_version(void) { return 8; }
 
 const char* pgr_last_error(void) { return g_last_error.c_str(); }
 
@@ -233,6 +233,16 @@ int pgr_attn_fold_fixed_step(const void* q, const void* k, const void* v, const 
   return run_dense(PGR_MODE_FOLD_FIXED, q, k, v, valid, nullptr, const_cast<float*>(m), const_cast<float*>(l), acc,
                    nullptr, 0, 0, 16, batch, num_query_heads, num_kv_heads, tokens, head_dim, dtype, scale, softcap,
                    workspace, workspace_bytes, stream);
+}
+
+int pgr_attn_state_init(float* m, float* l, float* acc, int64_t rows, int64_t head_dim, void* stream) {
+  if (rows < 0 || head_dim <= 0) return set_err(pgr::kErrInvalid, "negative or zero dimension");
+  if (rows > ((int64_t)1 << 40) / head_dim) return set_err(pgr::kErrInvalid, "state too large");
+  if (rows == 0) return pgr::kOk;
+  if (!m || !l || !acc) return set_err(pgr::kErrInvalid, "null tensor pointer");
+  hipError_t e = pgr::launch_state_init(m, l, acc, rows, head_dim, as_stream(stream));
+  if (e != hipSuccess) return hip_err(e, "state init launch");
+  return pgr::kOk;
 }
 
 int pgr_attn_finalize(const float* acc, const float* l, void* out, int64_t rows, int64_t head_dim, int dtype,

@@ -99,6 +99,7 @@ int dense_wave_tokens(int dtype, int d, int batch, int hkv, int tc, int tokens_p
 hipError_t launch_dense(int dtype, int mode, int d, const DenseLaunch& p, hipStream_t stream);
 hipError_t launch_finalize(int dtype, const float* acc, const float* l, void* out, int rows, int d,
                            hipStream_t stream);
+hipError_t launch_state_init(float* m, float* l, float* acc, int64_t rows, int64_t d, hipStream_t stream);
 hipError_t launch_paged(int dtype, int d, const PagedLaunch& p, hipStream_t stream);
 hipError_t launch_paged_merge(int dtype, int d, const PagedLaunch& p, int n_seq, hipStream_t stream);
 hipError_t launch_mass_reduce(const SeqInfo* seqs, const int32_t* session_rows, const int32_t* session_first,

@@ -101,10 +101,19 @@ def _workspace(device, batch, hq, hkv, tokens, head_dim, mode, tpb=16):
 
 
 def streaming_attention_state_init(batch_size: int, num_query_heads: int, head_dim: int, device: torch.device):
-    """Fresh online-softmax accumulator state, before any KV chunk has been folded in (:444-449)."""
-    m = torch.full((batch_size, num_query_heads), float("-inf"), dtype=torch.float32, device=device)
-    l = torch.zeros((batch_size, num_query_heads), dtype=torch.float32, device=device)
-    acc = torch.zeros((batch_size, num_query_heads, head_dim), dtype=torch.float32, device=device)
+    """Fresh online-softmax accumulator state, before any KV chunk has been folded in (:444-449):
+    m = -inf, l = 0, acc = 0 in fp32, written by one native launch."""
+    device = torch.device(device)
+    if device.type != "cuda":
+        raise ValueError("streaming attention expects CUDA (HIP) tensors")
+    m = torch.empty((batch_size, num_query_heads), dtype=torch.float32, device=device)
+    l = torch.empty((batch_size, num_query_heads), dtype=torch.float32, device=device)
+    acc = torch.empty((batch_size, num_query_heads, head_dim), dtype=torch.float32, device=device)
+    N.nat.check(
+        N.lib().pgr_attn_state_init(m.data_ptr(), l.data_ptr(), acc.data_ptr(), batch_size * num_query_heads,
+                                    head_dim, N.stream_of(device)),
+        "streaming_attention_state_init",
+    )
     return m, l, acc
 
 

@@ -57,6 +57,25 @@ def max_abs(a, b):
     return (a.float().cpu() - b.float().cpu()).abs().max().item()
 
 
+@pytest.mark.parametrize("b,hq,d", [(0, 14, 64), (1, 14, 64), (3, 7, 8), (64, 128, 256)])
+def test_state_init_values_shapes_and_reuse(b, hq, d):
+    """state_init's one launch writes what the reference's three fills do (m = -inf, l = 0,
+    acc = 0, fp32, contiguous), over memory that held other values (the caching allocator
+    hands the same blocks back), including a grid-strided size of 2M acc elements."""
+    for _ in range(2):
+        junk = torch.full((b * hq * (d + 2) + 4096,), 7.0, device=dev())
+        del junk
+        m, l, acc = streaming_attention_state_init(b, hq, d, dev())
+        assert (m.shape, l.shape, acc.shape) == ((b, hq), (b, hq), (b, hq, d))
+        assert m.dtype == l.dtype == acc.dtype == torch.float32
+        assert m.is_contiguous() and l.is_contiguous() and acc.is_contiguous()
+        torch.cuda.synchronize()
+        assert bool(torch.all(m == float("-inf"))) and bool(torch.all(l == 0)) and bool(torch.all(acc == 0))
+        assert not bool(torch.signbit(acc).any())  # +0.0, as torch.zeros
+    with pytest.raises(ValueError):
+        streaming_attention_state_init(1, hq, d, torch.device("cpu"))
+
+
 # -- the reference's eight tests ---------------------------------------------------------
 
 
