@@ -28,6 +28,7 @@ extern "C" {
 #define PGR_ERR_STATE (-5)
 #define PGR_ERR_KEY (-6)
 #define PGR_ERR_BUDGET (-7)
+#define PGR_ERR_INTERNAL (-8) /* internal failure; no exception crosses this boundary */
 
 #define PGR_DTYPE_F16 0
 #define PGR_DTYPE_BF16 1

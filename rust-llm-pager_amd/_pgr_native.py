@@ -21,6 +21,7 @@ PGR_ERR_CAPACITY = -4
 PGR_ERR_STATE = -5
 PGR_ERR_KEY = -6
 PGR_ERR_BUDGET = -7
+PGR_ERR_INTERNAL = -8
 
 DTYPE_F16 = 0
 DTYPE_BF16 = 1
@@ -222,6 +223,7 @@ _EXC = {
     PGR_ERR_STATE: RuntimeError,
     PGR_ERR_KEY: KeyError,
     PGR_ERR_BUDGET: RuntimeError,
+    PGR_ERR_INTERNAL: RuntimeError,
 }
 
 

@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cmath>
+#include <exception>
 #include <mutex>
 #include <new>
 #include <string>
@@ -147,6 +148,30 @@ int noalloc_scratch(void** out) {
   return pgr::kOk;
 }
 
+// Status for an exception caught at the C boundary (called inside a catch block): none may
+// cross into a C caller, not even one thrown while recording the message.
+int exception_status() noexcept {
+  int code = pgr::kErrInternal;
+  const char* what = nullptr;
+  try {
+    throw;
+  } catch (const std::bad_alloc&) {
+    code = pgr::kErrCapacity;
+  } catch (const std::exception& e) {
+    what = e.what();  // the exception lives until the caller's catch block ends
+  } catch (...) {
+  }
+  try {
+    if (code == pgr::kErrCapacity)
+      g_last_error = "out of host memory";
+    else
+      g_last_error = std::string("internal error") + (what ? std::string(": ") + what : std::string());
+  } catch (...) {
+    g_last_error.clear();
+  }
+  return code;
+}
+
 pgr::PagedKV* kv_of(void* h) { return static_cast<pgr::PagedKV*>(h); }
 
 int kv_rc(pgr::PagedKV* kv, int rc) {
@@ -164,55 +189,72 @@ const char* pgr_last_error(void) { return g_last_error.c_str(); }
 
 size_t pgr_attn_workspace_bytes(int64_t batch, int64_t num_query_heads, int64_t num_kv_heads, int64_t tokens,
                                 int64_t head_dim, int mode, int64_t tokens_per_block) {
-  if (batch <= 0 || num_kv_heads <= 0 || num_query_heads <= 0 || tokens <= 0 || head_dim <= 0) return 0;
-  if (mode == PGR_MODE_ACCUMULATE && (tokens_per_block <= 0 || tokens_per_block % 16 != 0)) return 0;
-  // The geometry depends on the element type only at head dims 32/64/128 (16-bit there runs the
-  // MFMA kernel, fp32 the generic one): the size covers both.
-  const size_t a = plan_dense(batch, num_query_heads, num_kv_heads, tokens, head_dim, mode, tokens_per_block,
-                              pgr::kF16).bytes;
-  const size_t b = plan_dense(batch, num_query_heads, num_kv_heads, tokens, head_dim, mode, tokens_per_block,
-                              pgr::kF32).bytes;
-  return a > b ? a : b;
+  try {
+    if (batch <= 0 || num_kv_heads <= 0 || num_query_heads <= 0 || tokens <= 0 || head_dim <= 0) return 0;
+    if (mode == PGR_MODE_ACCUMULATE && (tokens_per_block <= 0 || tokens_per_block % 16 != 0)) return 0;
+    // The geometry depends on the element type only at head dims 32/64/128 (16-bit there runs the
+    // MFMA kernel, fp32 the generic one): the size covers both.
+    const size_t a = plan_dense(batch, num_query_heads, num_kv_heads, tokens, head_dim, mode, tokens_per_block,
+                                pgr::kF16).bytes;
+    const size_t b = plan_dense(batch, num_query_heads, num_kv_heads, tokens, head_dim, mode, tokens_per_block,
+                                pgr::kF32).bytes;
+    return a > b ? a : b;
+  } catch (...) {
+    exception_status();
+    return 0;
+  }
 }
 
 int pgr_attn_step(const void* q, const void* k, const void* v, const int32_t* valid, const int32_t* active, float* m,
                   float* l, float* acc, int64_t batch, int64_t num_query_heads, int64_t num_kv_heads, int64_t tokens,
                   int64_t head_dim, int dtype, float scale, float softcap, void* workspace, size_t workspace_bytes,
                   void* stream) {
-  return run_dense(PGR_MODE_FOLD, q, k, v, valid, active, m, l, acc, nullptr, 0, 0, 16, batch, num_query_heads,
-                   num_kv_heads, tokens, head_dim, dtype, scale, softcap, workspace, workspace_bytes, stream);
+  try {
+    return run_dense(PGR_MODE_FOLD, q, k, v, valid, active, m, l, acc, nullptr, 0, 0, 16, batch, num_query_heads,
+                     num_kv_heads, tokens, head_dim, dtype, scale, softcap, workspace, workspace_bytes, stream);
+  } catch (...) {
+    return exception_status();
+  }
 }
 
 int pgr_attn_step_noalloc(const void* q, const void* k, const void* v, const int32_t* valid, const int32_t* active,
                           float* m, float* l, float* acc, int64_t batch, int64_t num_query_heads,
                           int64_t num_kv_heads, int64_t tokens, int64_t head_dim, int dtype, float scale,
                           float softcap, void* stream) {
-  int rc = check_dense(batch, num_query_heads, num_kv_heads, tokens, head_dim, dtype, scale);
-  if (rc != pgr::kOk) return rc;
-  if (tokens == 0 || batch == 0) return pgr::kOk;
-  // Every partial slot that the merge reads is written by the fold launch before it (a row
-  // with active = 0 is skipped by both), so nothing left in `scratch` by an earlier call is
-  // read and nothing needs clearing.
-  const size_t need =
-      plan_dense(batch, num_query_heads, num_kv_heads, tokens, head_dim, PGR_MODE_FOLD, 16, dtype).bytes;
-  if (need > kNoAllocScratchBytes)
-    return set_err(pgr::kErrCapacity, "pgr_attn_step_noalloc: this chunk needs " + std::to_string(need) +
-                                          " bytes of split-K partials, more than the " +
-                                          std::to_string(kNoAllocScratchBytes) +
-                                          "-byte static scratch; use pgr_attn_step with a workspace");
-  void* ws = nullptr;
-  rc = noalloc_scratch(&ws);
-  if (rc != pgr::kOk) return rc;
-  return run_dense(PGR_MODE_FOLD, q, k, v, valid, active, m, l, acc, nullptr, 0, 0, 16, batch, num_query_heads,
-                   num_kv_heads, tokens, head_dim, dtype, scale, softcap, ws, kNoAllocScratchBytes, stream);
+  try {
+    int rc = check_dense(batch, num_query_heads, num_kv_heads, tokens, head_dim, dtype, scale);
+    if (rc != pgr::kOk) return rc;
+    if (tokens == 0 || batch == 0) return pgr::kOk;
+    // Every partial slot that the merge reads is written by the fold launch before it (a row
+    // with active = 0 is skipped by both), so nothing left in `scratch` by an earlier call is
+    // read and nothing needs clearing.
+    const size_t need =
+        plan_dense(batch, num_query_heads, num_kv_heads, tokens, head_dim, PGR_MODE_FOLD, 16, dtype).bytes;
+    if (need > kNoAllocScratchBytes)
+      return set_err(pgr::kErrCapacity, "pgr_attn_step_noalloc: this chunk needs " + std::to_string(need) +
+                                            " bytes of split-K partials, more than the " +
+                                            std::to_string(kNoAllocScratchBytes) +
+                                            "-byte static scratch; use pgr_attn_step with a workspace");
+    void* ws = nullptr;
+    rc = noalloc_scratch(&ws);
+    if (rc != pgr::kOk) return rc;
+    return run_dense(PGR_MODE_FOLD, q, k, v, valid, active, m, l, acc, nullptr, 0, 0, 16, batch, num_query_heads,
+                     num_kv_heads, tokens, head_dim, dtype, scale, softcap, ws, kNoAllocScratchBytes, stream);
+  } catch (...) {
+    return exception_status();
+  }
 }
 
 int pgr_attn_stats_step(const void* q, const void* k, const int32_t* valid, const int32_t* active, float* m, float* l,
                         int64_t batch, int64_t num_query_heads, int64_t num_kv_heads, int64_t tokens, int64_t head_dim,
                         int dtype, float scale, float softcap, void* workspace, size_t workspace_bytes, void* stream) {
-  return run_dense(PGR_MODE_STATS, q, k, nullptr, valid, active, m, l, nullptr, nullptr, 0, 0, 16, batch,
-                   num_query_heads, num_kv_heads, tokens, head_dim, dtype, scale, softcap, workspace, workspace_bytes,
-                   stream);
+  try {
+    return run_dense(PGR_MODE_STATS, q, k, nullptr, valid, active, m, l, nullptr, nullptr, 0, 0, 16, batch,
+                     num_query_heads, num_kv_heads, tokens, head_dim, dtype, scale, softcap, workspace, workspace_bytes,
+                     stream);
+  } catch (...) {
+    return exception_status();
+  }
 }
 
 int pgr_attn_accumulate_step(const void* q, const void* k, const void* v, const int32_t* valid, const int32_t* active,
@@ -221,330 +263,490 @@ int pgr_attn_accumulate_step(const void* q, const void* k, const void* v, const 
                              int64_t num_query_heads, int64_t num_kv_heads, int64_t tokens, int64_t head_dim,
                              int dtype, float scale, float softcap, void* workspace, size_t workspace_bytes,
                              void* stream) {
-  return run_dense(PGR_MODE_ACCUMULATE, q, k, v, valid, active, const_cast<float*>(m), const_cast<float*>(l), acc,
-                   block_mass, max_blocks, block_id_offset, tokens_per_block, batch, num_query_heads, num_kv_heads,
-                   tokens, head_dim, dtype, scale, softcap, workspace, workspace_bytes, stream);
+  try {
+    return run_dense(PGR_MODE_ACCUMULATE, q, k, v, valid, active, const_cast<float*>(m), const_cast<float*>(l), acc,
+                     block_mass, max_blocks, block_id_offset, tokens_per_block, batch, num_query_heads, num_kv_heads,
+                     tokens, head_dim, dtype, scale, softcap, workspace, workspace_bytes, stream);
+  } catch (...) {
+    return exception_status();
+  }
 }
 
 int pgr_attn_fold_fixed_step(const void* q, const void* k, const void* v, const int32_t* valid, const float* m,
                              const float* l, float* acc, int64_t batch, int64_t num_query_heads, int64_t num_kv_heads,
                              int64_t tokens, int64_t head_dim, int dtype, float scale, float softcap, void* workspace,
                              size_t workspace_bytes, void* stream) {
-  return run_dense(PGR_MODE_FOLD_FIXED, q, k, v, valid, nullptr, const_cast<float*>(m), const_cast<float*>(l), acc,
-                   nullptr, 0, 0, 16, batch, num_query_heads, num_kv_heads, tokens, head_dim, dtype, scale, softcap,
-                   workspace, workspace_bytes, stream);
+  try {
+    return run_dense(PGR_MODE_FOLD_FIXED, q, k, v, valid, nullptr, const_cast<float*>(m), const_cast<float*>(l), acc,
+                     nullptr, 0, 0, 16, batch, num_query_heads, num_kv_heads, tokens, head_dim, dtype, scale, softcap,
+                     workspace, workspace_bytes, stream);
+  } catch (...) {
+    return exception_status();
+  }
 }
 
 int pgr_attn_state_init(float* m, float* l, float* acc, int64_t rows, int64_t head_dim, void* stream) {
-  if (rows < 0 || head_dim <= 0) return set_err(pgr::kErrInvalid, "negative or zero dimension");
-  if (rows > ((int64_t)1 << 40) / head_dim) return set_err(pgr::kErrInvalid, "state too large");
-  if (rows == 0) return pgr::kOk;
-  if (!m || !l || !acc) return set_err(pgr::kErrInvalid, "null tensor pointer");
-  hipError_t e = pgr::launch_state_init(m, l, acc, rows, head_dim, as_stream(stream));
-  if (e != hipSuccess) return hip_err(e, "state init launch");
-  return pgr::kOk;
+  try {
+    if (rows < 0 || head_dim <= 0) return set_err(pgr::kErrInvalid, "negative or zero dimension");
+    if (rows > ((int64_t)1 << 40) / head_dim) return set_err(pgr::kErrInvalid, "state too large");
+    if (rows == 0) return pgr::kOk;
+    if (!m || !l || !acc) return set_err(pgr::kErrInvalid, "null tensor pointer");
+    hipError_t e = pgr::launch_state_init(m, l, acc, rows, head_dim, as_stream(stream));
+    if (e != hipSuccess) return hip_err(e, "state init launch");
+    return pgr::kOk;
+  } catch (...) {
+    return exception_status();
+  }
 }
 
 int pgr_attn_finalize(const float* acc, const float* l, void* out, int64_t rows, int64_t head_dim, int dtype,
                       void* stream) {
-  if (rows < 0 || head_dim <= 0) return set_err(pgr::kErrInvalid, "negative or zero dimension");
-  if (dtype != pgr::kF16 && dtype != pgr::kBF16 && dtype != PGR_DTYPE_F32)
-    return set_err(pgr::kErrInvalid, "dtype must be fp16, bf16 or fp32");
-  if (rows == 0) return pgr::kOk;
-  if (!acc || !l || !out) return set_err(pgr::kErrInvalid, "null tensor pointer");
-  hipError_t e = pgr::launch_finalize(dtype, acc, l, out, (int)rows, (int)head_dim, as_stream(stream));
-  if (e != hipSuccess) return hip_err(e, "finalize launch");
-  return pgr::kOk;
+  try {
+    if (rows < 0 || head_dim <= 0) return set_err(pgr::kErrInvalid, "negative or zero dimension");
+    if (dtype != pgr::kF16 && dtype != pgr::kBF16 && dtype != PGR_DTYPE_F32)
+      return set_err(pgr::kErrInvalid, "dtype must be fp16, bf16 or fp32");
+    if (rows == 0) return pgr::kOk;
+    if (!acc || !l || !out) return set_err(pgr::kErrInvalid, "null tensor pointer");
+    hipError_t e = pgr::launch_finalize(dtype, acc, l, out, (int)rows, (int)head_dim, as_stream(stream));
+    if (e != hipSuccess) return hip_err(e, "finalize launch");
+    return pgr::kOk;
+  } catch (...) {
+    return exception_status();
+  }
 }
 
 // ---- placement -----------------------------------------------------------------------
 
 void* pgr_pager_new(uint64_t vram, uint64_t ram, uint64_t recent, uint64_t rebalance_interval, float promote_margin,
                     float ram_promote_margin, const char* policy) {
-  const std::string name = policy ? policy : "heavy_hitter";
-  return new (std::nothrow) pgr::PlacementPager(vram, ram, recent, rebalance_interval, promote_margin,
-                                                ram_promote_margin, pgr::policy_from_name(name));
+  try {
+    const std::string name = policy ? policy : "heavy_hitter";
+    return new (std::nothrow) pgr::PlacementPager(vram, ram, recent, rebalance_interval, promote_margin,
+                                                  ram_promote_margin, pgr::policy_from_name(name));
+  } catch (...) {
+    exception_status();
+    return nullptr;
+  }
 }
 
 void pgr_pager_free(void* pager) { delete static_cast<pgr::PlacementPager*>(pager); }
 
 int pgr_pager_on_step(void* pager, uint64_t token_idx, uint32_t layer, const float* attention, size_t n) {
-  (void)layer;
-  if (!pager || (n && !attention)) return set_err(pgr::kErrInvalid, "null pointer");
-  if (n > ((size_t)1 << 31)) return set_err(pgr::kErrInvalid, "attention vector too long");
-  if (!static_cast<pgr::PlacementPager*>(pager)->on_step(token_idx, attention, n))
-    return set_err(pgr::kErrState, "attempt to calculate the remainder with a divisor of zero");
-  return pgr::kOk;
+  try {
+    (void)layer;
+    if (!pager || (n && !attention)) return set_err(pgr::kErrInvalid, "null pointer");
+    if (n > ((size_t)1 << 31)) return set_err(pgr::kErrInvalid, "attention vector too long");
+    if (!static_cast<pgr::PlacementPager*>(pager)->on_step(token_idx, attention, n))
+      return set_err(pgr::kErrState, "attempt to calculate the remainder with a divisor of zero");
+    return pgr::kOk;
+  } catch (...) {
+    exception_status();
+  }
 }
 
 int pgr_pager_force_rebalance(void* pager, uint64_t token_idx) {
-  if (!pager) return set_err(pgr::kErrInvalid, "null pager");
-  if (token_idx >= ((uint64_t)1 << 31)) return set_err(pgr::kErrInvalid, "token_idx too large for the block table");
-  static_cast<pgr::PlacementPager*>(pager)->force_rebalance(token_idx);
-  return pgr::kOk;
+  try {
+    if (!pager) return set_err(pgr::kErrInvalid, "null pager");
+    if (token_idx >= ((uint64_t)1 << 31)) return set_err(pgr::kErrInvalid, "token_idx too large for the block table");
+    static_cast<pgr::PlacementPager*>(pager)->force_rebalance(token_idx);
+    return pgr::kOk;
+  } catch (...) {
+    return exception_status();
+  }
 }
 
 size_t pgr_pager_num_blocks(void* pager) { return pager ? static_cast<pgr::PlacementPager*>(pager)->num_blocks() : 0; }
 
 size_t pgr_pager_tiers(void* pager, uint8_t* out, size_t cap) {
-  if (!pager) return 0;
-  auto* p = static_cast<pgr::PlacementPager*>(pager);
-  const size_t n = p->num_blocks();
-  if (out && cap >= n) p->tiers(out);
-  return n;
+  try {
+    if (!pager) return 0;
+    auto* p = static_cast<pgr::PlacementPager*>(pager);
+    const size_t n = p->num_blocks();
+    if (out && cap >= n) p->tiers(out);
+    return n;
+  } catch (...) {
+    exception_status();
+    return 0;
+  }
 }
 
 size_t pgr_pager_vram_block_ids(void* pager, uint64_t* out, size_t cap) {
-  if (!pager) return 0;
-  auto* p = static_cast<pgr::PlacementPager*>(pager);
-  const size_t n = p->vram_count();
-  if (out && cap >= n) p->vram_block_ids(out);
-  return n;
+  try {
+    if (!pager) return 0;
+    auto* p = static_cast<pgr::PlacementPager*>(pager);
+    const size_t n = p->vram_count();
+    if (out && cap >= n) p->vram_block_ids(out);
+    return n;
+  } catch (...) {
+    exception_status();
+    return 0;
+  }
 }
 
 int pgr_pager_metrics(void* pager, pgr_pager_metrics_t* out) {
-  if (!pager || !out) return set_err(pgr::kErrInvalid, "null pointer");
-  const pgr::PagerMetrics& m = static_cast<pgr::PlacementPager*>(pager)->metrics();
-  out->tokens = m.tokens;
-  out->vram_peak = m.vram_peak;
-  out->ram_peak = m.ram_peak;
-  out->swap_vram_ram = m.swap_vram_ram;
-  out->swap_ram_ssd = m.swap_ram_ssd;
-  out->attention_mass_total = m.attention_mass_total;
-  out->attention_mass_vram = m.attention_mass_vram;
-  return pgr::kOk;
+  try {
+    if (!pager || !out) return set_err(pgr::kErrInvalid, "null pointer");
+    const pgr::PagerMetrics& m = static_cast<pgr::PlacementPager*>(pager)->metrics();
+    out->tokens = m.tokens;
+    out->vram_peak = m.vram_peak;
+    out->ram_peak = m.ram_peak;
+    out->swap_vram_ram = m.swap_vram_ram;
+    out->swap_ram_ssd = m.swap_ram_ssd;
+    out->attention_mass_total = m.attention_mass_total;
+    out->attention_mass_vram = m.attention_mass_vram;
+    return pgr::kOk;
+  } catch (...) {
+    return exception_status();
+  }
 }
 
 // ---- paged KV store -------------------------------------------------------------------
 
 void* pgr_kv_create(const pgr_kv_config_t* c) {
-  if (!c) {
-    set_err(pgr::kErrInvalid, "null config");
+  try {
+    if (!c) {
+      set_err(pgr::kErrInvalid, "null config");
+      return nullptr;
+    }
+    pgr::PagedKVConfig cfg;
+    cfg.num_layers = c->num_layers;
+    cfg.kv_heads = c->kv_heads;
+    cfg.query_heads = c->query_heads;
+    cfg.head_dim = c->head_dim;
+    cfg.tokens_per_block = c->tokens_per_block;
+    cfg.dtype = c->dtype;
+    cfg.pool_slots = c->pool_slots;
+    cfg.host_records = c->host_records;
+    cfg.staging_slots = c->staging_slots;
+    cfg.staging_buffers = c->staging_buffers;
+    cfg.blocks_per_workgroup = c->blocks_per_workgroup > 0 ? c->blocks_per_workgroup : 32;
+    cfg.target_workgroups = c->target_workgroups > 0 ? c->target_workgroups : 0;
+    cfg.stream_mode = c->stream_mode;
+    auto* kv = new (std::nothrow) pgr::PagedKV(cfg);
+    if (!kv) {
+      set_err(pgr::kErrCapacity, "out of host memory");
+      return nullptr;
+    }
+    const int rc = kv->init();
+    if (rc != pgr::kOk) {
+      g_last_error = kv->error();
+      delete kv;
+      return nullptr;
+    }
+    return kv;
+  } catch (...) {
+    exception_status();
     return nullptr;
   }
-  pgr::PagedKVConfig cfg;
-  cfg.num_layers = c->num_layers;
-  cfg.kv_heads = c->kv_heads;
-  cfg.query_heads = c->query_heads;
-  cfg.head_dim = c->head_dim;
-  cfg.tokens_per_block = c->tokens_per_block;
-  cfg.dtype = c->dtype;
-  cfg.pool_slots = c->pool_slots;
-  cfg.host_records = c->host_records;
-  cfg.staging_slots = c->staging_slots;
-  cfg.staging_buffers = c->staging_buffers;
-  cfg.blocks_per_workgroup = c->blocks_per_workgroup > 0 ? c->blocks_per_workgroup : 32;
-  cfg.target_workgroups = c->target_workgroups > 0 ? c->target_workgroups : 0;
-  cfg.stream_mode = c->stream_mode;
-  auto* kv = new (std::nothrow) pgr::PagedKV(cfg);
-  if (!kv) {
-    set_err(pgr::kErrCapacity, "out of host memory");
-    return nullptr;
-  }
-  const int rc = kv->init();
-  if (rc != pgr::kOk) {
-    g_last_error = kv->error();
-    delete kv;
-    return nullptr;
-  }
-  return kv;
 }
 
 void pgr_kv_destroy(void* kv) { delete kv_of(kv); }
 
 int pgr_kv_add_session(void* kv, int32_t rows, int64_t capacity_tokens, const int32_t* lo_per_row) {
-  if (!kv) return set_err(pgr::kErrInvalid, "null store");
-  return kv_rc(kv_of(kv), kv_of(kv)->add_session(rows, capacity_tokens, lo_per_row));
+  try {
+    if (!kv) return set_err(pgr::kErrInvalid, "null store");
+    return kv_rc(kv_of(kv), kv_of(kv)->add_session(rows, capacity_tokens, lo_per_row));
+  } catch (...) {
+    exception_status();
+  }
 }
 
 int pgr_kv_remove_session(void* kv, int32_t sid) {
-  if (!kv) return set_err(pgr::kErrInvalid, "null store");
-  return kv_rc(kv_of(kv), kv_of(kv)->remove_session(sid));
+  try {
+    if (!kv) return set_err(pgr::kErrInvalid, "null store");
+    return kv_rc(kv_of(kv), kv_of(kv)->remove_session(sid));
+  } catch (...) {
+    return exception_status();
+  }
 }
 
 int pgr_kv_set_lo(void* kv, int32_t sid, const int32_t* lo_per_row) {
-  if (!kv || !lo_per_row) return set_err(pgr::kErrInvalid, "null pointer");
-  return kv_rc(kv_of(kv), kv_of(kv)->set_lo(sid, lo_per_row));
+  try {
+    if (!kv || !lo_per_row) return set_err(pgr::kErrInvalid, "null pointer");
+    return kv_rc(kv_of(kv), kv_of(kv)->set_lo(sid, lo_per_row));
+  } catch (...) {
+    return exception_status();
+  }
 }
 
 int pgr_kv_reorder_rows(void* kv, int32_t sid, const int32_t* src_rows, int32_t n_rows, void* stream) {
-  if (!kv || !src_rows) return set_err(pgr::kErrInvalid, "null pointer");
-  return kv_rc(kv_of(kv), kv_of(kv)->reorder_rows(sid, src_rows, n_rows, as_stream(stream)));
+  try {
+    if (!kv || !src_rows) return set_err(pgr::kErrInvalid, "null pointer");
+    return kv_rc(kv_of(kv), kv_of(kv)->reorder_rows(sid, src_rows, n_rows, as_stream(stream)));
+  } catch (...) {
+    return exception_status();
+  }
 }
 
 int pgr_kv_set_length(void* kv, int32_t sid, int64_t n_tokens) {
-  if (!kv) return set_err(pgr::kErrInvalid, "null store");
-  return kv_rc(kv_of(kv), kv_of(kv)->set_length(sid, n_tokens));
+  try {
+    if (!kv) return set_err(pgr::kErrInvalid, "null store");
+    return kv_rc(kv_of(kv), kv_of(kv)->set_length(sid, n_tokens));
+  } catch (...) {
+    return exception_status();
+  }
 }
 
 int pgr_kv_import(void* kv, int32_t sid, int32_t row, int32_t layer, const void* k, const void* v, int64_t n_src,
                   int64_t n_tokens, void* stream) {
-  if (!kv || !k || !v) return set_err(pgr::kErrInvalid, "null pointer");
-  return kv_rc(kv_of(kv), kv_of(kv)->import_tokens(sid, row, layer, k, v, n_src, n_tokens, as_stream(stream)));
+  try {
+    if (!kv || !k || !v) return set_err(pgr::kErrInvalid, "null pointer");
+    return kv_rc(kv_of(kv), kv_of(kv)->import_tokens(sid, row, layer, k, v, n_src, n_tokens, as_stream(stream)));
+  } catch (...) {
+    return exception_status();
+  }
 }
 
 int pgr_kv_export(void* kv, int32_t sid, int32_t row, int32_t layer, void* k, void* v, int64_t n_tokens,
                   void* stream) {
-  if (!kv || !k || !v) return set_err(pgr::kErrInvalid, "null pointer");
-  return kv_rc(kv_of(kv), kv_of(kv)->export_tokens(sid, row, layer, k, v, n_tokens, as_stream(stream)));
+  try {
+    if (!kv || !k || !v) return set_err(pgr::kErrInvalid, "null pointer");
+    return kv_rc(kv_of(kv), kv_of(kv)->export_tokens(sid, row, layer, k, v, n_tokens, as_stream(stream)));
+  } catch (...) {
+    return exception_status();
+  }
 }
 
 int pgr_kv_put_block(void* kv, int32_t sid, int64_t block_id, const void* key, const void* value, void* stream) {
-  if (!kv || !key || !value) return set_err(pgr::kErrInvalid, "null pointer");
-  return kv_rc(kv_of(kv), kv_of(kv)->put_block(sid, block_id, key, value, as_stream(stream)));
+  try {
+    if (!kv || !key || !value) return set_err(pgr::kErrInvalid, "null pointer");
+    return kv_rc(kv_of(kv), kv_of(kv)->put_block(sid, block_id, key, value, as_stream(stream)));
+  } catch (...) {
+    return exception_status();
+  }
 }
 
 int pgr_kv_get_block(void* kv, int32_t sid, int64_t block_id, void* key, void* value, void* stream) {
-  if (!kv || !key || !value) return set_err(pgr::kErrInvalid, "null pointer");
-  return kv_rc(kv_of(kv), kv_of(kv)->get_block(sid, block_id, key, value, as_stream(stream)));
+  try {
+    if (!kv || !key || !value) return set_err(pgr::kErrInvalid, "null pointer");
+    return kv_rc(kv_of(kv), kv_of(kv)->get_block(sid, block_id, key, value, as_stream(stream)));
+  } catch (...) {
+    return exception_status();
+  }
 }
 
 int pgr_kv_apply_tiers(void* kv, int32_t sid, const uint8_t* tiers, int64_t n_tiers, int64_t* to_gpu, int64_t* n_gpu,
                        int64_t* to_cpu, int64_t* n_cpu, int64_t* fail_block, void* stream) {
-  if (!kv || (n_tiers && !tiers) || !to_gpu || !n_gpu || !to_cpu || !n_cpu || !fail_block)
-    return set_err(pgr::kErrInvalid, "null pointer");
-  return kv_rc(kv_of(kv), kv_of(kv)->apply_tiers(sid, tiers, n_tiers, to_gpu, n_gpu, to_cpu, n_cpu, fail_block,
-                                                 as_stream(stream)));
+  try {
+    if (!kv || (n_tiers && !tiers) || !to_gpu || !n_gpu || !to_cpu || !n_cpu || !fail_block)
+      return set_err(pgr::kErrInvalid, "null pointer");
+    return kv_rc(kv_of(kv), kv_of(kv)->apply_tiers(sid, tiers, n_tiers, to_gpu, n_gpu, to_cpu, n_cpu, fail_block,
+                                                   as_stream(stream)));
+  } catch (...) {
+    return exception_status();
+  }
 }
 
 int pgr_kv_set_ram_budget(void* kv, int64_t bytes) {
-  if (!kv) return set_err(pgr::kErrInvalid, "null store");
-  kv_of(kv)->set_ram_budget(bytes);
-  return pgr::kOk;
+  try {
+    if (!kv) return set_err(pgr::kErrInvalid, "null store");
+    kv_of(kv)->set_ram_budget(bytes);
+    return pgr::kOk;
+  } catch (...) {
+    return exception_status();
+  }
 }
 
 int pgr_kv_begin_step(void* kv, const int32_t* sids, int32_t n, void* stream) {
-  if (!kv || (n && !sids) || n < 0) return set_err(pgr::kErrInvalid, "null pointer or negative count");
-  return kv_rc(kv_of(kv), kv_of(kv)->begin_step(sids, n, as_stream(stream)));
+  try {
+    if (!kv || (n && !sids) || n < 0) return set_err(pgr::kErrInvalid, "null pointer or negative count");
+    return kv_rc(kv_of(kv), kv_of(kv)->begin_step(sids, n, as_stream(stream)));
+  } catch (...) {
+    return exception_status();
+  }
 }
 
 int pgr_kv_decode_layer(void* kv, int32_t layer, const void* q, const void* k_new, const void* v_new, void* out,
                         float* mass_accum, int64_t accum_stride, float scale, float softcap, int32_t window,
                         void* stream) {
-  if (!kv || !q || !k_new || !v_new || !out) return set_err(pgr::kErrInvalid, "null pointer");
-  if (!(scale > 0.f) || !std::isfinite(scale)) return set_err(pgr::kErrInvalid, "scale must be positive and finite");
-  return kv_rc(kv_of(kv), kv_of(kv)->decode_layer(layer, q, k_new, v_new, out, mass_accum, accum_stride, scale,
-                                                  softcap > 0.f ? softcap : 0.f, window > 0 ? window : 0,
-                                                  as_stream(stream)));
+  try {
+    if (!kv || !q || !k_new || !v_new || !out) return set_err(pgr::kErrInvalid, "null pointer");
+    if (!(scale > 0.f) || !std::isfinite(scale)) return set_err(pgr::kErrInvalid, "scale must be positive and finite");
+    return kv_rc(kv_of(kv), kv_of(kv)->decode_layer(layer, q, k_new, v_new, out, mass_accum, accum_stride, scale,
+                                                    softcap > 0.f ? softcap : 0.f, window > 0 ? window : 0,
+                                                    as_stream(stream)));
+  } catch (...) {
+    return exception_status();
+  }
 }
 
 int pgr_kv_step_signature(void* kv, int64_t* out, int64_t cap) {
-  if (!kv || (cap && !out)) return set_err(pgr::kErrInvalid, "null pointer");
-  const int rc = kv_of(kv)->step_signature(out, cap);
-  if (rc < 0) return set_err(rc, "step_signature outside a decode step");
-  return rc;
+  try {
+    if (!kv || (cap && !out)) return set_err(pgr::kErrInvalid, "null pointer");
+    const int rc = kv_of(kv)->step_signature(out, cap);
+    if (rc < 0) return set_err(rc, "step_signature outside a decode step");
+    return rc;
+  } catch (...) {
+    return exception_status();
+  }
 }
 
 int pgr_kv_step_replayed(void* kv, void* stream) {
-  if (!kv) return set_err(pgr::kErrInvalid, "null store");
-  return kv_rc(kv_of(kv), kv_of(kv)->step_replayed(as_stream(stream)));
+  try {
+    if (!kv) return set_err(pgr::kErrInvalid, "null store");
+    return kv_rc(kv_of(kv), kv_of(kv)->step_replayed(as_stream(stream)));
+  } catch (...) {
+    return exception_status();
+  }
 }
 
 int pgr_kv_end_step(void* kv, int32_t* completed, int32_t* n_completed) {
-  if (!kv) return set_err(pgr::kErrInvalid, "null store");
-  int c = 0;
-  const int rc = kv_of(kv)->end_step(completed, &c);
-  if (n_completed) *n_completed = c;
-  return kv_rc(kv_of(kv), rc);
+  try {
+    if (!kv) return set_err(pgr::kErrInvalid, "null store");
+    int c = 0;
+    const int rc = kv_of(kv)->end_step(completed, &c);
+    if (n_completed) *n_completed = c;
+    return kv_rc(kv_of(kv), rc);
+  } catch (...) {
+    return exception_status();
+  }
 }
 
 int pgr_kv_attach_pager(void* kv, int32_t sid, void* pager, int32_t scores_from_mass) {
-  if (!kv) return set_err(pgr::kErrInvalid, "null store");
-  return kv_rc(kv_of(kv), kv_of(kv)->attach_pager(sid, static_cast<pgr::PlacementPager*>(pager), scores_from_mass));
+  try {
+    if (!kv) return set_err(pgr::kErrInvalid, "null store");
+    return kv_rc(kv_of(kv), kv_of(kv)->attach_pager(sid, static_cast<pgr::PlacementPager*>(pager), scores_from_mass));
+  } catch (...) {
+    return exception_status();
+  }
 }
 
 int pgr_kv_end_step_place(void* kv, const float* mass_accum, int64_t accum_stride, int32_t num_layers,
                           int32_t* completed, int32_t* n_completed, int64_t* counts, int64_t* moves,
                           int64_t moves_cap, double* scores, int64_t scores_cap, void* stream) {
-  if (!kv) return set_err(pgr::kErrInvalid, "null store");
-  if (num_layers <= 0) return set_err(pgr::kErrInvalid, "num_layers must be positive");
-  int c = 0;
-  const int rc = kv_of(kv)->end_step_place(mass_accum, accum_stride, num_layers, as_stream(stream), completed, &c,
-                                           counts, moves, moves_cap, scores, scores_cap);
-  if (n_completed) *n_completed = c;
-  return kv_rc(kv_of(kv), rc);
+  try {
+    if (!kv) return set_err(pgr::kErrInvalid, "null store");
+    if (num_layers <= 0) return set_err(pgr::kErrInvalid, "num_layers must be positive");
+    int c = 0;
+    const int rc = kv_of(kv)->end_step_place(mass_accum, accum_stride, num_layers, as_stream(stream), completed, &c,
+                                             counts, moves, moves_cap, scores, scores_cap);
+    if (n_completed) *n_completed = c;
+    return kv_rc(kv_of(kv), rc);
+  } catch (...) {
+    return exception_status();
+  }
 }
 
 int pgr_kv_session_info(void* kv, int32_t sid, int64_t* info) {
-  if (!kv || !info) return set_err(pgr::kErrInvalid, "null pointer");
-  const int rc = kv_of(kv)->session_info(sid, &info[0], &info[1], &info[2], &info[3]);
-  if (rc != pgr::kOk) return set_err(rc, "unknown session");
-  return rc;
+  try {
+    if (!kv || !info) return set_err(pgr::kErrInvalid, "null pointer");
+    const int rc = kv_of(kv)->session_info(sid, &info[0], &info[1], &info[2], &info[3]);
+    if (rc != pgr::kOk) return set_err(rc, "unknown session");
+    return rc;
+  } catch (...) {
+    return exception_status();
+  }
 }
 
 int pgr_kv_block_ids(void* kv, int32_t sid, int32_t gpu, int64_t* out, int64_t cap) {
-  if (!kv || (cap && !out)) return set_err(pgr::kErrInvalid, "null pointer");
-  const int rc = kv_of(kv)->block_ids(sid, gpu, out, cap);
-  if (rc < 0) return set_err(rc, "unknown session");
-  return rc;
+  try {
+    if (!kv || (cap && !out)) return set_err(pgr::kErrInvalid, "null pointer");
+    const int rc = kv_of(kv)->block_ids(sid, gpu, out, cap);
+    if (rc < 0) return set_err(rc, "unknown session");
+    return rc;
+  } catch (...) {
+    return exception_status();
+  }
 }
 
 int pgr_kv_step_host_blocks(void* kv, int32_t seq, int64_t* out, int64_t cap) {
-  if (!kv || (cap && !out)) return set_err(pgr::kErrInvalid, "null pointer");
-  const int rc = kv_of(kv)->step_host_blocks(seq, out, cap);
-  if (rc < 0) return set_err(rc, "no such sequence in the last step");
-  return rc;
+  try {
+    if (!kv || (cap && !out)) return set_err(pgr::kErrInvalid, "null pointer");
+    const int rc = kv_of(kv)->step_host_blocks(seq, out, cap);
+    if (rc < 0) return set_err(rc, "no such sequence in the last step");
+    return rc;
+  } catch (...) {
+    return exception_status();
+  }
 }
 
 int pgr_kv_step_stats(void* kv, pgr_kv_step_stats_t* out) {
-  if (!kv || !out) return set_err(pgr::kErrInvalid, "null pointer");
-  const pgr::StepStats& s = kv_of(kv)->step_stats();
-  out->resident_tokens = s.resident_tokens;
-  out->host_tokens = s.host_tokens;
-  out->host_blocks = s.host_blocks;
-  out->copies = s.copies;
-  out->chunks = s.chunks;
-  out->launches = s.launches;
-  out->work_items = s.work_items;
-  return pgr::kOk;
+  try {
+    if (!kv || !out) return set_err(pgr::kErrInvalid, "null pointer");
+    const pgr::StepStats& s = kv_of(kv)->step_stats();
+    out->resident_tokens = s.resident_tokens;
+    out->host_tokens = s.host_tokens;
+    out->host_blocks = s.host_blocks;
+    out->copies = s.copies;
+    out->chunks = s.chunks;
+    out->launches = s.launches;
+    out->work_items = s.work_items;
+    return pgr::kOk;
+  } catch (...) {
+    return exception_status();
+  }
 }
 
 int pgr_kv_stats(void* kv, pgr_kv_stats_t* out) {
-  if (!kv || !out) return set_err(pgr::kErrInvalid, "null pointer");
-  const pgr::StoreStats s = kv_of(kv)->stats();
-  out->gpu_to_cpu_bytes = s.gpu_to_cpu_bytes;
-  out->cpu_to_gpu_bytes = s.cpu_to_gpu_bytes;
-  out->gpu_to_cpu_copies = s.gpu_to_cpu_copies;
-  out->cpu_to_gpu_copies = s.cpu_to_gpu_copies;
-  out->gpu_to_cpu_sec = s.gpu_to_cpu_sec;
-  out->cpu_to_gpu_sec = s.cpu_to_gpu_sec;
-  out->evict_bytes_copied = s.evict_bytes_copied;
-  out->load_bytes_copied = s.load_bytes_copied;
-  out->stream_bytes = s.stream_bytes;
-  out->stream_copies = s.stream_copies;
-  return pgr::kOk;
+  try {
+    if (!kv || !out) return set_err(pgr::kErrInvalid, "null pointer");
+    const pgr::StoreStats s = kv_of(kv)->stats();
+    out->gpu_to_cpu_bytes = s.gpu_to_cpu_bytes;
+    out->cpu_to_gpu_bytes = s.cpu_to_gpu_bytes;
+    out->gpu_to_cpu_copies = s.gpu_to_cpu_copies;
+    out->cpu_to_gpu_copies = s.cpu_to_gpu_copies;
+    out->gpu_to_cpu_sec = s.gpu_to_cpu_sec;
+    out->cpu_to_gpu_sec = s.cpu_to_gpu_sec;
+    out->evict_bytes_copied = s.evict_bytes_copied;
+    out->load_bytes_copied = s.load_bytes_copied;
+    out->stream_bytes = s.stream_bytes;
+    out->stream_copies = s.stream_copies;
+    return pgr::kOk;
+  } catch (...) {
+    return exception_status();
+  }
 }
 
 int pgr_kv_resident_bytes(void* kv, int64_t* gpu, int64_t* cpu) {
-  if (!kv || !gpu || !cpu) return set_err(pgr::kErrInvalid, "null pointer");
-  *gpu = kv_of(kv)->resident_gpu_bytes();
-  *cpu = kv_of(kv)->resident_cpu_bytes();
-  return pgr::kOk;
+  try {
+    if (!kv || !gpu || !cpu) return set_err(pgr::kErrInvalid, "null pointer");
+    *gpu = kv_of(kv)->resident_gpu_bytes();
+    *cpu = kv_of(kv)->resident_cpu_bytes();
+    return pgr::kOk;
+  } catch (...) {
+    return exception_status();
+  }
 }
 
 int pgr_kv_block_bytes(void* kv, int32_t sid, int64_t* bytes) {
-  if (!kv || !bytes) return set_err(pgr::kErrInvalid, "null pointer");
-  int64_t info[4];
-  if (kv_of(kv)->session_info(sid, &info[0], &info[1], &info[2], &info[3]) != pgr::kOk)
-    return set_err(pgr::kErrKey, "unknown session");
-  *bytes = kv_of(kv)->block_bytes_all_layers(sid);
-  return pgr::kOk;
+  try {
+    if (!kv || !bytes) return set_err(pgr::kErrInvalid, "null pointer");
+    int64_t info[4];
+    if (kv_of(kv)->session_info(sid, &info[0], &info[1], &info[2], &info[3]) != pgr::kOk)
+      return set_err(pgr::kErrKey, "unknown session");
+    *bytes = kv_of(kv)->block_bytes_all_layers(sid);
+    return pgr::kOk;
+  } catch (...) {
+    return exception_status();
+  }
 }
 
 int pgr_kv_set_timing(void* kv, int32_t on) {
-  if (!kv) return set_err(pgr::kErrInvalid, "null store");
-  kv_of(kv)->set_timing(on != 0);
-  return pgr::kOk;
+  try {
+    if (!kv) return set_err(pgr::kErrInvalid, "null store");
+    kv_of(kv)->set_timing(on != 0);
+    return pgr::kOk;
+  } catch (...) {
+    return exception_status();
+  }
 }
 
 int pgr_kv_kernel_time(void* kv, double* ms, int64_t* launches, int64_t* bytes) {
-  if (!kv || !ms || !launches || !bytes) return set_err(pgr::kErrInvalid, "null pointer");
-  return kv_rc(kv_of(kv), kv_of(kv)->kernel_time(ms, launches, bytes));
+  try {
+    if (!kv || !ms || !launches || !bytes) return set_err(pgr::kErrInvalid, "null pointer");
+    return kv_rc(kv_of(kv), kv_of(kv)->kernel_time(ms, launches, bytes));
+  } catch (...) {
+    return exception_status();
+  }
 }
 
 int pgr_kv_sync(void* kv) {
-  if (!kv) return set_err(pgr::kErrInvalid, "null store");
-  return kv_rc(kv_of(kv), kv_of(kv)->sync());
+  try {
+    if (!kv) return set_err(pgr::kErrInvalid, "null store");
+    return kv_rc(kv_of(kv), kv_of(kv)->sync());
+  } catch (...) {
+    return exception_status();
+  }
 }
 
 }  // extern "C"

@@ -155,12 +155,21 @@ __global__ void plan_upload_kernel(const void* src, void* dst, int64_t n_vec) {
 }  // namespace
 
 void HostWorker::submit(std::function<hipError_t()> job) {
-  {
-    std::lock_guard<std::mutex> lk(mu_);
-    job_ = std::move(job);
-    pending_ = true;
-    if (!thread_.joinable()) thread_ = std::thread([this] { run(); });
+  std::unique_lock<std::mutex> lk(mu_);
+  if (!thread_.joinable()) {
+    try {
+      thread_ = std::thread([this] { run(); });
+    } catch (const std::system_error&) {  // no thread to be had: the job runs here
+      lk.unlock();
+      const hipError_t r = job();
+      lk.lock();
+      result_ = r;
+      return;
+    }
   }
+  job_ = std::move(job);
+  pending_ = true;
+  lk.unlock();
   cv_.notify_all();
 }
 

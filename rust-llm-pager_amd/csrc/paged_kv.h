@@ -24,6 +24,7 @@
 #include <cstdint>
 #include <functional>
 #include <mutex>
+#include <system_error>
 #include <string>
 #include <thread>
 #include <vector>
@@ -81,7 +82,8 @@ class HostWorker {
   HostWorker(const HostWorker&) = delete;
   HostWorker& operator=(const HostWorker&) = delete;
   ~HostWorker() { stop(); }
-  // Runs `job` on the worker thread. A job submitted before must have been waited for.
+  // Runs `job` on the worker thread (here, at once, if no thread can be started). A job
+  // submitted before must have been waited for.
   void submit(std::function<hipError_t()> job);
   // Returns once the submitted job (if any) has run, with its result; hipSuccess if none.
   hipError_t wait();

@@ -20,6 +20,7 @@ enum Status : int {
   kErrState = -5,        // call not valid in the object's current state
   kErrKey = -6,          // unknown block / sequence id
   kErrBudget = -7,       // ram budget would be exceeded
+  kErrInternal = -8,     // an internal failure (an exception caught at the C boundary)
 };
 
 // Query heads sharing one KV head are packed into the 16 columns of one MFMA tile.
