@@ -1283,6 +1283,9 @@ int PagedKV::begin_step(const int32_t* sids, int n, hipStream_t stream) {
 // kernels wait for the host to return from begin_step) while they are issued. Everything the
 // job reads is fixed after init, apart from the spans, which it takes by value; the GPU-side
 // order is the same as when the calls are made here, as every copy waits for mirror_go_.
+// They may overlap a graph capture that the caller begins on its own stream after
+// begin_step: all of them are asynchronous calls on the store's non-blocking copy stream,
+// which a capture in global mode permits on other threads (no implicit synchronization).
 int PagedKV::issue_mirror_copies(hipStream_t stream) {
   if (int rc = order_after_decode(stream); rc != kOk) return rc;
   PGR_HIP(mirror_issuer_.wait());  // the last step's job: mirror_done_ is recorded
