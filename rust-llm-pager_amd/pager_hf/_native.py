@@ -25,8 +25,16 @@ def dtype_code(dtype: torch.dtype) -> int:
         ) from None
 
 
+# torch's own accessor of the current raw stream (what torch.cuda.current_stream(d).cuda_stream
+# returns, without building a Stream object: ~0.3 against ~1.9 us per call).
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_of(device: torch.device) -> int:
     """Raw hipStream_t of torch's current stream on `device`."""
+    if _raw_stream is not None:
+        idx = device.index if device.index is not None else torch.cuda.current_device()
+        return _raw_stream(idx)
     return torch.cuda.current_stream(device).cuda_stream
 
 
