@@ -53,6 +53,25 @@ def test_abi_version_and_error_string():
     assert rc == nat.PGR_ERR_UNSUPPORTED and "16" in nat.last_error()
 
 
+def test_status_codes_match_the_header():
+    text = open(HEADER).read()
+    codes = {name: int(val) for name, val in re.findall(r"#define (PGR_(?:OK|ERR_[A-Z]+)) \(?(-?\d+)\)?", text)}
+    assert codes["PGR_OK"] == 0 and len(codes) == 9
+    for name, val in codes.items():
+        if name != "PGR_OK":
+            assert getattr(nat, name) == val, name
+    assert sorted(codes.values()) == list(range(-8, 1))
+
+
+def test_state_init_validates_before_any_launch():
+    lib = nat.load()
+    assert lib.pgr_attn_state_init(None, None, None, 0, 64, None) == 0  # nothing to write
+    assert lib.pgr_attn_state_init(None, None, None, 4, 64, None) == nat.PGR_ERR_INVALID
+    assert "null" in nat.last_error()
+    assert lib.pgr_attn_state_init(None, None, None, 4, 0, None) == nat.PGR_ERR_INVALID
+    assert lib.pgr_attn_state_init(None, None, None, -1, 64, None) == nat.PGR_ERR_INVALID
+
+
 def test_workspace_size_is_deterministic_and_positive():
     lib = nat.load()
     a = lib.pgr_attn_workspace_bytes(8, 14, 2, 2048, 64, nat.MODE_FOLD, 16)
