@@ -76,6 +76,45 @@ def test_state_init_values_shapes_and_reuse(b, hq, d):
         streaming_attention_state_init(1, hq, d, torch.device("cpu"))
 
 
+@pytest.mark.parametrize("tokens,dtype", [(256, torch.float16), (4096, torch.bfloat16), (32768, torch.float16)])
+def test_operator_call_replayed_from_a_graph_matches_eager(tokens, dtype):
+    """state_init + step + finalize captured in a HIP graph (as the operator benchmark replays
+    them) and replayed over new inputs, with eager calls and synchronizations between the
+    replays: every replay equals the eager call on the same inputs bit for bit."""
+    g = torch.Generator().manual_seed(tokens)
+    hq, hkv, d = 28, 4, 128
+
+    def draw():
+        return ((torch.randn(1, hq, d, generator=g) * 0.5).to(dtype).cuda(),
+                (torch.randn(1, hkv, tokens, d, generator=g) * 0.5).to(dtype).cuda(),
+                (torch.randn(1, hkv, tokens, d, generator=g) * 0.5).to(dtype).cuda())
+
+    def call(q, k, v):
+        m, l, acc = streaming_attention_state_init(1, hq, d, q.device)
+        streaming_attention_step(q, k, v, m, l, acc)
+        return streaming_attention_finalize(acc, l, dtype)
+
+    sq, sk, sv = draw()
+    call(sq, sk, sv)  # library and allocator set up outside the capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = call(sq, sk, sv)
+    for rep in range(4):
+        q, k, v = draw()
+        sq.copy_(q)
+        sk.copy_(k)
+        sv.copy_(v)
+        graph.replay()
+        torch.cuda.synchronize()
+        want = call(q, k, v)
+        torch.cuda.synchronize()
+        assert torch.equal(out, want)
+        if rep == 0:
+            ref, _ = dense(q.cpu(), k.cpu(), v.cpu(), hq // hkv)
+            assert max_abs(out, ref) < TOL
+
+
 # -- the reference's eight tests ---------------------------------------------------------
 
 
