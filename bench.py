@@ -243,6 +243,7 @@ def continuous(args):
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     tokens = sum(len(r.generated_tokens) for r in reqs) - tokens0
+    hbm_store = eng.decoder.pool.hbm_bytes()
     sched.stop()
     link = host_bytes[0] / dt / 1e9
     hbm = hbm_bytes[0] / dt / 1e9
@@ -261,6 +262,7 @@ def continuous(args):
         "hbm": {"achieved": round(hbm, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(hbm / HBM_PEAK_GBS, 4),
                 "bytes_per_round": hbm_bytes[0] // args.cb_rounds},
         "live_context_lengths": live_lens,
+        "hbm_kv_bytes": hbm_store,
         "dtype": "bf16",
         "data": "synthetic: random-init weights, random token ids",
         "config": {"workload": "continuous batching, Qwen2.5-1.5B architecture, 64 concurrent, prompts lognormal("
@@ -424,6 +426,7 @@ def _layer_config(args, name, *, hq, hkv, d, dtype, batch, ctx, resident, window
     torch.cuda.synchronize()
     dec.pool.sync()
     dt = (time.perf_counter() - t0) / steps
+    hbm_store = dec.pool.hbm_bytes()
     dec.pool.close()
     tok_bytes = 2 * hkv * d * 2
     host_b, hbm_b = host / steps * tok_bytes, res_tok / steps * tok_bytes
@@ -437,6 +440,7 @@ def _layer_config(args, name, *, hq, hkv, d, dtype, batch, ctx, resident, window
         "kv_GBs": round((host_b + hbm_b) / dt / 1e9, 2),
         "host_link": _rate(host_b, dt, LINK_PEAK_GBS),
         "hbm": _rate(hbm_b, dt, HBM_PEAK_GBS),
+        "hbm_kv_bytes": hbm_store,
         "cpu_baseline": _cpu_record(cpu_bytes, cpu_s, batch, threads,
                                     f"dense fp32 attention and block mass in torch over the same in-scope K/V of "
                                     f"all {batch} sequences, repeated for ~{args.cpu_seconds / 3:.0f} s"),
@@ -502,10 +506,10 @@ def config3(args):
         t0 = time.perf_counter()
         pm.generate(ids2, torch.ones_like(ids2), n_new)
         torch.cuda.synchronize()
-        timed[(graphs, mode)] = ((time.perf_counter() - t0) / n_new, pm.last_run_stats)
+        timed[(graphs, mode)] = ((time.perf_counter() - t0) / n_new, pm.last_run_stats, pm.decoder.pool.hbm_bytes())
         pm.reset()
     best = min(timed, key=lambda k: (not k[0], timed[k][0]))  # the fastest graph run
-    dt, st = timed[best]
+    dt, st, hbm_store = timed[best]
     del model
     torch.cuda.empty_cache()
     kv_tok = 2 * 4 * 64 * 2 * 22  # K+V bytes of one token over all layers
@@ -531,6 +535,9 @@ def config3(args):
         "host_link": _rate(host_b, dt, LINK_PEAK_GBS),
         "hbm": _rate(hbm_b, dt, HBM_PEAK_GBS),
         "mean_attention_in_gpu": round(st.mean_attention_in_gpu, 4),
+        "hbm_kv_bytes": hbm_store,
+        "hbm_kv_bytes_by_run": {("graphs_" if g else "eager_") + m: timed[(g, m)][2]["total"] for g, m in timed},
+        "hbm_budget_bytes": 41 * 32 * kv_tok,  # the 41-block placement budget, all layers
         "cpu_baseline": _cpu_record(in_scope * kv_tok, cpu_s, 1, threads,
                                     f"dense fp32 attention and block mass in torch for all 22 layers of one decode "
                                     f"step at the mean context ({in_scope} tokens), repeated for "
@@ -571,6 +578,7 @@ def config5(args):
         "hbm": {"bytes_per_step": res["hbm"]["bytes_per_round"], "GBs": res["hbm"]["achieved"],
                 "peak": HBM_PEAK_GBS, "frac": res["hbm"]["frac"]},
         "kv_GBs": round((res["host_link"]["bytes_per_round"] + res["hbm"]["bytes_per_round"]) / dt / 1e9, 2),
+        "hbm_kv_bytes": res["hbm_kv_bytes"],
         "cpu_baseline": {"value": round(cpu_gbs, 3), "unit": "GB/s", "tokens_per_s": round(64 / round_s, 2),
                          "cores": threads, "kind": "port",
                          "sample": f"dense bf16->fp32 attention and block mass in torch over 8 of the live sessions "
@@ -680,10 +688,15 @@ def operator_api(dtype_name="float16"):
     events, state init + step + finalize per call), at the probe's chunk sizes and at 32768
     tokens, with torch's eager attention (matmul, softmax, matmul over repeated KV heads) on
     the same inputs beside it as the probe does. K/V GB/s counts the chunk's K and V bytes."""
+    import ctypes
+
     import torch
 
+    import _pgr_native as nat
     from pager_hf.streaming_attention import (streaming_attention_finalize, streaming_attention_state_init,
                                               streaming_attention_step)
+
+    lib = nat.load()
 
     dtype = getattr(torch, dtype_name)
     hq, hkv, d = 28, 4, 128
@@ -731,15 +744,29 @@ def operator_api(dtype_name="float16"):
             ours()
         ms_graph = time_cuda(graph.replay)
         del graph
+        # The fold kernel alone: event pairs around each of 20 attention launches (the library's
+        # operator timing), without the state init, merge and finalize launches of a call.
+        nat.check(lib.pgr_attn_set_timing(1), "pgr_attn_set_timing")
+        for _ in range(20):
+            ours()
+        fold_ms, fold_n, fold_bytes = ctypes.c_double(0), ctypes.c_int64(0), ctypes.c_int64(0)
+        nat.check(lib.pgr_attn_kernel_time(ctypes.byref(fold_ms), ctypes.byref(fold_n), ctypes.byref(fold_bytes)),
+                  "pgr_attn_kernel_time")
+        nat.check(lib.pgr_attn_set_timing(0), "pgr_attn_set_timing")
+        fold_us = fold_ms.value * 1e3 / max(fold_n.value, 1)
+        fold_gbs = fold_bytes.value / max(fold_n.value, 1) / (fold_us * 1e3)
         kv = 2 * hkv * tokens * d * k.element_size()
         rows.append({"tokens": tokens, "ms_per_call": round(ms, 4), "torch_eager_ms": round(ms_eager, 4),
                      "ms_per_call_graph": round(ms_graph, 4), "kv_GBs_graph": round(kv / ms_graph / 1e6, 1),
-                     "hbm_frac_graph": round(kv / ms_graph / 1e6 / HBM_PEAK_GBS, 4)})
+                     "hbm_frac_graph": round(kv / ms_graph / 1e6 / HBM_PEAK_GBS, 4),
+                     "fold_us": round(fold_us, 3), "fold_GBs": round(fold_gbs, 1),
+                     "fold_frac": round(fold_gbs / HBM_PEAK_GBS, 4)})
     return {
         "workload": "operator API, Qwen2.5-7B shape (28q/4kv, D 128), batch 1, one contiguous chunk per call; "
                     "state_init + step + finalize per call, 20 calls between two events (ms_per_call: eager calls, "
                     "as the reference's probe times them; ms_per_call_graph: replays of the call captured in a HIP "
-                    "graph)",
+                    "graph; fold_us / fold_frac: the attention kernel alone, events around each launch, its K+V "
+                    "bytes over 8 TB/s)",
         "dtype": dtype_name, "rows": rows,
     }
 

@@ -36,7 +36,7 @@ extern "C" {
 
 /* ---- library ------------------------------------------------------------------------- */
 
-/* ABI version of this header (increments when an entry point is added or changed); 8. */
+/* ABI version of this header (increments when an entry point is added or changed); 9. */
 int pgr_abi_version(void);
 /* Message of the last failing call on this thread ("" if none). */
 const char* pgr_last_error(void);
@@ -104,6 +104,15 @@ int pgr_attn_fold_fixed_step(const void* q, const void* k, const void* v, const 
                              const float* l, float* acc, int64_t batch, int64_t num_query_heads, int64_t num_kv_heads,
                              int64_t tokens, int64_t head_dim, int dtype, float scale, float softcap, void* workspace,
                              size_t workspace_bytes, void* stream);
+
+/* No counterpart in the reference (its probe times whole calls with torch events,
+ * bench/streaming_attention_kernel_scaling_probe.py:42-53). For measurement: with timing on,
+ * every operator call of this process records a pair of events around its attention kernel
+ * launch (not the merge launch after it); pgr_attn_kernel_time waits for them and returns the
+ * summed milliseconds, the number of launches and the K/V bytes they read (K only in stats
+ * mode), then forgets them. Process-wide; not for use under graph capture. */
+int pgr_attn_set_timing(int32_t on);
+int pgr_attn_kernel_time(double* ms, int64_t* launches, int64_t* bytes);
 
 /* Fresh state for rows = B * Hq: m[r] = -inf, l[r] = 0, acc[r, :] = 0 (fp32, contiguous), in
  * one launch. Replaces streaming_attention_state_init, pager_hf/streaming_attention.py:444-449
@@ -173,17 +182,22 @@ typedef struct pgr_kv_config_s {
  * step's host blocks fit one buffer and staging_buffers >= 2, pgr_kv_decode_layer(l) also
  * queues layer l+1's copies right after layer l's attention, so that they run under the
  * caller's work between the two layers. */
-/* MIRROR: every layer has an HBM mirror of its host records (HBM: host_records records per
- * layer). pgr_kv_begin_step has a host thread of the store queue, on the store's side stream
- * and behind the work queued on `stream` before begin_step: DMA copies of each layer's span of
- * the step's host records into that layer's mirror, and after each layer's copies a word that
- * the layer's attention launch waits for (one lane per workgroup, a bounded wait of ~20 ms).
- * Its workgroups then read host blocks from the mirror, or from the host in place if the word
- * is still clear when the wait ends (same data). The copies run beside whatever the caller
- * runs between the step's layers, including a replayed graph of the layers; the next
- * begin_step waits for them. pgr_kv_sync and pgr_kv_destroy wait for the thread's queueing
- * (destroy ends the thread). For one long-context session whose host share fits in HBM as a
- * mirror (a model between layers, e.g. a captured decode step). */
+/* MIRROR: a ring of n = min(staging_buffers, num_layers) HBM buffers, each holding one layer's
+ * share of a step's host records (the span from each row's first to last host record of the
+ * step, rows packed; staging_slots records at first, grown by begin_step when a step needs
+ * more). pgr_kv_begin_step has a host thread of the store queue, on the store's side stream
+ * and behind the work queued on `stream` before begin_step, per layer l: DMA copies of the
+ * layer's share into buffer l % n, then a word that the layer's attention launch waits for
+ * (one lane per workgroup, a bounded wait of ~20 ms). For l >= n the thread first waits until
+ * the merge launch of layer l - n has published the step's token in a pinned word: that
+ * layer's attention launch, the buffer's last reader, has finished. A workgroup reads host
+ * blocks from the ring buffer, or from the host in place if its word is still clear when the
+ * wait ends (same data). The copies run beside whatever the caller runs between the step's
+ * layers, including a replayed graph of the layers; the next begin_step waits for them.
+ * Layers are expected in order: one decoded before the layers n below it waits its bounded
+ * wait and reads the host. pgr_kv_sync waits for the copies queued so far, pgr_kv_destroy
+ * for all of them and then ends the thread. For long-context sessions with a model between
+ * the layers (a captured decode step, say). */
 #define PGR_STREAM_DIRECT 0
 #define PGR_STREAM_STAGED 1
 #define PGR_STREAM_MIRROR 2
@@ -194,8 +208,12 @@ typedef struct pgr_kv_stats_s {
   uint64_t evict_bytes_copied, load_bytes_copied, stream_bytes, stream_copies;
 } pgr_kv_stats_t;
 
+/* Per step: resident_tokens / host_tokens / host_blocks count what the attention launches
+ * read from HBM and from the host tier (where the bytes are); gather_blocks counts the
+ * entries of the step's gather lists (blocks the placement put on the host tier; they differ
+ * only for prompt blocks that wait for their first placement, see pgr_kv_apply_tiers). */
 typedef struct pgr_kv_step_stats_s {
-  int64_t resident_tokens, host_tokens, host_blocks, copies, chunks, launches, work_items;
+  int64_t resident_tokens, host_tokens, host_blocks, copies, chunks, launches, work_items, gather_blocks;
 } pgr_kv_step_stats_t;
 
 /* Creates a store (allocates HBM pools, pinned host mirror, staging). NULL on failure.
@@ -241,7 +259,13 @@ int pgr_kv_put_block(void* kv, int32_t sid, int64_t block_id, const void* key, c
 int pgr_kv_get_block(void* kv, int32_t sid, int64_t block_id, void* key, void* value, void* stream);
 /* Moves full blocks to the tier the pager assigned (0 = HBM, else host; ids >= n_tiers ->
  * host), ascending by id; writes moved ids. PGR_ERR_BUDGET with *fail_block when an
- * offload would exceed the RAM budget (earlier moves stay done). The copies are queued on
+ * offload would exceed the RAM budget (earlier moves stay done). The record copies of one
+ * call go evictions first, then loads (the move lists and byte counts are those of the
+ * ascending order). A prompt block placed in HBM for the first time takes an HBM slot only
+ * while the pool keeps two slots per row free, the most recent blocks first; the others count
+ * as HBM-resident and have their bytes written to and read from the host records until a
+ * later call loads or evicts them, so that a pool sized to the placement budget suffices
+ * (PGR_ERR_CAPACITY when a load finds no slot). The copies are queued on
  * `stream`, after the work already there, and after the last decode step's launches when
  * those ran on another stream (that stream must still be valid); this store's later calls
  * on another stream wait for the copies through one event recorded here.
@@ -256,10 +280,15 @@ int pgr_kv_begin_step(void* kv, const int32_t* sids, int32_t n, void* stream);
 /* One layer of the step: appends k_new/v_new [S, Hkv, D] at each sequence's next position,
  * folds every in-scope block (HBM in place, host blocks streamed), writes out [S, Hq, D]
  * and, if mass_accum != NULL, adds the per-block attention mass (mean over the session's
- * rows and query heads) into mass_accum[session_in_step * accum_stride + block].
+ * rows and query heads) into mass_accum[session_in_step * accum_stride + block]. In a step
+ * whose sessions have a pager scoring by mass (pgr_kv_attach_pager), that addition is made
+ * for all layers at once, in layer order, by pgr_kv_end_step / pgr_kv_end_step_place (same
+ * values; the layers' shares of the step, num_layers x rows x Hq x blocks floats, must fit
+ * 64 MiB, else each layer adds its own as it runs).
  * window > 0: this layer's own sliding window (alternating-window models); it also masks
  * the stored positions c <= p - window, p being the current token's position (the rule
- * col > pos - W of paged_model.py:977-982). Blocks are still read; window <= 0: none.
+ * col > pos - W of paged_model.py:977-982). Tiles wholly below it are not read (the
+ * reference reads every block and masks, paged_model.py:961); window <= 0: none.
  * Replaces the patched layer forward's gather + fold loop, paged_model.py:926-1086
  * (gather :878-924, tail append :955, mass :1041-1048). */
 int pgr_kv_decode_layer(void* kv, int32_t layer, const void* q, const void* k_new, const void* v_new, void* out,
@@ -296,7 +325,7 @@ int pgr_kv_attach_pager(void* kv, int32_t sid, void* pager, int32_t scores_from_
  * wait for the step's launches (the decode stream must still be valid).
  * Replaces _forward_step's placement tail and _finalize_streaming_block_attention,
  * paged_model.py:768-812 and :865-876. */
-int pgr_kv_end_step_place(void* kv, const float* mass_accum, int64_t accum_stride, int32_t num_layers,
+int pgr_kv_end_step_place(void* kv, float* mass_accum, int64_t accum_stride, int32_t num_layers,
                           int32_t* completed, int32_t* n_completed, int64_t* counts, int64_t* moves,
                           int64_t moves_cap, double* scores, int64_t scores_cap, void* stream);
 /* info[4] = {n_tokens, n_full_blocks, gpu_blocks, cpu_blocks}. */
@@ -312,6 +341,10 @@ int pgr_kv_step_stats(void* kv, pgr_kv_step_stats_t* out);
 int pgr_kv_stats(void* kv, pgr_kv_stats_t* out);
 /* Replaces resident_gpu_bytes / resident_cpu_bytes, kv_block_store.py:179-183. */
 int pgr_kv_resident_bytes(void* kv, int64_t* gpu, int64_t* cpu);
+/* No counterpart in the reference (its blocks are torch allocations). Device memory the store
+ * holds, in bytes: out[5] = {HBM slot pools, mirror-mode ring buffers, staged-mode staging
+ * buffers, workspace (step plan, split-K partials, block mass), total}. */
+int pgr_kv_hbm_bytes(void* kv, int64_t* out);
 /* Bytes of one block of session sid over all layers and rows (kv_nbytes of a reference block). */
 int pgr_kv_block_bytes(void* kv, int32_t sid, int64_t* bytes);
 /* Event timing of the attention launches (for measurement). */

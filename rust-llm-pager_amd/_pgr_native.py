@@ -36,7 +36,7 @@ STREAM_DIRECT = 0
 STREAM_STAGED = 1
 STREAM_MIRROR = 2
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 c_i32, c_i64, c_u8, c_u32, c_u64 = ctypes.c_int32, ctypes.c_int64, ctypes.c_uint8, ctypes.c_uint32, ctypes.c_uint64
 c_f32, c_f64, c_size, c_vp = ctypes.c_float, ctypes.c_double, ctypes.c_size_t, ctypes.c_void_p
@@ -97,6 +97,7 @@ class KVStepStats(ctypes.Structure):
         ("chunks", c_i64),
         ("launches", c_i64),
         ("work_items", c_i64),
+        ("gather_blocks", c_i64),
     ]
 
 
@@ -130,6 +131,8 @@ SIGNATURES: dict[str, tuple] = {
         [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_i64, ctypes.c_int, c_f32, c_f32,
          c_vp, c_size, c_vp],
     ),
+    "pgr_attn_set_timing": (ctypes.c_int, [c_i32]),
+    "pgr_attn_kernel_time": (ctypes.c_int, [P(c_f64), P(c_i64), P(c_i64)]),
     "pgr_attn_state_init": (ctypes.c_int, [c_vp, c_vp, c_vp, c_i64, c_i64, c_vp]),
     "pgr_attn_finalize": (ctypes.c_int, [c_vp, c_vp, c_vp, c_i64, c_i64, ctypes.c_int, c_vp]),
     "pgr_pager_new": (c_vp, [c_u64, c_u64, c_u64, c_u64, c_f32, c_f32, ctypes.c_char_p]),
@@ -175,6 +178,7 @@ SIGNATURES: dict[str, tuple] = {
     "pgr_kv_step_stats": (ctypes.c_int, [c_vp, P(KVStepStats)]),
     "pgr_kv_stats": (ctypes.c_int, [c_vp, P(KVStats)]),
     "pgr_kv_resident_bytes": (ctypes.c_int, [c_vp, P(c_i64), P(c_i64)]),
+    "pgr_kv_hbm_bytes": (ctypes.c_int, [c_vp, P(c_i64)]),
     "pgr_kv_block_bytes": (ctypes.c_int, [c_vp, c_i32, P(c_i64)]),
     "pgr_kv_set_timing": (ctypes.c_int, [c_vp, c_i32]),
     "pgr_kv_kernel_time": (ctypes.c_int, [c_vp, P(c_f64), P(c_i64), P(c_i64)]),

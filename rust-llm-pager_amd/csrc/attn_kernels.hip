@@ -770,10 +770,12 @@ struct PagedArgs {
   int hq, hkv, n_rep, tokens_per_block, mass_stride;
   float scale, softcap;
   int window;             // > 0: the layer's sliding window (see PagedLaunch)
-  const uint16_t* mirror;       // mirror mode: HBM copy of `stage` (the host mirror), or null
+  const uint16_t* mirror;       // mirror mode: the layer's ring buffer (host records, packed), or null
   const uint32_t* mirror_flag;  // set once this layer's copies into `mirror` have landed
   uint32_t* plan_flag;    // merge: pinned word for plan_token (see PagedLaunch), or null
   uint32_t plan_token;
+  uint32_t* release_flag; // merge, mirror mode: pinned word for the step token (see PagedLaunch)
+  float* mass_w;          // merge, deferred mass: this layer's [S][Hq][mass_stride] weights
 };
 
 constexpr float kLog2e = 1.4426950408889634f;
@@ -945,6 +947,7 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(const WorkItem* __restr
   // change while its session holds it, and the mirror is refilled only after the launches
   // of the step before have finished.
   const uint16_t* host_src = stage;
+  int host_shift = 0;  // ring buffer record = host record - host_shift
   if (a.mirror_flag != nullptr) {
     __shared__ uint32_t mirror_ready;
     if (threadIdx.x == 0) {
@@ -953,10 +956,17 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(const WorkItem* __restr
         __builtin_amdgcn_s_sleep(127);
         f = __hip_atomic_load(a.mirror_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
       }
+      // The ring buffer held another layer's records when this launch started, and a cache
+      // may still hold lines of them: a system-scope acquire (cache invalidate) orders the
+      // workgroup's reads after the DMA copy that the word announces.
+      if (f != 0u) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "");
       mirror_ready = f;
     }
     __syncthreads();
-    if (__builtin_amdgcn_readfirstlane(mirror_ready) != 0u) host_src = a.mirror;
+    if (__builtin_amdgcn_readfirstlane(mirror_ready) != 0u) {
+      host_src = a.mirror;
+      host_shift = wi->mirror_off;
+    }
   }
 
   RunVec<D> q[LaneRun<D>::N];  // loaded behind the first tile (below)
@@ -980,12 +990,18 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(const WorkItem* __restr
   int nf = 0, fe = 0, ftb = 0;
   auto fetch = [&](PTile<D>& t, TileMeta& mt) {
     const int slot = ecur.slot, bid = ecur.block_id;
-    const uint16_t* rb = slot >= 0 ? pool + (size_t)slot * rec : host_src + (size_t)(-slot - 1) * rec;
-    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(rb + head_off), (short)0, nf < tiles ? 0x7fffffff : 0, kBufferFlags);
+    const uint16_t* rb =
+        slot >= 0 ? pool + (size_t)slot * rec : host_src + (size_t)((-slot - 1) - host_shift) * rec;
+    // A tile with no token in [lo, hi) (below a layer's own sliding window, or past the
+    // current token in the open block) is fully masked: its loads go through an empty
+    // resource and return zeros without a memory access, as past the wave's last tile.
+    const int tt0 = bid * T + ftb * 16;
+    const bool read = nf < tiles && tt0 + 16 > lo && tt0 < hi;
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(rb + head_off), (short)0, read ? 0x7fffffff : 0, kBufferFlags);
     const uint32_t sk = (uint32_t)(ftb * 16 * D * 2);
     load_tile_rs<D>(t, r, sk, sk + (uint32_t)(v_off * 2), k_lane, v_lane);
-    mt.t0 = bid * T + ftb * 16;
+    mt.t0 = tt0;
     mt.block_id = bid;
     mt.last = (ftb == tpb - 1) ? fe : -1;
     ++nf;
@@ -1134,6 +1150,10 @@ __global__ __launch_bounds__(256) void paged_merge_kernel(const SeqInfo* __restr
   // plan buffer is free (a system-scope vector store into pinned host memory).
   if (a.plan_flag != nullptr && seq == 0 && qh == 0 && tid == 0)
     __hip_atomic_store(a.plan_flag, a.plan_token, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  // Mirror mode: the layer's attention launch has finished reading its ring buffer; the host
+  // may queue the next copies into it once this word holds the step's token.
+  if (a.release_flag != nullptr && seq == 0 && qh == 0 && tid == 0)
+    __hip_atomic_store(a.release_flag, si->step_token, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 
   // Group 0 also computes the current token's score (its loads overlap the partial loads).
   uint32_t qd = 0, kd = 0, vd = 0;
@@ -1196,36 +1216,51 @@ __global__ __launch_bounds__(256) void paged_merge_kernel(const SeqInfo* __restr
   acc_s[grp][2 * c] = acc.x;
   acc_s[grp][2 * c + 1] = acc.y;
   __syncthreads();
-  if (grp != 0) return;
-
-  dot = dot_s[0];
+  __shared__ float fin_s[2];  // final (m, l) of this (sequence, head), for the block weights
+  if (grp == 0) {
+    dot = dot_s[0];
 #pragma unroll
-  for (int w = 1; w < kLanes / kRed; ++w) dot += dot_s[w];
-  float x_cur;
-  if (a.softcap > 0.f)
-    x_cur = a.softcap * tanhf(dot * (a.scale / a.softcap)) * kLog2e;
-  else
-    x_cur = dot * (a.scale * kLog2e);
-  float mf = x_cur;  // the current token is always valid: mf is finite
+    for (int w = 1; w < kLanes / kRed; ++w) dot += dot_s[w];
+    float x_cur;
+    if (a.softcap > 0.f)
+      x_cur = a.softcap * tanhf(dot * (a.scale / a.softcap)) * kLog2e;
+    else
+      x_cur = dot * (a.scale * kLog2e);
+    float mf = x_cur;  // the current token is always valid: mf is finite
 #pragma unroll
-  for (int g2 = 0; g2 < G; ++g2) mf = fmaxf(mf, m_s[g2]);
-  const float pc = __builtin_amdgcn_exp2f(x_cur - mf);
-  const float pcr = Ty::to_f(Ty::cvt(pc));  // P rounded to the K/V type before P.V
-  float lf = pc;
-  float o0 = pcr * Ty::to_f((uint16_t)(vd & 0xffffu));
-  float o1 = pcr * Ty::to_f((uint16_t)(vd >> 16));
+    for (int g2 = 0; g2 < G; ++g2) mf = fmaxf(mf, m_s[g2]);
+    const float pc = __builtin_amdgcn_exp2f(x_cur - mf);
+    const float pcr = Ty::to_f(Ty::cvt(pc));  // P rounded to the K/V type before P.V
+    float lf = pc;
+    float o0 = pcr * Ty::to_f((uint16_t)(vd & 0xffffu));
+    float o1 = pcr * Ty::to_f((uint16_t)(vd >> 16));
 #pragma unroll
-  for (int g2 = 0; g2 < G; ++g2) {
-    const float w = __builtin_amdgcn_exp2f(m_s[g2] - mf);  // empty group: m = -inf, w = 0
-    lf += l_s[g2] * w;
-    o0 += acc_s[g2][2 * c] * w;
-    o1 += acc_s[g2][2 * c + 1] * w;
+    for (int g2 = 0; g2 < G; ++g2) {
+      const float w = __builtin_amdgcn_exp2f(m_s[g2] - mf);  // empty group: m = -inf, w = 0
+      lf += l_s[g2] * w;
+      o0 += acc_s[g2][2 * c] * w;
+      o1 += acc_s[g2][2 * c + 1] * w;
+    }
+    const uint32_t packed = (uint32_t)Ty::cvt(o0 / lf) | ((uint32_t)Ty::cvt(o1 / lf) << 16);
+    *reinterpret_cast<uint32_t*>(a.out + ((size_t)seq * hq + qh) * D + 2 * c) = packed;
+    if (c == 0) {
+      a.mf[(size_t)seq * hq + qh] = mf;
+      a.lf[(size_t)seq * hq + qh] = lf;
+      fin_s[0] = mf;
+      fin_s[1] = lf;
+    }
   }
-  const uint32_t packed = (uint32_t)Ty::cvt(o0 / lf) | ((uint32_t)Ty::cvt(o1 / lf) << 16);
-  *reinterpret_cast<uint32_t*>(a.out + ((size_t)seq * hq + qh) * D + 2 * c) = packed;
-  if (c == 0) {
-    a.mf[(size_t)seq * hq + qh] = mf;
-    a.lf[(size_t)seq * hq + qh] = lf;
+  if (a.mass_w == nullptr) return;
+  // Deferred mass: the weight of every in-scope block of this (sequence, head) under the
+  // final (m, l), s_b * 2^(m_b - m_f) / l_f (l_f > 0: the current token always counts), by
+  // all threads. Blocks below mass_lo keep the 0 the last step's reduction left.
+  __syncthreads();
+  const float mfin = fin_s[0], lfin = fin_s[1];
+  const size_t row = (size_t)seq * hq + qh;
+  const int n_mass = si->n_mass;
+  for (int b = si->mass_lo + tid; b < n_mass; b += 256) {
+    const size_t mi = row * a.mass_stride + b;
+    a.mass_w[mi] = a.mass_s[mi] * __builtin_amdgcn_exp2f(a.mass_m[mi] - mfin) / lfin;
   }
 }
 
@@ -1272,6 +1307,48 @@ __global__ __launch_bounds__(256) void mass_reduce_kernel(const SeqInfo* seqs, c
     const float sum = ((part[0][bl] + part[1][bl]) + part[2][bl]) + part[3][bl];
     mass_accum[(size_t)sess * accum_stride + blk] += sum / (float)(rows * hq);
   }
+}
+
+// Deferred mass, once per step (see launch_mass_step_reduce): the same per-layer mean as
+// mass_reduce_kernel, computed from the weights the merges wrote, over the layers in order.
+__global__ __launch_bounds__(256) void mass_step_reduce_kernel(const SeqInfo* seqs, const int32_t* session_rows,
+                                                               const int32_t* session_first, float* mass_w,
+                                                               int64_t layer_floats, int num_layers,
+                                                               float* mass_accum, int accum_stride, int hq,
+                                                               int mass_stride, int max_blocks) {
+  __shared__ float part[kMassHeadGroups][kMassBlocksPerWG];
+  const int sess = blockIdx.y;
+  const int bl = threadIdx.x % kMassBlocksPerWG, hg = threadIdx.x / kMassBlocksPerWG;
+  const int blk = blockIdx.x * kMassBlocksPerWG + bl;
+  const int first = session_first[sess], rows = session_rows[sess];
+  const int n_mass = seqs[first].n_mass;
+  const bool live = blk < n_mass && blk < max_blocks;
+  float acc = 0.f;
+  if (hg == 0 && live) acc = mass_accum[(size_t)sess * accum_stride + blk];
+  for (int layer = 0; layer < num_layers; ++layer) {
+    float* w = mass_w + (size_t)layer * layer_floats;
+    float total = 0.f;
+    if (live) {
+      for (int r = 0; r < rows; ++r) {
+        if (blk < seqs[first + r].mass_lo) continue;  // out of scope for this row: mass 0
+        const size_t row0 = (size_t)(first + r) * hq;
+#pragma unroll 4
+        for (int qh = hg; qh < hq; qh += kMassHeadGroups) {
+          const size_t mi = (row0 + qh) * mass_stride + blk;
+          total += w[mi];
+          w[mi] = 0.f;
+        }
+      }
+    }
+    part[hg][bl] = total;
+    __syncthreads();
+    if (hg == 0 && live) {
+      const float sum = ((part[0][bl] + part[1][bl]) + part[2][bl]) + part[3][bl];
+      acc += sum / (float)(rows * hq);
+    }
+    __syncthreads();
+  }
+  if (hg == 0 && live) mass_accum[(size_t)sess * accum_stride + blk] = acc;
 }
 
 hipError_t launch_dense_merge(const DenseArgs& a, int mode, int batch, int d, float* m, float* l, float* acc,
@@ -1476,6 +1553,7 @@ hipError_t launch_dense(int dtype, int mode, int d, const DenseLaunch& p, hipStr
   a.scale = p.scale;
   a.softcap = p.softcap;
   hipError_t e;
+  if (p.ev_start != nullptr && (e = hipEventRecord(p.ev_start, stream)) != hipSuccess) return e;
   if (dtype == kF32)
     e = launch_generic_32(a, mode, p.batch, d, stream);
   else if (!head_dim_supported(d))
@@ -1485,6 +1563,7 @@ hipError_t launch_dense(int dtype, int mode, int d, const DenseLaunch& p, hipStr
     e = dtype == kF16 ? launch_dense_ty<F16>(a, mode, p.batch, d, stream)
                       : launch_dense_ty<BF16>(a, mode, p.batch, d, stream);
   if (e != hipSuccess) return e;
+  if (p.ev_stop != nullptr && (e = hipEventRecord(p.ev_stop, stream)) != hipSuccess) return e;
   return launch_dense_merge(a, mode, p.batch, d, p.m, p.l, p.acc, stream);
 }
 
@@ -1570,6 +1649,11 @@ hipError_t launch_paged_merge(int dtype, int d, const PagedLaunch& p, int n_seq,
   a.softcap = p.softcap;
   a.plan_flag = p.plan_flag;
   a.plan_token = p.plan_token;
+  a.release_flag = p.release_flag;
+  a.mass_w = p.mass_w;
+  a.mass_m = p.mass_m;
+  a.mass_s = p.mass_s;
+  a.mass_stride = p.mass_stride;
   dim3 grid(n_seq, p.hq);
   if (dtype == kF16)
     launch_merge_d<F16>(a, d, grid, stream);
@@ -1586,6 +1670,18 @@ hipError_t launch_mass_reduce(const SeqInfo* seqs, const int32_t* session_rows, 
   dim3 grid((max_blocks + kMassBlocksPerWG - 1) / kMassBlocksPerWG, n_sessions);
   mass_reduce_kernel<<<grid, 256, 0, stream>>>(seqs, session_rows, session_first, mass_m, mass_s, mf, lf, mass_accum,
                                                accum_stride, hq, mass_stride, n_sessions, max_blocks);
+  return hipGetLastError();
+}
+
+hipError_t launch_mass_step_reduce(const SeqInfo* seqs, const int32_t* session_rows, const int32_t* session_first,
+                                   float* mass_w, int64_t layer_floats, int num_layers, float* mass_accum,
+                                   int accum_stride, int hq, int mass_stride, int n_sessions, int max_blocks,
+                                   hipStream_t stream) {
+  if (n_sessions == 0 || max_blocks == 0 || num_layers == 0) return hipSuccess;
+  dim3 grid((max_blocks + kMassBlocksPerWG - 1) / kMassBlocksPerWG, n_sessions);
+  mass_step_reduce_kernel<<<grid, 256, 0, stream>>>(seqs, session_rows, session_first, mass_w, layer_floats,
+                                                    num_layers, mass_accum, accum_stride, hq, mass_stride,
+                                                    max_blocks);
   return hipGetLastError();
 }
 

@@ -8,6 +8,7 @@
 #include <mutex>
 #include <new>
 #include <string>
+#include <vector>
 
 #include "paged_kv.h"
 #include "pager_core.h"
@@ -79,6 +80,26 @@ DensePlan plan_dense(int64_t batch, int64_t hq, int64_t hkv, int64_t tokens, int
   return p;
 }
 
+// Launch timing of the operator API's attention kernel (pgr_attn_set_timing): fence-free
+// events around each fold launch, resolved by pgr_attn_kernel_time. One process-wide list.
+struct DenseTiming {
+  hipEvent_t start, stop;
+  int64_t bytes;
+};
+std::mutex g_timing_mu;
+bool g_timing_on = false;
+std::vector<DenseTiming> g_timing_pending;
+std::vector<hipEvent_t> g_timing_free;
+
+hipError_t timing_event(hipEvent_t* ev) {
+  if (!g_timing_free.empty()) {
+    *ev = g_timing_free.back();
+    g_timing_free.pop_back();
+    return hipSuccess;
+  }
+  return hipEventCreateWithFlags(ev, hipEventDisableSystemFence);
+}
+
 int run_dense(int mode, const void* q, const void* k, const void* v, const int32_t* valid, const int32_t* active,
               float* m, float* l, float* acc, float* block_mass, int64_t max_blocks, int64_t block_id_offset,
               int64_t tpb, int64_t batch, int64_t hq, int64_t hkv, int64_t tokens, int64_t d, int dtype, float scale,
@@ -122,7 +143,21 @@ int run_dense(int mode, const void* q, const void* k, const void* v, const int32
   L.block_id_offset = (int)block_id_offset;
   L.scale = scale;
   L.softcap = softcap > 0.f ? softcap : 0.f;
+  std::unique_lock<std::mutex> lk(g_timing_mu);
+  const bool timed = g_timing_on;
+  if (timed) {
+    hipError_t te = timing_event(&L.ev_start);
+    if (te == hipSuccess) te = timing_event(&L.ev_stop);
+    if (te != hipSuccess) return hip_err(te, "timing event");
+  } else {
+    lk.unlock();
+  }
   hipError_t e = pgr::launch_dense(dtype, mode, (int)d, L, as_stream(stream));
+  if (timed) {
+    const int64_t elem = dtype == pgr::kF32 ? 4 : 2;
+    const int64_t kv = batch * hkv * tokens * d * elem * (mode == PGR_MODE_STATS ? 1 : 2);
+    g_timing_pending.push_back({L.ev_start, L.ev_stop, kv});
+  }
   if (e != hipSuccess) return hip_err(e, "dense attention launch");
   return pgr::kOk;
 }
@@ -183,7 +218,7 @@ int kv_rc(pgr::PagedKV* kv, int rc) {
 
 extern "C" {
 
-int pgr_abi_version(void) { return 8; }
+int pgr_abi_version(void) { return 9; }
 
 const char* pgr_last_error(void) { return g_last_error.c_str(); }
 
@@ -280,6 +315,43 @@ int pgr_attn_fold_fixed_step(const void* q, const void* k, const void* v, const 
     return run_dense(PGR_MODE_FOLD_FIXED, q, k, v, valid, nullptr, const_cast<float*>(m), const_cast<float*>(l), acc,
                      nullptr, 0, 0, 16, batch, num_query_heads, num_kv_heads, tokens, head_dim, dtype, scale, softcap,
                      workspace, workspace_bytes, stream);
+  } catch (...) {
+    return exception_status();
+  }
+}
+
+int pgr_attn_set_timing(int32_t on) {
+  try {
+    std::lock_guard<std::mutex> lk(g_timing_mu);
+    g_timing_on = on != 0;
+    return pgr::kOk;
+  } catch (...) {
+    return exception_status();
+  }
+}
+
+int pgr_attn_kernel_time(double* ms, int64_t* launches, int64_t* bytes) {
+  try {
+    if (!ms || !launches || !bytes) return set_err(pgr::kErrInvalid, "null pointer");
+    std::lock_guard<std::mutex> lk(g_timing_mu);
+    double total = 0.0;
+    int64_t n = 0, b = 0;
+    for (const DenseTiming& t : g_timing_pending) {
+      hipError_t e = hipEventSynchronize(t.stop);
+      float one = 0.f;
+      if (e == hipSuccess) e = hipEventElapsedTime(&one, t.start, t.stop);
+      if (e != hipSuccess) return hip_err(e, "timing event");
+      total += one;
+      ++n;
+      b += t.bytes;
+      g_timing_free.push_back(t.start);
+      g_timing_free.push_back(t.stop);
+    }
+    g_timing_pending.clear();
+    *ms = total;
+    *launches = n;
+    *bytes = b;
+    return pgr::kOk;
   } catch (...) {
     return exception_status();
   }
@@ -611,7 +683,7 @@ int pgr_kv_attach_pager(void* kv, int32_t sid, void* pager, int32_t scores_from_
   }
 }
 
-int pgr_kv_end_step_place(void* kv, const float* mass_accum, int64_t accum_stride, int32_t num_layers,
+int pgr_kv_end_step_place(void* kv, float* mass_accum, int64_t accum_stride, int32_t num_layers,
                           int32_t* completed, int32_t* n_completed, int64_t* counts, int64_t* moves,
                           int64_t moves_cap, double* scores, int64_t scores_cap, void* stream) {
   try {
@@ -671,6 +743,7 @@ int pgr_kv_step_stats(void* kv, pgr_kv_step_stats_t* out) {
     out->chunks = s.chunks;
     out->launches = s.launches;
     out->work_items = s.work_items;
+    out->gather_blocks = s.gather_blocks;
     return pgr::kOk;
   } catch (...) {
     return exception_status();
@@ -702,6 +775,21 @@ int pgr_kv_resident_bytes(void* kv, int64_t* gpu, int64_t* cpu) {
     if (!kv || !gpu || !cpu) return set_err(pgr::kErrInvalid, "null pointer");
     *gpu = kv_of(kv)->resident_gpu_bytes();
     *cpu = kv_of(kv)->resident_cpu_bytes();
+    return pgr::kOk;
+  } catch (...) {
+    return exception_status();
+  }
+}
+
+int pgr_kv_hbm_bytes(void* kv, int64_t* out) {
+  try {
+    if (!kv || !out) return set_err(pgr::kErrInvalid, "null pointer");
+    const pgr::HbmBytes h = kv_of(kv)->hbm_bytes();
+    out[0] = h.pool;
+    out[1] = h.mirror;
+    out[2] = h.staging;
+    out[3] = h.workspace;
+    out[4] = h.total;
     return pgr::kOk;
   } catch (...) {
     return exception_status();

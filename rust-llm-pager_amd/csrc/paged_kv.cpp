@@ -11,6 +11,7 @@
 #include "paged_kv.h"
 
 #include <algorithm>
+#include <chrono>
 #include <cstring>
 
 #include "pager_core.h"
@@ -19,6 +20,13 @@
 namespace pgr {
 
 namespace {
+
+// Deferred block mass holds one [S][Hq][stride] share per layer; steps that would need more
+// than this many floats reduce the mass per layer instead.
+constexpr size_t kMassDeferredMaxFloats = (size_t)16 << 20;
+// Longest wait of the mirror thread for one release word before it stops queueing copies for
+// the step (the layers after it then read the host in place after their bounded wait).
+constexpr std::chrono::seconds kReleaseWaitLimit(10);
 
 // V chunk c (16 bytes) of a record's V region holds dims d0, d0 + 1 of four consecutive tokens
 // (v_record_index): tile `tile` of head `h`, tokens 16 tile + 4g .. + 3. Maps c to those.
@@ -181,6 +189,11 @@ hipError_t HostWorker::wait() {
   return r;
 }
 
+bool HostWorker::busy() {
+  std::lock_guard<std::mutex> lk(mu_);
+  return pending_;
+}
+
 void HostWorker::stop() {
   {
     std::lock_guard<std::mutex> lk(mu_);
@@ -208,9 +221,22 @@ void HostWorker::run() {
 PagedKV::PagedKV(const PagedKVConfig& cfg) : cfg_(cfg) {}
 
 PagedKV::~PagedKV() {
-  mirror_issuer_.stop();  // its last job queues work on the copy stream and records mirror_done_
+  // The mirror thread's copies are drained before the thread ends. Ended first, the thread
+  // left its last DMA copies in flight: an async-copy tracer (rocprofv3 --memory-copy-trace)
+  // then never delivered their completions (it retired the thread's correlation ids as
+  // dangling at exit) and its exit-time teardown crashed in __cxa_finalize. So: stop a job
+  // still waiting for a release, wait for it, have the thread itself wait for its copies,
+  // then end it.
+  mirror_cancel_ = true;
+  mirror_issuer_.wait();
+  if (mirror_issuer_.started() && copy_stream_) {
+    hipStream_t cs = copy_stream_;
+    mirror_issuer_.submit([cs]() { return hipStreamSynchronize(cs); });
+    mirror_issuer_.wait();
+  }
   if (copy_stream_) hipStreamSynchronize(copy_stream_);
   hipDeviceSynchronize();
+  mirror_issuer_.stop();
   for (void* p : pool_)
     if (p) hipFree(p);
   for (void* p : host_)
@@ -243,9 +269,11 @@ PagedKV::~PagedKV() {
   if (cap_fork_) hipEventDestroy(cap_fork_);
   if (mirror_go_) hipEventDestroy(mirror_go_);
   if (mirror_done_) hipEventDestroy(mirror_done_);
-  for (void* p : mirror_)
+  for (void* p : ring_)
     if (p) hipFree(p);
   if (mirror_flags_) hipFree(mirror_flags_);
+  if (mirror_release_) hipHostFree(mirror_release_);
+  if (mass_w_) hipFree(mass_w_);
   if (stage_copies_done_) hipEventDestroy(stage_copies_done_);
   if (moves_done_) hipEventDestroy(moves_done_);
   if (decode_done_) hipEventDestroy(decode_done_);
@@ -361,11 +389,16 @@ int PagedKV::init() {
   // and the copy kernels read and write the host mirror in place.
   if (cfg_.stream_mode == 1) PGR_HIP(hipMalloc(&stage_, rec * (size_t)cfg_.staging_slots * cfg_.staging_buffers));
   if (cfg_.stream_mode == 2) {
-    mirror_.assign(cfg_.num_layers, nullptr);
-    for (int l = 0; l < cfg_.num_layers; ++l)
-      if (cfg_.host_records > 0) PGR_HIP(hipMalloc(&mirror_[l], rec * (size_t)cfg_.host_records));
+    // The ring: one buffer per layer up to staging_buffers, each grown by begin_step to the
+    // step's host share of a layer.
+    ring_.assign(std::min(cfg_.staging_buffers, cfg_.num_layers), nullptr);
+    ring_records_ = cfg_.staging_slots;
+    for (void*& b : ring_) PGR_HIP(hipMalloc(&b, rec * (size_t)ring_records_));
     PGR_HIP(hipMalloc(reinterpret_cast<void**>(&mirror_flags_), 256 * sizeof(uint32_t)));
     PGR_HIP(hipMemset(mirror_flags_, 0, 256 * sizeof(uint32_t)));
+    PGR_HIP(hipHostMalloc(reinterpret_cast<void**>(&mirror_release_), 256 * sizeof(uint32_t), hipHostMallocDefault));
+    std::memset(mirror_release_, 0, 256 * sizeof(uint32_t));
+    PGR_HIP(hipHostGetDevicePointer(reinterpret_cast<void**>(&mirror_release_dev_), mirror_release_, 0));
   }
   PGR_HIP(hipStreamCreateWithFlags(&copy_stream_, hipStreamNonBlocking));
   buf_free_.resize(cfg_.staging_buffers);
@@ -754,7 +787,7 @@ int PagedKV::get_block(int sid, int64_t block_id, void* key, void* value, hipStr
   const int64_t T = cfg_.tokens_per_block;
   if (block_id < 0 || block_id >= s.n_tokens / T) return fail(kErrKey, "block is not a registered full block");
   if (int rc0 = order_after_moves(stream); rc0 != kOk) return rc0;
-  const bool on_gpu = s.on_gpu[block_id] != 0;
+  const bool on_gpu = s.slot[block_id * s.rows] >= 0;  // where the bytes are
   // Record index per row: pool slots, or host mirror records read in place.
   IndexBuf* ib = nullptr;
   int rc = acquire_index_buf((size_t)s.rows, &ib);
@@ -781,38 +814,51 @@ double PagedKV::ram_usage_ratio() const {
   return (double)cpu_bytes_ / (double)ram_budget_;
 }
 
-int PagedKV::move_block(Session& s, int64_t b, bool to_gpu, hipStream_t) {
-  // Record copies are collected here and issued by apply_tiers in one launch per direction.
+int PagedKV::load_block(Session& s, int64_t b) {
   const size_t rec = rec_bytes();
   for (int r = 0; r < s.rows; ++r) {
     const size_t k = (size_t)b * s.rows + r;
-    if (to_gpu) {
-      const int sl = alloc_slot();
-      if (sl < 0) return fail(kErrCapacity, "HBM pool exhausted while loading a block");
-      s.slot[k] = sl;
-      if (s.host_valid[k]) {
-        load_pairs_.push_back(s.row[r].host_off + b);
-        load_pairs_.push_back(sl);
-        stats_.load_bytes_copied += rec * cfg_.num_layers;
-      }
-    } else {
-      const int32_t sl = s.slot[k];
-      if (sl >= 0) {
-        if (!s.host_valid[k]) {
-          evict_pairs_.push_back(sl);
-          evict_pairs_.push_back(s.row[r].host_off + b);
-          stats_.evict_bytes_copied += rec * cfg_.num_layers;
-          s.host_valid[k] = 1;
+    if (s.slot[k] >= 0) continue;
+    const int sl = alloc_slot();
+    if (sl < 0) {
+      for (int q = 0; q < r; ++q) {  // leave the block wholly on the host side
+        const size_t kq = (size_t)b * s.rows + q;
+        free_slot(s.slot[kq]);
+        s.slot[kq] = -1;
+        if (s.host_valid[kq]) {
+          load_pairs_.resize(load_pairs_.size() - 2);
+          stats_.load_bytes_copied -= rec * cfg_.num_layers;
         }
-        // Recycled only by work queued after this call's copies on the caller's stream; a
-        // load of this same call that takes the slot is copied after the evictions.
-        free_slot(sl);
-        s.slot[k] = -1;
       }
+      return fail(kErrCapacity, "HBM pool exhausted while loading a block");
+    }
+    s.slot[k] = sl;
+    if (s.host_valid[k]) {
+      load_pairs_.push_back(s.row[r].host_off + b);
+      load_pairs_.push_back(sl);
+      stats_.load_bytes_copied += rec * cfg_.num_layers;
     }
   }
-  s.on_gpu[b] = to_gpu ? 1 : 0;
   return kOk;
+}
+
+void PagedKV::evict_block(Session& s, int64_t b) {
+  const size_t rec = rec_bytes();
+  for (int r = 0; r < s.rows; ++r) {
+    const size_t k = (size_t)b * s.rows + r;
+    const int32_t sl = s.slot[k];
+    if (sl < 0) continue;
+    if (!s.host_valid[k]) {
+      evict_pairs_.push_back(sl);
+      evict_pairs_.push_back(s.row[r].host_off + b);
+      stats_.evict_bytes_copied += rec * cfg_.num_layers;
+      s.host_valid[k] = 1;
+    }
+    // Recycled only by work queued after this call's copies on the caller's stream; a load
+    // of this same call that takes the slot is copied after the evictions.
+    free_slot(sl);
+    s.slot[k] = -1;
+  }
 }
 
 int PagedKV::apply_tiers(int sid, const uint8_t* tiers, int64_t n_tiers, int64_t* to_gpu, int64_t* n_gpu,
@@ -835,26 +881,36 @@ int PagedKV::apply_tiers(int sid, const uint8_t* tiers, int64_t n_tiers, int64_t
   if (int rc0 = order_after_decode(stream); rc0 != kOk) return rc0;
   evict_pairs_.clear();
   load_pairs_.clear();
+  // Logical pass, ascending by id as kv_block_store.py:216-226: the move lists, the byte
+  // accounting and the RAM-budget check (which stops the pass, moves before it stay).
+  std::vector<int64_t> evict, load, first_gpu;  // physical work, done below
   int rc = kOk;
   for (int64_t b = 0; b < n_full; ++b) {
     const int desired = b < n_tiers ? tiers[b] : 2;
+    const bool phys_gpu = s.slot[(size_t)b * s.rows] >= 0;
     if (desired == 0 && !s.on_gpu[b]) {
-      rc = move_block(s, b, true, stream);
-      if (rc != kOk) break;
-      if (s.placed[b]) cpu_bytes_ -= bb;
+      if (s.placed[b]) {
+        cpu_bytes_ -= bb;
+        load.push_back(b);
+      } else {
+        first_gpu.push_back(b);  // a prompt block's first place: HBM
+      }
       s.placed[b] = 1;
+      s.on_gpu[b] = 1;
       gpu_bytes_ += bb;
       stats_.cpu_to_gpu_bytes += bb;
       stats_.cpu_to_gpu_copies += 1;
       to_gpu[(*n_gpu)++] = b;
+    } else if (desired == 0 && !phys_gpu) {
+      load.push_back(b);  // placed in HBM while its bytes sat on the host: loaded now
     } else if (desired != 0 && s.on_gpu[b]) {
       if (ram_budget_ >= 0 && cpu_bytes_ + bb > ram_budget_) {
         *fail_block = b;
         rc = fail(kErrBudget, "ram_budget exceeded");
         break;
       }
-      rc = move_block(s, b, false, stream);
-      if (rc != kOk) break;
+      if (phys_gpu) evict.push_back(b);
+      s.on_gpu[b] = 0;
       cpu_bytes_ += bb;
       gpu_bytes_ -= bb;
       stats_.gpu_to_cpu_bytes += bb;
@@ -868,9 +924,28 @@ int PagedKV::apply_tiers(int sid, const uint8_t* tiers, int64_t n_tiers, int64_t
         rc = fail(kErrBudget, "ram_budget exceeded");
         break;
       }
+      if (phys_gpu) evict.push_back(b);
       cpu_bytes_ += bb;
       s.placed[b] = 1;
     }
+  }
+  // Physical pass: evictions first, so that loads may take the slots they free; then the
+  // loads; then HBM slots for prompt blocks placed in HBM for the first time, the most recent
+  // first, as long as the pool keeps one slot per row for the next open block. A prompt block
+  // left without a slot stays logically in HBM with its bytes on the host (read from there)
+  // until a later placement loads or evicts it.
+  for (int64_t b : evict) evict_block(s, b);
+  for (int64_t b : load) {
+    const int lrc = load_block(s, b);
+    if (lrc != kOk) {
+      if (rc == kOk) rc = lrc;
+      break;
+    }
+  }
+  for (auto it = first_gpu.rbegin(); rc == kOk && it != first_gpu.rend(); ++it) {
+    if ((int64_t)free_slots_.size() < 2 * (int64_t)s.rows) break;
+    if (s.slot[(size_t)*it * s.rows] >= 0) continue;
+    if (load_block(s, *it) != kOk) break;
   }
   // Evictions first: a load may reuse a slot an eviction of this call freed.
   bool launched = false;
@@ -963,6 +1038,9 @@ int PagedKV::begin_step(const int32_t* sids, int n, hipStream_t stream) {
   std::vector<Pending> pend;
   std::vector<int32_t> append_slot, append_pos;  // per sequence: record and offset of the current token
   const int64_t chunk_cap = cfg_.staging_slots;
+  int64_t mirror_ring_used = 0;          // mirror mode: ring records taken by the spans so far
+  std::vector<int32_t> seq_mirror_off;   // per sequence: host record - ring record
+  ++step_token_;
   int64_t used_in_chunk = 0;
   int chunk = 0;
   int max_mass = 1;
@@ -980,11 +1058,16 @@ int PagedKV::begin_step(const int32_t* sids, int n, hipStream_t stream) {
       const int64_t first_blk = std::min<int64_t>(std::max<int64_t>(si.lo, 0) / T, n_full);
       si.mass_lo = (int32_t)first_blk;
       si.session = i;
+      si.step_token = step_token_;
       seqs_.push_back(si);
       append_slot.push_back(s.slot[(p / T) * s.rows + r]);
       append_pos.push_back((int32_t)(p % T));
       max_mass = std::max<int>(max_mass, (int)n_full);
+      // The gather list: blocks on the host tier (logical residency, paged_model.py:907-916).
       std::vector<int64_t> host_ids;
+      for (int64_t x = first_blk; x < n_full; ++x)
+        if (!s.on_gpu[x]) host_ids.push_back(x);
+      step_stats_.gather_blocks += (int64_t)host_ids.size();
       int64_t span_lo = -1, span_hi = -1;  // mirror mode: this row's host records to copy
       int64_t b = first_blk;
       while (b < n_full) {
@@ -997,10 +1080,8 @@ int PagedKV::begin_step(const int32_t* sids, int n, hipStream_t stream) {
         }
         int64_t e = b;
         while (e < n_full && s.slot[e * s.rows + r] < 0) ++e;
-        for (int64_t x = b; x < e; ++x) {
+        for (int64_t x = b; x < e; ++x)
           if (!s.host_valid[x * s.rows + r]) return fail(kErrState, "host block without data (not imported)");
-          host_ids.push_back(x);
-        }
         if (cfg_.stream_mode != 1) {  // direct and mirror: the kernel reads host record indices
           for (int64_t x = b; x < e; ++x)
             pend.push_back({seq, BlockEntry{(int32_t)(-(s.row[r].host_off + x) - 1), (int32_t)x}, 0});
@@ -1036,7 +1117,15 @@ int PagedKV::begin_step(const int32_t* sids, int n, hipStream_t stream) {
         pend.push_back({seq, BlockEntry{s.slot[(p / T) * s.rows + r], (int32_t)(p / T)}, 0});
       step_stats_.resident_tokens += p % T + 1;  // stored part of the open block + the current token
       step_host_ids_.push_back(std::move(host_ids));
-      if (span_lo >= 0) mirror_spans_.push_back({span_lo, span_hi - span_lo});
+      // Mirror mode: the row's span is packed into the ring buffers after the spans before it;
+      // its host record h then sits at ring record h - mirror_off.
+      int32_t moff = 0;
+      if (span_lo >= 0) {
+        moff = (int32_t)(span_lo - mirror_ring_used);
+        mirror_ring_used += span_hi - span_lo;
+        mirror_spans_.push_back({span_lo, span_hi - span_lo});
+      }
+      seq_mirror_off.push_back(moff);
     }
   }
   const bool any_host = !copies_.empty();
@@ -1075,6 +1164,7 @@ int PagedKV::begin_step(const int32_t* sids, int n, hipStream_t stream) {
     w.n_mass = seqs_[seq].n_mass;
     w.append_slot = seq_wg[seq] == 0 ? append_slot[seq] : -1;
     w.append_pos = append_pos[seq];
+    w.mirror_off = seq_mirror_off[seq];
     ++seq_wg[seq];
     return w;
   };
@@ -1193,6 +1283,31 @@ int PagedKV::begin_step(const int32_t* sids, int n, hipStream_t stream) {
   const size_t o_lf = carve(sizeof(float) * (size_t)S * hq);
   int rc = ensure_workspace(off);
   if (rc != kOk) return rc;
+  // Deferred mass for steps with sessions whose pager scores by mass: one [S][Hq][stride]
+  // share per layer, cleared by each step's reduction (and zero when allocated).
+  mass_deferred_ = false;
+  mass_w_dirty_ = false;
+  {
+    bool want = false;
+    for (int i = 0; i < n; ++i) want = want || (sessions_[sids[i]].pager && sessions_[sids[i]].scores_from_mass);
+    const size_t layer_floats = (size_t)S * hq * mass_stride_;
+    const size_t total = layer_floats * cfg_.num_layers;
+    if (want && total <= kMassDeferredMaxFloats) {
+      if (total > mass_w_floats_) {
+        PGR_HIP(hipDeviceSynchronize());
+        forget_streams();
+        const size_t grow = std::max(total, mass_w_floats_ * 3 / 2);
+        if (mass_w_) PGR_HIP(hipFree(mass_w_));
+        mass_w_ = nullptr;
+        mass_w_floats_ = 0;
+        PGR_HIP(hipMalloc(reinterpret_cast<void**>(&mass_w_), grow * sizeof(float)));
+        PGR_HIP(hipMemset(mass_w_, 0, grow * sizeof(float)));
+        mass_w_floats_ = grow;
+      }
+      mass_deferred_ = true;
+      mass_layer_floats_ = layer_floats;
+    }
+  }
   // Pinned plan buffer; wait until the GPU has read it before overwriting it. With several
   // layers per step the first launch reads the plan early in its step, so one buffer holds
   // the host back by little, and a launch signature stays the same from step to step (a
@@ -1293,6 +1408,21 @@ int PagedKV::issue_mirror_copies(hipStream_t stream) {
     PGR_HIP(hipStreamWaitEvent(stream, mirror_done_, 0));
     mirror_pending_ = false;
   }
+  // Each ring buffer holds one layer's share of the step: the rows' spans, packed.
+  int64_t need = 0;
+  for (const auto& sp : mirror_spans_) need += sp.second;
+  if (need > ring_records_) {
+    PGR_HIP(hipDeviceSynchronize());
+    forget_streams();
+    const int64_t grow = std::max(need, ring_records_ * 3 / 2);
+    for (void*& b : ring_) {
+      if (b) PGR_HIP(hipFree(b));
+      b = nullptr;
+    }
+    ring_records_ = 0;
+    for (void*& b : ring_) PGR_HIP(hipMalloc(&b, rec_bytes() * (size_t)grow));
+    ring_records_ = grow;
+  }
   mirror_flags_reset_kernel<<<1, 256, 0, stream>>>(mirror_flags_, cfg_.num_layers, mirror_spans_.empty() ? 1u : 0u);
   PGR_HIP(hipGetLastError());
   mirror_step_bytes_ = 0;
@@ -1301,20 +1431,60 @@ int PagedKV::issue_mirror_copies(hipStream_t stream) {
   const size_t rec = rec_bytes();
   for (const auto& sp : mirror_spans_) mirror_step_bytes_ += (uint64_t)sp.second * rec;
   mirror_pending_ = true;
-  mirror_issuer_.submit([this, rec, spans = mirror_spans_]() -> hipError_t {
+  step_closed_ = false;
+  const uint32_t token = step_token_;
+  mirror_issuer_.submit([this, rec, token, spans = mirror_spans_, ring = ring_]() -> hipError_t {
+    const int n_ring = (int)ring.size();
     hipError_t e = hipSetDevice(device_);
     if (e == hipSuccess) e = hipStreamWaitEvent(copy_stream_, mirror_go_, 0);
     for (int l = 0; l < cfg_.num_layers && e == hipSuccess; ++l) {
-      for (size_t i = 0; i < spans.size() && e == hipSuccess; ++i)
-        e = hipMemcpyHtoDAsync(static_cast<char*>(mirror_[l]) + (size_t)spans[i].first * rec,
-                               static_cast<char*>(host_[l]) + (size_t)spans[i].first * rec,
+      // Buffer l % n was last read by layer l - n of this step: its records may be replaced
+      // once that layer's merge has published the step's token.
+      if (l >= n_ring && !wait_release(l - n_ring, token)) break;
+      char* dst = static_cast<char*>(ring[l % n_ring]);
+      int64_t at = 0;
+      for (size_t i = 0; i < spans.size() && e == hipSuccess; ++i) {
+        e = hipMemcpyHtoDAsync(dst + (size_t)at * rec, static_cast<char*>(host_[l]) + (size_t)spans[i].first * rec,
                                (size_t)spans[i].second * rec, copy_stream_);
+        at += spans[i].second;
+      }
       if (e == hipSuccess) e = hipStreamWriteValue32(copy_stream_, mirror_flags_ + l, 1u, 0);
     }
-    if (e == hipSuccess) e = hipEventRecord(mirror_done_, copy_stream_);
-    return e;
+    const hipError_t e2 = hipEventRecord(mirror_done_, copy_stream_);
+    return e != hipSuccess ? e : e2;
   });
   return kOk;
+}
+
+bool PagedKV::wait_release(int layer, uint32_t token) {
+  auto released = [&] { return (int32_t)(__atomic_load_n(mirror_release_ + layer, __ATOMIC_ACQUIRE) - token) >= 0; };
+  if (released()) return true;
+  mirror_waiting_ = 1;
+  const auto t0 = std::chrono::steady_clock::now();
+  bool ok = false;
+  for (uint64_t poll = 1;; ++poll) {
+    if (released()) {
+      ok = true;
+      break;
+    }
+#if defined(__x86_64__)
+    __builtin_ia32_pause();
+#endif
+    if ((poll & 1023) != 0) continue;
+    if (mirror_cancel_) break;
+    if (step_closed_) {
+      // The step is closed: every launch of it is queued on its decode stream. Once that has
+      // drained, a release still missing never comes (a layer that was not decoded).
+      const hipError_t q = closed_has_stream_ ? hipStreamQuery(closed_stream_.load()) : hipSuccess;
+      if (q != hipErrorNotReady) {
+        ok = released();
+        break;
+      }
+    }
+    if (std::chrono::steady_clock::now() - t0 > kReleaseWaitLimit) break;
+  }
+  mirror_waiting_ = 0;
+  return ok;
 }
 
 int PagedKV::decode_layer(int layer, const void* q, const void* k_new, const void* v_new, void* out,
@@ -1340,8 +1510,9 @@ int PagedKV::decode_layer(int layer, const void* q, const void* k_new, const voi
   pl.pool = pool_[layer];
   pl.stage = cfg_.stream_mode == 1 ? stage_ : host_dev_[layer];
   if (cfg_.stream_mode == 2) {
-    pl.mirror = mirror_[layer];
+    pl.mirror = ring_[layer % ring_.size()];
     pl.mirror_flag = mirror_flags_ + layer;
+    pl.release_flag = mirror_release_dev_ + layer;
   }
   pl.seqs = d_seqs_;
   pl.pm = d_pm_;
@@ -1472,10 +1643,21 @@ int PagedKV::decode_layer(int layer, const void* q, const void* k_new, const voi
   }
   pl.plan_flag = merge_flag;
   pl.plan_token = merge_token;
+  // Deferred mass: the merge writes this layer's block weights, the step's reduction adds
+  // them up once (end_step / end_step_place); otherwise a reduction per layer.
+  const bool deferred = mass_accum && mass_deferred_;
+  if (deferred) {
+    pl.mass_w = mass_w_ + (size_t)layer * mass_layer_floats_;
+    if (!capturing) mass_w_dirty_ = true;  // a replay marks it (step_replayed)
+  }
   PGR_HIP(launch_paged_merge(cfg_.dtype, cfg_.head_dim, pl, (int)seqs_.size(), stream));
-  if (mass_accum) {
+  if (mass_accum && !deferred) {
     PGR_HIP(launch_mass_reduce(d_seqs_, d_sess_rows_, d_sess_first_, d_mass_m_, d_mass_s_, d_mf_, d_lf_, mass_accum,
                                (int)accum_stride, hq, mass_stride_, (int)step_sids_.size(), mass_stride_, stream));
+  }
+  if (mass_accum) {
+    mass_accum_last_ = mass_accum;
+    mass_stride_last_ = accum_stride;
   }
   if (!capturing) {
     decode_stream_ = stream;
@@ -1499,6 +1681,8 @@ int PagedKV::step_replayed(hipStream_t stream) {
   decode_stream_ = stream;
   decode_pending_ = true;
   decode_waited_.clear();
+  // A graph captured with deferred mass writes the step's block weights on every replay.
+  if (mass_deferred_ && mass_accum_last_) mass_w_dirty_ = true;
   return kOk;
 }
 
@@ -1512,7 +1696,9 @@ int PagedKV::step_signature(int64_t* out, int64_t cap) const {
       (int64_t)cfg_.stream_mode, (int64_t)seqs_.size(), (int64_t)step_sids_.size(), (int64_t)mass_stride_,
       (int64_t)launch_work_begin_.size(), (int64_t)(uintptr_t)plan_bufs_[plan_buf_].dev, (int64_t)plan_on_device_,
       (int64_t)n_chunks_, (int64_t)prefetch_step_, (int64_t)(uintptr_t)d_stage_pairs_,
-      (int64_t)(uintptr_t)d_chunk_begin_};
+      (int64_t)(uintptr_t)d_chunk_begin_, (int64_t)mass_deferred_, (int64_t)(uintptr_t)mass_w_,
+      (int64_t)mass_layer_floats_, ring_records_};
+  for (void* b : ring_) v.push_back((int64_t)(uintptr_t)b);
   for (size_t L = 0; L < launch_work_begin_.size(); ++L) {
     v.push_back(launch_work_begin_[L]);
     v.push_back(launch_work_end_[L]);
@@ -1522,8 +1708,27 @@ int PagedKV::step_signature(int64_t* out, int64_t cap) const {
   return (int)v.size();
 }
 
+int PagedKV::finish_step_mass(float* mass_accum, int64_t accum_stride, hipStream_t stream) {
+  PGR_HIP(launch_mass_step_reduce(d_seqs_, d_sess_rows_, d_sess_first_, mass_w_, (int64_t)mass_layer_floats_,
+                                  cfg_.num_layers, mass_accum, (int)accum_stride, cfg_.query_heads, mass_stride_,
+                                  (int)step_sids_.size(), mass_stride_, stream));
+  // The next step's merges write the weights this launch clears: work on another stream
+  // waits for it (order_after_moves).
+  PGR_HIP(hipEventRecord(moves_done_, stream));
+  moves_stream_ = stream;
+  moves_queued_ = true;
+  moves_waited_.clear();
+  return kOk;
+}
+
 int PagedKV::end_step(int32_t* completed, int* n_completed) {
   if (!in_step_) return fail(kErrState, "end_step without begin_step");
+  if (mass_deferred_ && mass_w_dirty_ && mass_accum_last_)
+    if (int rc = finish_step_mass(mass_accum_last_, mass_stride_last_, decode_stream_); rc != kOk) return rc;
+  return close_step(completed, n_completed);
+}
+
+int PagedKV::close_step(int32_t* completed, int* n_completed) {
   const int64_t T = cfg_.tokens_per_block;
   // Host blocks read in place (direct mode) or copied to staging (staged mode) this step, every
   // layer (counted here rather than per launch, so that steps replayed from a captured graph
@@ -1548,6 +1753,11 @@ int PagedKV::end_step(int32_t* completed, int* n_completed) {
   }
   if (n_completed) *n_completed = c;
   in_step_ = false;
+  if (cfg_.stream_mode == 2) {  // the mirror thread may now tell a missing release from a late one
+    closed_has_stream_ = decode_pending_;
+    closed_stream_ = decode_stream_;
+    step_closed_ = true;
+  }
   return kOk;
 }
 
@@ -1558,7 +1768,7 @@ int PagedKV::attach_pager(int sid, PlacementPager* pager, bool scores_from_mass)
   return kOk;
 }
 
-int PagedKV::end_step_place(const float* mass_accum, int64_t accum_stride, int num_layers, hipStream_t stream,
+int PagedKV::end_step_place(float* mass_accum, int64_t accum_stride, int num_layers, hipStream_t stream,
                             int32_t* completed, int* n_completed, int64_t* counts, int64_t* moves,
                             int64_t moves_cap, double* scores, int64_t scores_cap) {
   if (!in_step_) return fail(kErrState, "end_step_place without begin_step");
@@ -1585,13 +1795,16 @@ int PagedKV::end_step_place(const float* mass_accum, int64_t accum_stride, int n
       PGR_HIP(hipHostMalloc(reinterpret_cast<void**>(&mass_host_), want * sizeof(float), hipHostMallocDefault));
       mass_host_floats_ = want;
     }
+    // The reduction reads the step's plan, which the step's first launch put on the device.
+    if (mass_deferred_ && mass_w_dirty_)
+      if (int rc = finish_step_mass(mass_accum, accum_stride, stream); rc != kOk) return rc;
     // The reference reads the mass back with .tolist() (a full sync) at this point too.
     PGR_HIP(hipMemcpyAsync(mass_host_, mass_accum, want * sizeof(float), hipMemcpyDeviceToHost, stream));
     PGR_HIP(hipStreamSynchronize(stream));
   }
   std::vector<int32_t> done(n);
   int n_done = 0;
-  int rc = end_step(done.data(), &n_done);
+  int rc = close_step(done.data(), &n_done);
   if (rc != kOk) return rc;
   if (completed)
     for (int i = 0; i < n_done; ++i) completed[i] = done[i];
@@ -1690,6 +1903,21 @@ int PagedKV::step_host_blocks(int seq_index, int64_t* out, int64_t cap) const {
   return (int)v.size();
 }
 
+HbmBytes PagedKV::hbm_bytes() const {
+  HbmBytes h;
+  const int64_t rec = (int64_t)rec_bytes();
+  for (void* p : pool_)
+    if (p) h.pool += rec * cfg_.pool_slots;
+  for (void* p : ring_)
+    if (p) h.mirror += rec * ring_records_;
+  if (stage_) h.staging = rec * cfg_.staging_slots * cfg_.staging_buffers;
+  h.workspace = (int64_t)ws_bytes_ + (int64_t)(mass_w_floats_ * sizeof(float)) +
+                (bases_dev_ ? (int64_t)(2 * cfg_.num_layers * sizeof(void*)) : 0) +
+                (mirror_flags_ ? (int64_t)(256 * sizeof(uint32_t)) : 0);
+  h.total = h.pool + h.mirror + h.staging + h.workspace;
+  return h;
+}
+
 int64_t PagedKV::resident_gpu_bytes() const { return gpu_bytes_; }
 int64_t PagedKV::resident_cpu_bytes() const { return cpu_bytes_; }
 
@@ -1752,7 +1980,13 @@ int PagedKV::kernel_time(double* ms, int64_t* launches, int64_t* bytes) {
 }
 
 int PagedKV::sync() {
-  PGR_HIP(mirror_issuer_.wait());
+  if (in_step_ && cfg_.stream_mode == 2) {
+    // In an open step the mirror job may wait for releases that launches not yet made would
+    // publish: wait until it has queued what it can.
+    while (mirror_issuer_.busy() && !mirror_waiting_) std::this_thread::yield();
+  } else {
+    PGR_HIP(mirror_issuer_.wait());
+  }
   PGR_HIP(hipStreamSynchronize(copy_stream_));
   PGR_HIP(hipDeviceSynchronize());
   forget_streams();

@@ -14,12 +14,22 @@
 //     the attention kernel in place. In the direct mode (default) the attention kernel reads
 //     host blocks straight from the mirror over the host link, and imports, exports and tier
 //     moves read and write the mirror in place through its device mapping.
+//   * Mirror ring in HBM (mirror stream mode only): min(staging_buffers, num_layers) buffers,
+//     each holding one layer's share of a step's host records (grown on demand). Layer l's
+//     records go to buffer l % n by DMA once layer l - n has released it.
 // Blocks are immutable once full, so a host copy stays valid after the block is loaded back
 // to HBM and a later eviction of it needs no copy.
+// Residency is logical (the tier the placement decided, what every move list and counter
+// reports) and physical (where the record bytes are). They agree except for prompt blocks
+// between their import and their first placement: those count as HBM-resident, as the
+// reference's initial store holds them (paged_model.py:1183-1192), but only as many as the
+// pool has room for get an HBM slot; the rest are written to the host mirror and read from
+// there, so that the pool never needs more than the placement budget.
 #pragma once
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <condition_variable>
 #include <cstdint>
 #include <functional>
@@ -44,8 +54,8 @@ struct PagedKVConfig {
   int dtype = kF16;
   int64_t pool_slots = 0;        // HBM records per layer
   int64_t host_records = 0;      // pinned host records per layer
-  int64_t staging_slots = 0;     // records per staging buffer
-  int staging_buffers = 2;       // ring depth
+  int64_t staging_slots = 0;     // records per staging buffer (mirror mode: initial records per ring buffer)
+  int staging_buffers = 2;       // ring depth (staged mode: staging buffers; mirror mode: ring buffers)
   int blocks_per_workgroup = 32; // most block entries folded by one workgroup (4 waves)
   int target_workgroups = 0;     // workgroups a launch aims for (0: a multiple of the CU count)
   int stream_mode = 0;           // 0: kernels read host blocks in place; 1: staged copies; 2: HBM mirror
@@ -66,11 +76,21 @@ struct StoreStats {
 struct StepStats {
   int64_t resident_tokens = 0;  // in-scope tokens read from the HBM pool (incl. the open block)
   int64_t host_tokens = 0;      // in-scope tokens streamed from host (whole blocks)
-  int64_t host_blocks = 0;
+  int64_t host_blocks = 0;      // (block, row) records read from the host tier (physical residency)
   int64_t copies = 0;           // H2D copy calls per layer
   int64_t chunks = 0;
   int64_t launches = 0;         // attention kernel launches per layer
   int64_t work_items = 0;
+  int64_t gather_blocks = 0;    // (block, row) entries of the gather lists (logical host residency)
+};
+
+// Device memory a store holds, in bytes.
+struct HbmBytes {
+  int64_t pool = 0;       // HBM slot pools, all layers
+  int64_t mirror = 0;     // mirror-mode ring buffers
+  int64_t staging = 0;    // staged-mode staging buffers
+  int64_t workspace = 0;  // step plan, split-K partials, block mass
+  int64_t total = 0;
 };
 
 // One host thread that runs submitted jobs one at a time: here, the HIP calls that queue a
@@ -87,6 +107,8 @@ class HostWorker {
   void submit(std::function<hipError_t()> job);
   // Returns once the submitted job (if any) has run, with its result; hipSuccess if none.
   hipError_t wait();
+  bool started() const { return thread_.joinable(); }
+  bool busy();  // a submitted job has not finished
   void stop();  // runs a submitted job to its end, then ends the thread
 
  private:
@@ -167,7 +189,7 @@ class PagedKV {
   // moves gets each session's to-HBM then to-host ids, scores the values handed to the
   // pager (before f32 rounding); both may be null.
   int attach_pager(int sid, PlacementPager* pager, bool scores_from_mass);
-  int end_step_place(const float* mass_accum, int64_t accum_stride, int num_layers, hipStream_t stream,
+  int end_step_place(float* mass_accum, int64_t accum_stride, int num_layers, hipStream_t stream,
                      int32_t* completed, int* n_completed, int64_t* counts, int64_t* moves, int64_t moves_cap,
                      double* scores, int64_t scores_cap);
 
@@ -180,6 +202,7 @@ class PagedKV {
   int64_t block_bytes_all_layers(int sid) const;
   int64_t resident_gpu_bytes() const;
   int64_t resident_cpu_bytes() const;
+  HbmBytes hbm_bytes() const;
 
   // Optional timing of the attention launches (HIP events on the compute stream).
   void set_timing(bool on) { timing_ = on; }
@@ -230,8 +253,19 @@ class PagedKV {
   int ensure_workspace(size_t bytes);
   int default_workgroups() const;
   int ensure_block_capacity(Session& s, int64_t blocks);
-  int move_block(Session& s, int64_t b, bool to_gpu, hipStream_t stream);
+  // Physical moves of block b (every row): into HBM slots (a load, copied from the host
+  // record if that holds data) or out of them (an eviction, copied to the host record unless
+  // that holds the data already). The copies are collected and issued by apply_tiers.
+  int load_block(Session& s, int64_t b);
+  void evict_block(Session& s, int64_t b);
   int resolve_timing();
+  // Block mass of a step run with deferred mass (sessions whose pager scores by mass): each
+  // layer's merge writes that layer's normalized per-block weights into mass_w_; one launch
+  // at the end of the step averages them over rows and heads, adds them up over the layers
+  // in layer order into mass_accum, and clears mass_w_ for the next step.
+  int finish_step_mass(float* mass_accum, int64_t accum_stride, hipStream_t stream);
+  // Closes the open step (every session grows by one token).
+  int close_step(int32_t* completed, int* n_completed);
   // Record index lists for the copy kernels live in pinned host memory that the kernels read
   // in place, in a small ring so a list is not overwritten while a queued kernel still
   // needs it.
@@ -322,20 +356,47 @@ class PagedKV {
   // before a replay precedes the whole graph on its stream.
   hipEvent_t cap_fork_ = nullptr;
   bool cap_forked_ = false;
-  // Mirror mode: per layer an HBM copy of the host records, filled by DMA on copy_stream_ at
-  // begin_step; mirror_flags_[l] (device words) is set once layer l's copies have landed.
-  std::vector<void*> mirror_;
+  // Mirror mode: a ring of HBM buffers; layer l's share of the step's host records goes to
+  // ring_[l % ring_.size()] by DMA on copy_stream_, and mirror_flags_[l] (device words) is
+  // set once it has landed. The merge launch of layer l stores the step's token into
+  // mirror_release_[l] (pinned): the attention launch of layer l, the buffer's reader, has
+  // finished, so the copies of layer l + ring_.size() may overwrite it.
+  std::vector<void*> ring_;
+  int64_t ring_records_ = 0;  // records per ring buffer
   uint32_t* mirror_flags_ = nullptr;
+  uint32_t* mirror_release_ = nullptr;      // pinned, one word per layer
+  uint32_t* mirror_release_dev_ = nullptr;  // its device mapping
+  uint32_t step_token_ = 0;                 // token of the open (or last) step
   hipEvent_t mirror_go_ = nullptr;    // on the step's stream, after the flags are cleared
   hipEvent_t mirror_done_ = nullptr;  // on copy_stream_, after the step's copies
   bool mirror_pending_ = false;
-  // Issues the mirror copies and word writes of a step (about 0.25 ms of HIP calls for 22
-  // layers) while begin_step returns. issue_mirror_copies waits for its previous job before
-  // it records or waits on mirror_go_ / mirror_done_ again, and so do sync() and the
-  // destructor before they drain the copy stream.
+  // Issues the mirror copies and word writes of a step while begin_step returns: a layer's
+  // copies once the layer n before it has released its buffer (a host-side wait on the
+  // release word), so the thread runs beside the step's launches. issue_mirror_copies waits
+  // for its previous job before it records or waits on mirror_go_ / mirror_done_ again, and
+  // so do sync() and the destructor before they drain the copy stream.
   HostWorker mirror_issuer_;
+  // The job gives up waiting for a release (it then queues no further copies of the step;
+  // those layers read the host in place after their bounded wait) when the store is being
+  // destroyed (mirror_cancel_), or when the step is closed and its decode stream has drained
+  // without the release (a layer that was not decoded), or after kReleaseWaitLimit.
+  std::atomic<bool> mirror_cancel_{false};
+  std::atomic<bool> step_closed_{false};
+  std::atomic<bool> closed_has_stream_{false};
+  std::atomic<hipStream_t> closed_stream_{nullptr};
+  std::atomic<int> mirror_waiting_{0};  // the job is waiting for a release
+  // Returns true once mirror_release_[layer] holds `token` (or later), false to give up.
+  bool wait_release(int layer, uint32_t token);
   std::vector<std::pair<int64_t, int64_t>> mirror_spans_;  // (first host record, count) per row
   uint64_t mirror_step_bytes_ = 0;                         // bytes copied per layer this step
+  // Deferred block mass (see finish_step_mass).
+  float* mass_w_ = nullptr;
+  size_t mass_w_floats_ = 0;
+  bool mass_deferred_ = false;         // the open step runs with deferred mass
+  bool mass_w_dirty_ = false;          // a merge of the open step may have written mass_w_
+  float* mass_accum_last_ = nullptr;   // mass_accum of the last decode_layer call
+  int64_t mass_stride_last_ = 0;
+  size_t mass_layer_floats_ = 0;       // floats of one layer's share of mass_w_ in the open step
   std::vector<char> buf_free_cap_;
   std::vector<char> buf_free_eager_;
   std::vector<int32_t> free_slots_;

@@ -49,6 +49,10 @@ struct WorkItem {
   int32_t n_mass;       // blocks below this id get a mass entry
   int32_t append_slot;  // >= 0 (one work item per sequence): write the current token's K/V to
   int32_t append_pos;   // position append_pos of pool record append_slot
+  // Mirror mode: host record r of this sequence sits at record r - mirror_off of the layer's
+  // ring buffer (the step's host span of each row is packed there); 0 in the other modes.
+  int32_t mirror_off;
+  int32_t pad_[3];
   BlockEntry entries[kMaxWorkEntries];
 };
 
@@ -61,7 +65,7 @@ struct SeqInfo {
   int32_t partial_base;  // first partial slot of this sequence
   int32_t partial_count; // number of partial slots (work items) of this sequence
   int32_t session;       // session index (rows of one session share placement and mass)
-  int32_t pad_;
+  uint32_t step_token;   // the step's number (mirror mode: the merge publishes it per layer)
 };
 
 inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }

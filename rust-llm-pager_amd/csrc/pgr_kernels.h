@@ -42,6 +42,10 @@ struct DenseLaunch {
   int wave_tokens, n_split;
   int tokens_per_block, max_blocks, block_id_offset;
   float scale, softcap;
+  // Optional timing events recorded right before and after the attention launch (not the
+  // merge): the fold kernel's own duration for measurement.
+  hipEvent_t ev_start = nullptr;
+  hipEvent_t ev_stop = nullptr;
 };
 
 // The paged decode kernels of one layer. launch_paged folds work items [work, work + n_work)
@@ -82,6 +86,14 @@ struct PagedLaunch {
   // the step's plan buffer, have finished.
   uint32_t* plan_flag = nullptr;
   uint32_t plan_token = 0;
+  // Merge launch, mirror mode: the merge stores the step's token (SeqInfo::step_token) to
+  // *release_flag (pinned host memory) as it starts: the layer's attention launches, the
+  // readers of its ring buffer, have finished.
+  uint32_t* release_flag = nullptr;
+  // Merge launch, deferred mass: the merge writes s_b * 2^(m_b - m_final) / l_final of every
+  // in-scope block of its (sequence, query head) to mass_w[(seq * Hq + head) * mass_stride + b]
+  // instead of a mass_reduce launch per layer.
+  float* mass_w = nullptr;
 };
 
 // Head dims of the MFMA dense kernel (32, 64, 128).
@@ -106,6 +118,13 @@ hipError_t launch_mass_reduce(const SeqInfo* seqs, const int32_t* session_rows, 
                               const float* mass_m, const float* mass_s, const float* mf, const float* lf,
                               float* mass_accum, int accum_stride, int hq, int mass_stride, int n_sessions,
                               int max_blocks, hipStream_t stream);
+// Deferred mass, once per step: for each session and block, over layers 0..num_layers-1 in
+// order, adds the mean over the session's rows and query heads of mass_w[layer] into
+// mass_accum, and clears the mass_w entries it reads.
+hipError_t launch_mass_step_reduce(const SeqInfo* seqs, const int32_t* session_rows, const int32_t* session_first,
+                                   float* mass_w, int64_t layer_floats, int num_layers, float* mass_accum,
+                                   int accum_stride, int hq, int mass_stride, int n_sessions, int max_blocks,
+                                   hipStream_t stream);
 
 // kv_kernels.hip
 // Reference block layout <-> pool records for one layer:

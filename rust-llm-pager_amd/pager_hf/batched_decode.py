@@ -81,10 +81,11 @@ class BatchedPagedEngine:
         device = next(model.parameters()).device
         self.device = device
         vram_blocks = max(1, vram_budget_per_session // BLOCK_SIZE_BYTES)
-        ctx_blocks = -(-max_context_tokens // T) + 2
-        # HBM: every session's budget plus its open block, and one fresh session's whole prompt
-        # (resident until its first step places it).
-        pool = max_sessions * (vram_blocks + 2) + ctx_blocks + 16
+        # HBM: every session's budget plus its open block and a block completed in a step before
+        # its placement. A fresh session's prompt needs no room of its own: its blocks count as
+        # HBM-resident until the first placement, but only those the pool has room for get a
+        # slot (the others are read from their host records until then).
+        pool = max_sessions * (vram_blocks + 2) + 16
         host_tokens = host_token_capacity if host_token_capacity is not None else max_sessions * max_context_tokens
         host = -(-host_tokens // T) + max_sessions * 2
         self.decoder = PagedDecoder(

@@ -1,16 +1,16 @@
 """Python handle of the native paged KV store (``pgr_kv_*`` in include/pgr.h).
 
 One NativeKVPool owns, for every layer, an HBM slot pool and a pinned host mirror (plus an HBM
-staging ring in the staged mode, or an HBM copy of the host mirror per layer in the mirror
-mode), and the per-session block tables. ``stream_mode="direct"`` (default) has the
-decode kernel read host-resident blocks in place over the host link; ``"staged"`` copies
-them into the staging ring first (and, when one buffer holds a layer's host blocks, queues
-the next layer's copies under the current layer); ``"mirror"`` keeps an HBM mirror of every
-layer's host records, refilled by DMA copies that begin_step queues on a side stream for the
-whole step, and the decode kernel of a layer waits for that layer's copies and reads the
-mirror (or the host in place, if they have not landed within its bounded wait). Sessions are
-groups of rows that share one
-placement (the reference's one-PagedModel-per-session model, kv_block_store.py:36-56).
+staging ring in the staged mode, or a ring of HBM buffers in the mirror mode), and the
+per-session block tables. ``stream_mode="direct"`` (default) has the decode kernel read
+host-resident blocks in place over the host link; ``"staged"`` copies them into the staging
+ring first (and, when one buffer holds a layer's host blocks, queues the next layer's copies
+under the current layer); ``"mirror"`` copies each layer's host share of the step by DMA on a
+side stream into a ring of ``staging_buffers`` HBM buffers (layer l into buffer l % n, once
+layer l - n has finished reading it), and the decode kernel of a layer waits for that layer's
+copies and reads the buffer (or the host in place, if they have not landed within its bounded
+wait). Sessions are groups of rows that share one placement (the reference's
+one-PagedModel-per-session model, kv_block_store.py:36-56).
 """
 from __future__ import annotations
 
@@ -290,6 +290,12 @@ class NativeKVPool:
         g, c = ctypes.c_int64(0), ctypes.c_int64(0)
         nat.check(self.lib.pgr_kv_resident_bytes(self.handle, ctypes.byref(g), ctypes.byref(c)), "resident_bytes")
         return g.value, c.value
+
+    def hbm_bytes(self) -> dict:
+        """Device memory the store holds: {pool, mirror, staging, workspace, total} in bytes."""
+        arr = (ctypes.c_int64 * 5)()
+        nat.check(self.lib.pgr_kv_hbm_bytes(self.handle, arr), "hbm_bytes")
+        return dict(zip(("pool", "mirror", "staging", "workspace", "total"), (int(x) for x in arr)))
 
     def block_bytes(self, sid: int) -> int:
         b = ctypes.c_int64(0)

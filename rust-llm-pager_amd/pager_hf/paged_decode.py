@@ -163,7 +163,10 @@ class PagedDecoder:
         With place=True the pager places the blocks right away (on_step over a uniform score
         then force_rebalance, as a first decode step would) so that host blocks are streamed
         from the first step; with place=False every full block starts in HBM, like the
-        reference's initial store (paged_model.py:1183-1192).
+        reference's initial store (paged_model.py:1183-1192): logically, that is. Only as many
+        as the HBM pool has room for (keeping two slots per row free) get a slot, the most
+        recent first; the others are written to their host records and read from there until
+        the first placement loads or evicts them (pgr_kv_apply_tiers).
         """
         s = self.sessions[sid]
         self.pool.set_length(sid, n_tokens)
@@ -271,11 +274,13 @@ class PagedDecoder:
         sids = self._step
         blocks_after = [n + 1 for n in self._n_mass]  # upper bound on full blocks after the step
         cap = sum(blocks_after)
-        rc, completed, rows, moves, scores = self.pool.end_step_place(
-            len(sids), self._mass, self.num_layers, cap, cap if collect else 0
-        )
-        self._step = None
-        self._mass = None
+        try:  # the native call closes the step even when placement then fails
+            rc, completed, rows, moves, scores = self.pool.end_step_place(
+                len(sids), self._mass, self.num_layers, cap, cap if collect else 0
+            )
+        finally:
+            self._step = None
+            self._mass = None
         if rc != 0:
             bad = next(r[3] for r in rows if r[3] >= 0)
             raise RuntimeError(f"ram_budget exceeded: moving block {bad} to CPU")

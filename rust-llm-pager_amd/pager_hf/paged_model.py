@@ -46,6 +46,7 @@ logger = logging.getLogger(__name__)
 
 _ATTN_IMPL = "pgr_paged_decode"
 _POLICIES_WITHOUT_ATTENTION_SIGNAL = frozenset({"recent_only", "sinks_recent"})  # paged_model.py:40
+_PAGER_BLOCK_BYTES = 16 * 1024 * 1024  # the pager's logical block size (core.rs:6)
 _SUPPORTED_MODEL_TYPES = frozenset({"llama", "mistral", "qwen2", "qwen2_moe", "qwen3", "starcoder2", "gemma", "gemma2",
                                     "phi3"})
 # Model types whose every layer attends within config.sliding_window (when set): the blocks
@@ -445,22 +446,33 @@ class PagedModel:
         return cfg.num_hidden_layers, num_heads, num_kv, head_dim, window
 
     def _start_session(self, input_ids: torch.Tensor, attention_mask: torch.Tensor, max_new_tokens: int) -> None:
-        """paged_model.py:672-689: prefill all but the last token, store every full block in HBM."""
+        """paged_model.py:672-689: prefill all but the last token; every full block counts as
+        HBM-resident until the first placement, as in the reference's initial store.
+
+        The HBM pool holds the placement budget (vram_budget / 16 MiB blocks per row, the
+        pager's own bound, core.rs:185-186) plus the open block and a block completed in the
+        step before its placement: the reference frees a block's GPU memory when it offloads
+        it (kv_block_store.py:110-111), so its VRAM budget bounds its GPU memory. Prompt
+        blocks beyond the pool's room are written to their host records and read from there
+        until the first placement loads or evicts them."""
         layers, hq, hkv, d, _ = self._model_geometry()
         rows, total = input_ids.shape
         T = self.tokens_per_block
         n_prefix = total - 1
         capacity = max(self.max_context_tokens or 0, total + max_new_tokens + T)
         blocks = -(-capacity // T) + 2
+        budget_blocks = int(self._pager_kwargs["vram_budget"]) // _PAGER_BLOCK_BYTES
         dtype = next(self.model.parameters()).dtype
         device = input_ids.device
         # Staged mode: each buffer holds a whole layer's host blocks, so every step streams
         # one chunk per layer and queues the next layer's copies under the current layer.
+        # Mirror mode: three ring buffers, grown to a layer's host share by the first step.
         dec = PagedDecoder(
             num_layers=layers, num_query_heads=hq, num_kv_heads=hkv, head_dim=d, tokens_per_block=T, dtype=dtype,
-            device=device, pool_blocks=rows * blocks, host_blocks=rows * blocks,
+            device=device, pool_blocks=rows * (budget_blocks + 2), host_blocks=rows * blocks,
             staging_blocks=rows * blocks if self.stream_mode == "staged" else 64,
-            staging_buffers=2, ram_budget_bytes=self._ram_budget, stream_mode=self.stream_mode,
+            staging_buffers=3 if self.stream_mode == "mirror" else 2, ram_budget_bytes=self._ram_budget,
+            stream_mode=self.stream_mode,
         )
         pads = (attention_mask.shape[1] - attention_mask.long().sum(dim=1)).tolist()
         sid = dec.add_session(capacity_tokens=capacity, rows=rows, lo=pads, **self._pager_kwargs)
@@ -557,7 +569,7 @@ class PagedModel:
         dec.begin_step([sid])
         if position_ids is None:
             position_ids = self._position_ids_from_mask(current_attention_mask)[:, -1:]
-        host_blocks = dec.pool.step_stats()["host_blocks"]
+        host_blocks = dec.pool.step_stats()["gather_blocks"]  # blocks gathered from the host tier
         try:
             if self.use_hip_graphs:
                 logits = self._graph_forward(input_id_tensor, position_ids)

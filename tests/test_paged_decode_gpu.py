@@ -260,11 +260,13 @@ def test_staged_layers_prefetch_and_chunks(staging_blocks, staging_buffers, orde
     assert len(errs) == 8
 
 
-@pytest.mark.parametrize("mode,layers", [("direct", 1), ("direct", 2), ("staged", 2)])
+@pytest.mark.parametrize("mode,layers", [("direct", 1), ("direct", 2), ("staged", 2), ("mirror", 1), ("mirror", 3)])
 def test_sessions_join_and_leave_between_steps(mode, layers):
     """Sessions join (the step plan grows) and leave (their ids are reused by later
     sessions) between steps. A single-layer decoder alternates between two pinned plan
-    buffers, a two-layer one keeps one. Every step matches the oracle."""
+    buffers, a two-layer one keeps one. In the mirror mode the host ranges that leaving
+    sessions free are handed to joining ones, so a ring buffer's records change between steps
+    and within one (three layers, two buffers). Every step matches the oracle."""
     g = torch.Generator().manual_seed(31)
     p = Pair(layers=layers, hq=8, hkv=2, d=64, tpb=16, dtype=torch.float16, pool_blocks=400, host_blocks=3000,
              staging_blocks=1024, stream_mode=mode)
@@ -333,7 +335,7 @@ def test_scoring_placement_on_another_stream(mode):
     assert evicted >= 3
 
 
-@pytest.mark.parametrize("mode,layers", [("direct", 1), ("direct", 2), ("staged", 1)])
+@pytest.mark.parametrize("mode,layers", [("direct", 1), ("direct", 2), ("staged", 1), ("mirror", 3)])
 def test_back_to_back_steps_without_host_sync(mode, layers):
     """Steps issued back to back with no host synchronisation, as a serving loop issues them.
     Each step reads ~45 MB of host blocks per layer, so the host plans the next steps while

@@ -176,26 +176,51 @@ def _first_difference(a, b):
     return next((i for i, (x, y) in enumerate(zip(a, b)) if x != y), min(len(a), len(b)))
 
 
-def test_config3_tinyllama_8192_prompt_256_tokens():
+def _config3_hbm_bound(pm):
+    """The store's device memory at configuration 3: the HBM pool holds the 41-block placement
+    budget plus the open block and a block completed before its placement (rows x 43 records
+    per layer), the mirror mode's ring three buffers of one layer's host share (at most 1.5x
+    the context's blocks after growth), nothing else but the step workspace."""
+    rec = 2 * 4 * 32 * 64 * 2  # one 32-token block of one layer: K and V, 4 KV heads, D 64
+    hbm = pm.decoder.pool.hbm_bytes()
+    blocks = (8192 + 512) // 32 + 2
+    assert hbm["pool"] == 22 * (41 + 2) * rec
+    assert hbm["staging"] == 0
+    if pm.stream_mode == "mirror":
+        assert 0 < hbm["mirror"] <= 3 * int(1.5 * blocks) * rec
+    else:
+        assert hbm["mirror"] == 0
+    assert hbm["workspace"] < 8 << 20
+    return hbm
+
+
+@pytest.mark.parametrize("stream_mode", ["mirror", "direct"])
+def test_config3_tinyllama_8192_prompt_256_tokens(stream_mode):
     """TinyLlama-1.1B architecture, 8192 random prompt ids, 256 greedy tokens, sinks_heavy_hitter
     with a 41-block budget (4 sinks + 8 recent + 29 by score) and 32-token blocks, decode steps
-    replayed from HIP graphs: all 256 tokens equal the unpaged fp16 baseline's, and the paged
-    logits stay within LOGIT_TOL of the baseline's at every teacher-forced step."""
+    replayed from HIP graphs (the mirror stream mode is the one the benchmark reports): all 256
+    tokens equal the unpaged fp16 baseline's, the paged logits stay within LOGIT_TOL of the
+    baseline's at every teacher-forced step, and the store's HBM stays within the placement
+    budget (plus the mirror mode's ring)."""
     from pager_hf import PagedModel
 
     model = _config3_model()
     ids = _config3_prompt()
     mask = torch.ones_like(ids)
     want, logits, gaps = _baseline(model, ids, mask, 256)
-    pm = PagedModel(model, **CFG3_PAGER)
+    pm = PagedModel(model, stream_mode=stream_mode, **CFG3_PAGER)
     worst = _teacher_forced(pm, ids, mask, want, logits, [[1.0]] * 256)  # argmax must agree at every step
     assert worst < LOGIT_TOL
-    graphs = PagedModel(model, use_hip_graphs=True, **CFG3_PAGER)
+    graphs = PagedModel(model, use_hip_graphs=True, stream_mode=stream_mode, **CFG3_PAGER)
     got = graphs.generate(ids, mask, 256)
     assert got == want[0], f"first difference at step {_first_difference(got, want[0])}"
     st = graphs.last_run_stats
     assert st.final_num_blocks == (8192 + 256 - 1) // 32
     assert st.total_cpu_to_gpu_mb > 0  # host blocks were streamed every step
+    hbm = _config3_hbm_bound(graphs)
+    print(f"config 3 ({stream_mode}): store HBM {hbm}")
+    if stream_mode != "mirror":
+        return
     # The tokens depend on the far context, most of which sits in host blocks: replacing the
     # first 4096 prompt tokens (positions unchanged) changes the baseline's tokens.
     other = ids.clone()
@@ -210,22 +235,25 @@ def test_config3_tinyllama_8192_prompt_256_tokens():
     assert _first_difference(changed[0], want[0]) < 256
 
 
-def test_config3_placement_replays_through_the_oracle(monkeypatch):
+@pytest.mark.parametrize("stream_mode,graphs", [("direct", False), ("mirror", True)])
+def test_config3_placement_replays_through_the_oracle(monkeypatch, stream_mode, graphs):
     """The first 10 decode steps of configuration 3 (step 0 completes block 255, so it adds a
     block and forces a rebalance) replayed through the oracle: each layer's q / k_new / v_new
     are captured at the attention interface and fed to PagedDecodeOracle together with the
     prompt's K/V. Attention outputs agree within TOL, the scores handed to the pager within
     2e-5, and the gather lists, new block ids and tier moves bit for bit. The selection
     boundary of sinks_heavy_hitter (29th vs 30th scored block, EMA scores) is reported each
-    step against the measured score error."""
+    step against the measured score error. Run eagerly in the direct mode, and from HIP
+    graphs in the mirror mode (the benchmark's configuration): there the tensors a capture
+    handed to decode_layer are the graph's own, which each replay refills."""
     import numpy as np
 
     from oracle.paged_decode import PagedDecodeOracle
     from oracle.pager_policy import selection_margin
     from pager_hf import PagedDecoder, PagedModel
 
-    captured = {"prefill": None, "layers": {}, "gather": None}
-    orig_prefill, orig_decode = PagedDecoder.prefill, PagedDecoder.decode_layer
+    captured = {"prefill": None, "by_sig": {}, "sig": None, "gather": None}
+    orig_prefill, orig_decode, orig_end = PagedDecoder.prefill, PagedDecoder.decode_layer, PagedDecoder.end_step
 
     def prefill(self, sid, keys, values, n_tokens, **kw):
         captured["prefill"] = ([k.float().cpu().numpy() for k in keys], [v.float().cpu().numpy() for v in values],
@@ -233,18 +261,23 @@ def test_config3_placement_replays_through_the_oracle(monkeypatch):
         return orig_prefill(self, sid, keys, values, n_tokens, **kw)
 
     def decode_layer(self, layer, q, k_new, v_new, out=None, **kw):
+        # Tensors, not copies: under capture nothing may be read back, and a replay refills them.
         o = orig_decode(self, layer, q, k_new, v_new, out, **kw)
-        captured["layers"][layer] = tuple(x.float().cpu().numpy() for x in (q, k_new, v_new, o))
-        if layer == 0:
-            captured["gather"] = self.step_host_blocks(0)
+        captured["by_sig"].setdefault(self.pool.step_signature(), {})[layer] = (q, k_new, v_new, o)
         return o
+
+    def end_step(self, **kw):
+        captured["sig"] = self.pool.step_signature()
+        captured["gather"] = self.step_host_blocks(0)
+        return orig_end(self, **kw)
 
     monkeypatch.setattr(PagedDecoder, "prefill", prefill)
     monkeypatch.setattr(PagedDecoder, "decode_layer", decode_layer)
+    monkeypatch.setattr(PagedDecoder, "end_step", end_step)
     model = _config3_model()
     ids = _config3_prompt()
     mask = torch.ones_like(ids)
-    pm = PagedModel(model, **CFG3_PAGER)
+    pm = PagedModel(model, stream_mode=stream_mode, use_hip_graphs=graphs, **CFG3_PAGER)
     kw = {k: CFG3_PAGER[k] for k in ("vram_budget", "ram_budget", "recent_window", "policy")}
     ora = PagedDecodeOracle(num_layers=22, num_query_heads=32, num_kv_heads=4, head_dim=64, tokens_per_block=32)
     with torch.inference_mode():
@@ -257,7 +290,8 @@ def test_config3_placement_replays_through_the_oracle(monkeypatch):
         for step in range(10):
             logits, _ = pm._forward_step(nxt, cur)
             st = pm._decoder.sessions[pm._sid].step_stats[-1]
-            L = [captured["layers"][layer] for layer in range(22)]
+            refs = captured["by_sig"][captured["sig"]]
+            L = [tuple(x.float().cpu().numpy() for x in refs[layer]) for layer in range(22)]
             ref = ora.step([0], [x[0] for x in L], [x[1] for x in L], [x[2] for x in L])
             err = max(float(np.abs(x[3] - r).max()) for x, r in zip(L, ref["out"]))
             assert err < TOL, f"step {step}: attention max-abs error {err}"
@@ -275,6 +309,9 @@ def test_config3_placement_replays_through_the_oracle(monkeypatch):
                   f"{margin['gap']} between blocks {margin.get('last')} and {margin.get('first_out')}{note}")
             nxt = torch.argmax(logits, dim=-1, keepdim=True)
             cur = torch.cat([cur, torch.ones_like(cur[:, :1])], dim=1)
+        if graphs:
+            assert len(pm._graphs) > 0  # steps were replayed from captured graphs
+        _config3_hbm_bound(pm)
     pm.reset()
 
 

@@ -98,7 +98,8 @@ def test_config5_continuous_batching_rounds_against_the_oracle():
     For 72 rounds every session's host-block list, new block ids and tier moves equal the
     oracle's (placement-only sessions, uniform scores). Two watched sessions with host blocks
     have their layer 0 and layer 27 attention checked against the dense oracle on three rounds
-    (their K/V: the prompt exported from the store, then each round's k_new / v_new)."""
+    (their K/V: the prompt's K/V as the model's prefill produced it, taken before the store
+    imports it, then each round's k_new / v_new)."""
     import numpy as np
     from transformers import Qwen2Config, Qwen2ForCausalLM
 
@@ -139,6 +140,20 @@ def test_config5_continuous_batching_rounds_against_the_oracle():
     check_rounds = {5, 30, 60}
 
     dec = engine.decoder
+    # The watched requests' prompt K/V at layers 0 and 27, from the model's prefill, before the
+    # store imports it (sid -> {layer: (K, V)}, overwritten when a sid is reused).
+    prefill_kv: dict[int, dict] = {}
+    watched_prefix = {lens[i] - 1 for i in watched}
+    orig_prefill = dec.prefill
+
+    def prefill(sid, keys, values, n_tokens, **kwargs):
+        if n_tokens in watched_prefix:
+            prefill_kv[sid] = {layer: (keys[layer][0, :, :n_tokens].float().cpu().numpy(),
+                                       values[layer][0, :, :n_tokens].float().cpu().numpy())
+                               for layer in layers_checked}
+        return orig_prefill(sid, keys, values, n_tokens, **kwargs)
+
+    dec.prefill = prefill
     ora = PagedDecodeOracle(num_layers=28, num_query_heads=12, num_kv_heads=2, head_dim=128, tokens_per_block=T)
     seen: dict[int, object] = {}  # id(engine session) -> request (sids are reused after a close)
     failures: list[BaseException] = []  # the scheduler turns exceptions of a step into request errors
@@ -179,8 +194,9 @@ def test_config5_continuous_batching_rounds_against_the_oracle():
                     n_checked["admitted"] += 1
                 if idx in watched:
                     for layer in layers_checked:
-                        k, v = dec.pool.export_tokens(s.sid, 0, layer, n_prefix)
-                        kv[(idx, layer)] = [k.float().cpu().numpy(), v.float().cpu().numpy()]
+                        k, v = prefill_kv[s.sid][layer]
+                        assert k.shape == (2, n_prefix, 128)
+                        kv[(idx, layer)] = [k, v]
         logits = orig_step(sessions, tokens)
         sids = [s.sid for s in sessions]
         ref = ora.step(sids, None, None, None, compute=False)

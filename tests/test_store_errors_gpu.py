@@ -38,12 +38,19 @@ def _step(dec, sids):
 
 
 def test_hbm_pool_exhaustion_is_a_memory_error_and_the_store_stays_usable():
+    """A prompt placed in HBM before its first placement needs no pool room (blocks past it
+    keep their bytes on the host); a placement that loads more blocks than the pool holds
+    raises MemoryError."""
     dec = _dec(pool_blocks=4)
     sid = dec.add_session(capacity_tokens=400, vram_budget=64 * MIB16, ram_budget=1 << 30, recent_window=63,
                           policy="recent_only")
     ks, vs = _kv(200)  # 12 full blocks, all wanted in HBM, 4 slots
-    with pytest.raises(MemoryError):
-        dec.prefill(sid, ks, vs, 200, place=False)
+    moves = dec.prefill(sid, ks, vs, 200, place=False)
+    assert moves["to_gpu"] == list(range(12))
+    assert dec.pool.session_info(sid)[2] == 12  # all 12 count as HBM-resident
+    assert dec.pool.hbm_bytes()["pool"] == 4 * 2 * 2 * 16 * 64 * 2  # 4 slots of 8 KiB (K and V)
+    with pytest.raises(MemoryError):  # the first placement loads all 12 into 4 slots
+        _step(dec, [sid])
     dec.remove_session(sid)
     sid = dec.add_session(capacity_tokens=100, vram_budget=2 * MIB16, ram_budget=1 << 30, recent_window=1,
                           policy="recent_only")
