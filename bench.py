@@ -486,6 +486,7 @@ def config3(args):
     ids = torch.randint(0, 32000, (1, 8192), generator=g).cuda()
     n_new = args.c3_tokens
     timed = {}
+    mirror_copies = None
     # (eager or graphs, stream mode): host blocks read in place by the attention kernel
     # ("direct"), copied to an HBM staging buffer on a second stream, each layer's under the
     # layer before it ("staged"), or copied by DMA into per-layer HBM mirrors beside the
@@ -504,9 +505,23 @@ def config3(args):
         ids2 = torch.cat([ids, torch.tensor([first], device="cuda")], dim=1)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        pm.generate(ids2, torch.ones_like(ids2), n_new)
+        out = pm.generate(ids2, torch.ones_like(ids2), n_new)
         torch.cuda.synchronize()
         timed[(graphs, mode)] = ((time.perf_counter() - t0) / n_new, pm.last_run_stats, pm.decoder.pool.hbm_bytes())
+        if mode == "mirror":
+            # The DMA copies of each layer's host share, event-timed by the store on its copy
+            # stream over 16 more tokens (apart from the timed run, which they would perturb).
+            ids3 = torch.cat([ids2, torch.tensor([out], device="cuda")], dim=1)
+            pm.decoder.pool.set_timing(True)
+            pm.generate(ids3, torch.ones_like(ids3), 16)
+            pm.decoder.pool.set_timing(False)
+            ms, n_cp, nbytes = pm.decoder.pool.copy_time()
+            pm.decoder.pool.kernel_time()  # drop the eager launches' timings
+            mirror_copies = {"layer_copy_groups": n_cp, "avg_us": round(ms * 1e3 / max(n_cp, 1), 2),
+                             "avg_bytes": nbytes // max(n_cp, 1),
+                             "GBs": round(nbytes / max(ms, 1e-9) / 1e6, 2),
+                             "note": "each layer's DMA copies into its ring buffer, HIP events on the store's copy "
+                                     "stream, 16 tokens after the timed run"}
         pm.reset()
     best = min(timed, key=lambda k: (not k[0], timed[k][0]))  # the fastest graph run
     dt, st, hbm_store = timed[best]
@@ -538,6 +553,7 @@ def config3(args):
         "hbm_kv_bytes": hbm_store,
         "hbm_kv_bytes_by_run": {("graphs_" if g else "eager_") + m: timed[(g, m)][2]["total"] for g, m in timed},
         "hbm_budget_bytes": 41 * 32 * kv_tok,  # the 41-block placement budget, all layers
+        "mirror_copies": mirror_copies,
         "cpu_baseline": _cpu_record(in_scope * kv_tok, cpu_s, 1, threads,
                                     f"dense fp32 attention and block mass in torch for all 22 layers of one decode "
                                     f"step at the mean context ({in_scope} tokens), repeated for "
@@ -871,12 +887,13 @@ def main() -> int:
                     help="host blocks read in place over the host link, or copied into a staging ring")
     ap.add_argument("--resident-layers", type=int, default=24,
                     help="layers of the all-resident HBM measurement (0 skips it)")
-    ap.add_argument("--workload", choices=["batch8", "continuous", "register", "configs", "hbm-scale"],
+    ap.add_argument("--workload", choices=["batch8", "continuous", "register", "configs", "hbm-scale", "operator"],
                     default="batch8",
                     help="batch8: the headline line (configuration 2, plus the configurations in --configs as "
                          "sub-records); continuous: the 64-request continuous-batching run alone; register: prompt "
                          "registration at 8k-64k tokens; configs: only the configurations in --configs; "
-                         "hbm-scale: the all-resident kernel against bytes per launch")
+                         "hbm-scale: the all-resident kernel against bytes per launch; operator: the operator API "
+                         "rows alone")
     ap.add_argument("--configs", default="1,3,4,5",
                     help="other configurations measured into the line (comma list of 1, 3, 4, 5; empty for none)")
     ap.add_argument("--register-reps", type=int, default=3)
@@ -909,6 +926,12 @@ def main() -> int:
     if args.workload == "hbm-scale":
         line = hbm_scale(args)
         line.update({"n_gpus": 1, "steps": 8, "warmup": 2, "scaling": "weak", "vs_baseline": None})
+        print(json.dumps(line), flush=True)
+        return 0
+    if args.workload == "operator":
+        line = {"metric": "operator API calls (streaming_attention_state_init / _step / _finalize)",
+                "operator_api": operator_api(), "n_gpus": 1, "scaling": "weak", "vs_baseline": None,
+                "data": "synthetic N(0,1)*0.5, seeded"}
         print(json.dumps(line), flush=True)
         return 0
     if args.workload == "configs":

@@ -71,9 +71,13 @@ int pgr_attn_step(const void* q, const void* k, const void* v, const int32_t* va
  * fold as pgr_attn_step, same kernels and results, with its split-K partials in a static
  * device array of the library (8 MiB per GPU, held until the process ends) instead of a
  * workspace. It calls no allocating routine. A chunk whose partials exceed 8 MiB is
- * rejected with PGR_ERR_CAPACITY; chunks with batch * num_kv_heads <= 496 always fit
- * (head_dim <= 128, n_rep <= 16). Calls share their GPU's array: calls that overlap on one
- * GPU (two streams, two threads) race and must be serialized by the caller. */
+ * rejected with PGR_ERR_CAPACITY. With fp16/bf16 q/k/v, chunks with batch * num_kv_heads
+ * <= 496 always fit at head_dim <= 128 and n_rep <= 16. fp32 q/k/v run a kernel with more,
+ * smaller partial slots: there chunks with batch * num_kv_heads <= 496 always fit while
+ * head_dim * n_rep <= 1024 (head_dim 64 at n_rep 16, 128 at n_rep 8); at head_dim 128 with
+ * n_rep 16 a long chunk of even one row is rejected (1 x 16 x 65536 x 128 needs 8.5 MB).
+ * Calls share their GPU's array: calls that overlap on one GPU (two streams, two threads)
+ * race and must be serialized by the caller. */
 int pgr_attn_step_noalloc(const void* q, const void* k, const void* v, const int32_t* valid, const int32_t* active,
                           float* m, float* l, float* acc, int64_t batch, int64_t num_query_heads,
                           int64_t num_kv_heads, int64_t tokens, int64_t head_dim, int dtype, float scale,
@@ -347,9 +351,13 @@ int pgr_kv_resident_bytes(void* kv, int64_t* gpu, int64_t* cpu);
 int pgr_kv_hbm_bytes(void* kv, int64_t* out);
 /* Bytes of one block of session sid over all layers and rows (kv_nbytes of a reference block). */
 int pgr_kv_block_bytes(void* kv, int32_t sid, int64_t* bytes);
-/* Event timing of the attention launches (for measurement). */
+/* Event timing of the attention launches (for measurement; eager launches only, none under
+ * graph capture) and, in the mirror mode, of each layer's DMA copies on the store's side stream.
+ * pgr_kv_copy_time (outside a step) waits for the timed copies and returns their summed
+ * milliseconds, the number of layer copy groups and their bytes, then forgets them. */
 int pgr_kv_set_timing(void* kv, int32_t on);
 int pgr_kv_kernel_time(void* kv, double* ms, int64_t* launches, int64_t* bytes);
+int pgr_kv_copy_time(void* kv, double* ms, int64_t* copies, int64_t* bytes);
 /* Waits for all work of the store (both streams). */
 int pgr_kv_sync(void* kv);
 

@@ -182,6 +182,7 @@ SIGNATURES: dict[str, tuple] = {
     "pgr_kv_block_bytes": (ctypes.c_int, [c_vp, c_i32, P(c_i64)]),
     "pgr_kv_set_timing": (ctypes.c_int, [c_vp, c_i32]),
     "pgr_kv_kernel_time": (ctypes.c_int, [c_vp, P(c_f64), P(c_i64), P(c_i64)]),
+    "pgr_kv_copy_time": (ctypes.c_int, [c_vp, P(c_f64), P(c_i64), P(c_i64)]),
     "pgr_kv_sync": (ctypes.c_int, [c_vp]),
 }
 

@@ -1309,43 +1309,75 @@ __global__ __launch_bounds__(256) void mass_reduce_kernel(const SeqInfo* seqs, c
   }
 }
 
-// Deferred mass, once per step (see launch_mass_step_reduce): the same per-layer mean as
-// mass_reduce_kernel, computed from the weights the merges wrote, over the layers in order.
+// Deferred mass, once per step (see launch_mass_step_reduce). Workgroup: 16 blocks x 16 head
+// groups. For a pass of up to 32 layers every thread adds up its heads (h = g, g + 16, ...) of
+// its block per layer in LDS, 8 layers x 4 heads of loads in flight at a time, and clears what
+// it read; then one thread per (layer, block) adds the 16 groups in a fixed order, and one
+// thread per block adds the layers up in layer order, so the result does not depend on
+// scheduling.
+constexpr int kStepMassBlocks = 16;
+constexpr int kStepMassGroups = 16;
+constexpr int kStepMassLayers = 32;  // layers per pass through LDS
+constexpr int kStepMassUnrollL = 8;  // layers whose loads one thread has in flight together
+constexpr int kStepMassUnrollH = 4;  // heads per group and layer loaded together (hq <= 64)
+
 __global__ __launch_bounds__(256) void mass_step_reduce_kernel(const SeqInfo* seqs, const int32_t* session_rows,
                                                                const int32_t* session_first, float* mass_w,
                                                                int64_t layer_floats, int num_layers,
                                                                float* mass_accum, int accum_stride, int hq,
                                                                int mass_stride, int max_blocks) {
-  __shared__ float part[kMassHeadGroups][kMassBlocksPerWG];
+  __shared__ float part[kStepMassLayers][kStepMassGroups][kStepMassBlocks];
+  __shared__ float layer_sum[kStepMassLayers][kStepMassBlocks];
   const int sess = blockIdx.y;
-  const int bl = threadIdx.x % kMassBlocksPerWG, hg = threadIdx.x / kMassBlocksPerWG;
-  const int blk = blockIdx.x * kMassBlocksPerWG + bl;
+  const int bl = threadIdx.x % kStepMassBlocks, hg = threadIdx.x / kStepMassBlocks;
+  const int blk = blockIdx.x * kStepMassBlocks + bl;
   const int first = session_first[sess], rows = session_rows[sess];
   const int n_mass = seqs[first].n_mass;
   const bool live = blk < n_mass && blk < max_blocks;
+  const float denom = (float)(rows * hq);
   float acc = 0.f;
   if (hg == 0 && live) acc = mass_accum[(size_t)sess * accum_stride + blk];
-  for (int layer = 0; layer < num_layers; ++layer) {
-    float* w = mass_w + (size_t)layer * layer_floats;
-    float total = 0.f;
-    if (live) {
-      for (int r = 0; r < rows; ++r) {
-        if (blk < seqs[first + r].mass_lo) continue;  // out of scope for this row: mass 0
-        const size_t row0 = (size_t)(first + r) * hq;
-#pragma unroll 4
-        for (int qh = hg; qh < hq; qh += kMassHeadGroups) {
-          const size_t mi = (row0 + qh) * mass_stride + blk;
-          total += w[mi];
-          w[mi] = 0.f;
+  for (int l0 = 0; l0 < num_layers; l0 += kStepMassLayers) {
+    const int nl = min(kStepMassLayers, num_layers - l0);
+    for (int li = 0; li < nl; ++li) part[li][hg][bl] = 0.f;
+    for (int r = 0; live && r < rows; ++r) {
+      if (blk < seqs[first + r].mass_lo) continue;  // out of scope for this row: mass 0
+      float* wr = mass_w + (size_t)l0 * layer_floats + ((size_t)(first + r) * hq + hg) * mass_stride + blk;
+      for (int qh0 = hg; qh0 < hq; qh0 += kStepMassGroups * kStepMassUnrollH) {
+        for (int li0 = 0; li0 < nl; li0 += kStepMassUnrollL) {
+          float x[kStepMassUnrollL][kStepMassUnrollH];
+#pragma unroll
+          for (int u = 0; u < kStepMassUnrollL; ++u)
+#pragma unroll
+            for (int k = 0; k < kStepMassUnrollH; ++k) {
+              const bool in = li0 + u < nl && qh0 + k * kStepMassGroups < hq;
+              const size_t at = (size_t)(li0 + u) * layer_floats +
+                                (size_t)(qh0 - hg + k * kStepMassGroups) * mass_stride;
+              x[u][k] = in ? wr[at] : 0.f;
+            }
+#pragma unroll
+          for (int u = 0; u < kStepMassUnrollL; ++u)
+#pragma unroll
+            for (int k = 0; k < kStepMassUnrollH; ++k) {
+              if (li0 + u < nl && qh0 + k * kStepMassGroups < hq) {
+                wr[(size_t)(li0 + u) * layer_floats + (size_t)(qh0 - hg + k * kStepMassGroups) * mass_stride] = 0.f;
+                part[li0 + u][hg][bl] += x[u][k];  // heads in ascending order
+              }
+            }
         }
       }
     }
-    part[hg][bl] = total;
     __syncthreads();
-    if (hg == 0 && live) {
-      const float sum = ((part[0][bl] + part[1][bl]) + part[2][bl]) + part[3][bl];
-      acc += sum / (float)(rows * hq);
+    for (int t = threadIdx.x; t < nl * kStepMassBlocks; t += blockDim.x) {
+      const int li = t / kStepMassBlocks, b = t % kStepMassBlocks;
+      float sum = 0.f;
+#pragma unroll
+      for (int g = 0; g < kStepMassGroups; ++g) sum += part[li][g][b];
+      layer_sum[li][b] = sum;
     }
+    __syncthreads();
+    if (hg == 0 && live)
+      for (int li = 0; li < nl; ++li) acc += layer_sum[li][bl] / denom;
     __syncthreads();
   }
   if (hg == 0 && live) mass_accum[(size_t)sess * accum_stride + blk] = acc;
@@ -1678,8 +1710,8 @@ hipError_t launch_mass_step_reduce(const SeqInfo* seqs, const int32_t* session_r
                                    int accum_stride, int hq, int mass_stride, int n_sessions, int max_blocks,
                                    hipStream_t stream) {
   if (n_sessions == 0 || max_blocks == 0 || num_layers == 0) return hipSuccess;
-  dim3 grid((max_blocks + kMassBlocksPerWG - 1) / kMassBlocksPerWG, n_sessions);
-  mass_step_reduce_kernel<<<grid, 256, 0, stream>>>(seqs, session_rows, session_first, mass_w, layer_floats,
+  dim3 grid((max_blocks + kStepMassBlocks - 1) / kStepMassBlocks, n_sessions);
+  mass_step_reduce_kernel<<<grid, kStepMassBlocks * kStepMassGroups, 0, stream>>>(seqs, session_rows, session_first, mass_w, layer_floats,
                                                     num_layers, mass_accum, accum_stride, hq, mass_stride,
                                                     max_blocks);
   return hipGetLastError();

@@ -828,6 +828,15 @@ int pgr_kv_kernel_time(void* kv, double* ms, int64_t* launches, int64_t* bytes) 
   }
 }
 
+int pgr_kv_copy_time(void* kv, double* ms, int64_t* copies, int64_t* bytes) {
+  try {
+    if (!kv || !ms || !copies || !bytes) return set_err(pgr::kErrInvalid, "null pointer");
+    return kv_rc(kv_of(kv), kv_of(kv)->copy_time(ms, copies, bytes));
+  } catch (...) {
+    return exception_status();
+  }
+}
+
 int pgr_kv_sync(void* kv) {
   try {
     if (!kv) return set_err(pgr::kErrInvalid, "null store");

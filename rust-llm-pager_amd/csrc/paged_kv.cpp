@@ -265,6 +265,10 @@ PagedKV::~PagedKV() {
     hipEventDestroy(t.start);
     hipEventDestroy(t.stop);
   }
+  for (auto& t : copy_timing_) {
+    hipEventDestroy(t.start);
+    hipEventDestroy(t.stop);
+  }
   if (plan_uploaded_) hipEventDestroy(plan_uploaded_);
   if (cap_fork_) hipEventDestroy(cap_fork_);
   if (mirror_go_) hipEventDestroy(mirror_go_);
@@ -1433,7 +1437,8 @@ int PagedKV::issue_mirror_copies(hipStream_t stream) {
   mirror_pending_ = true;
   step_closed_ = false;
   const uint32_t token = step_token_;
-  mirror_issuer_.submit([this, rec, token, spans = mirror_spans_, ring = ring_]() -> hipError_t {
+  const bool timed = timing_;
+  mirror_issuer_.submit([this, rec, token, timed, spans = mirror_spans_, ring = ring_]() -> hipError_t {
     const int n_ring = (int)ring.size();
     hipError_t e = hipSetDevice(device_);
     if (e == hipSuccess) e = hipStreamWaitEvent(copy_stream_, mirror_go_, 0);
@@ -1442,11 +1447,23 @@ int PagedKV::issue_mirror_copies(hipStream_t stream) {
       // once that layer's merge has published the step's token.
       if (l >= n_ring && !wait_release(l - n_ring, token)) break;
       char* dst = static_cast<char*>(ring[l % n_ring]);
+      PendingTiming t{nullptr, nullptr, 0};
+      if (timed) {  // events around the layer's copies on the copy stream (measurement only)
+        e = hipEventCreateWithFlags(&t.start, hipEventDisableSystemFence);
+        if (e == hipSuccess) e = hipEventCreateWithFlags(&t.stop, hipEventDisableSystemFence);
+        if (e == hipSuccess) e = hipEventRecord(t.start, copy_stream_);
+      }
       int64_t at = 0;
       for (size_t i = 0; i < spans.size() && e == hipSuccess; ++i) {
         e = hipMemcpyHtoDAsync(dst + (size_t)at * rec, static_cast<char*>(host_[l]) + (size_t)spans[i].first * rec,
                                (size_t)spans[i].second * rec, copy_stream_);
         at += spans[i].second;
+      }
+      if (timed && e == hipSuccess) {
+        e = hipEventRecord(t.stop, copy_stream_);
+        t.bytes = at * (int64_t)rec;
+        std::lock_guard<std::mutex> lk(copy_timing_mu_);
+        copy_timing_.push_back(t);
       }
       if (e == hipSuccess) e = hipStreamWriteValue32(copy_stream_, mirror_flags_ + l, 1u, 0);
     }
@@ -1595,7 +1612,8 @@ int PagedKV::decode_layer(int layer, const void* q, const void* k_new, const voi
       pl.aux_vec = (int64_t)(plan_aux_bytes_ / 16);
     }
     PendingTiming t{nullptr, nullptr, 0};
-    if (timing_) {
+    const bool timed = timing_ && !capturing;  // no event nodes in a captured graph
+    if (timed) {
       // Timing-only events recorded on the stream right before and after the launch. Without
       // a system-scope fence at record time they do not write back and invalidate the caches
       // around the launch they stamp. (Events handed to the launch itself read 15 to 18 us on
@@ -1607,7 +1625,7 @@ int PagedKV::decode_layer(int layer, const void* q, const void* k_new, const voi
       PGR_HIP(hipEventRecord(t.start, stream));
     }
     PGR_HIP(launch_paged(cfg_.dtype, cfg_.head_dim, pl, stream));
-    if (timing_) PGR_HIP(hipEventRecord(t.stop, stream));
+    if (timed) PGR_HIP(hipEventRecord(t.stop, stream));
     if (first_read) {
       // The merge below stores the buffer's token once this launch has finished. Under stream
       // capture nothing runs now and the captured launches carry no token: the caller marks
@@ -1623,7 +1641,7 @@ int PagedKV::decode_layer(int layer, const void* q, const void* k_new, const voi
       }
       plan_on_device_ = true;
     }
-    if (timing_) {
+    if (timed) {
       int64_t ent = 0;
       for (int w = launch_work_begin_[L]; w < launch_work_end_[L]; ++w) ent += work_[w].entry_count;
       t.bytes = ent * (int64_t)T * 2 * cfg_.head_dim * 2 * cfg_.kv_heads;  // K+V bytes read, whole blocks
@@ -1976,6 +1994,30 @@ int PagedKV::kernel_time(double* ms, int64_t* launches, int64_t* bytes) {
   timing_ms_ = 0.0;
   timing_launches_ = 0;
   timing_bytes_ = 0;
+  return kOk;
+}
+
+int PagedKV::copy_time(double* ms, int64_t* copies, int64_t* bytes) {
+  if (in_step_) return fail(kErrState, "copy_time during a decode step");
+  PGR_HIP(mirror_issuer_.wait());
+  std::lock_guard<std::mutex> lk(copy_timing_mu_);
+  double total = 0.0;
+  int64_t b = 0;
+  for (const PendingTiming& t : copy_timing_) {
+    PGR_HIP(hipEventSynchronize(t.stop));
+    float one = 0.f;
+    PGR_HIP(hipEventElapsedTime(&one, t.start, t.stop));
+    total += one;
+    b += t.bytes;
+  }
+  *ms = total;
+  *copies = (int64_t)copy_timing_.size();
+  *bytes = b;
+  for (const PendingTiming& t : copy_timing_) {
+    hipEventDestroy(t.start);
+    hipEventDestroy(t.stop);
+  }
+  copy_timing_.clear();
   return kOk;
 }
 

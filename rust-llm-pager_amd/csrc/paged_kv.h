@@ -207,6 +207,9 @@ class PagedKV {
   // Optional timing of the attention launches (HIP events on the compute stream).
   void set_timing(bool on) { timing_ = on; }
   int kernel_time(double* ms, int64_t* launches, int64_t* bytes);
+  // Mirror mode with timing on: the DMA copies of each layer's share, event-timed on the copy
+  // stream. Waits for them; returns the summed milliseconds, the layer copy groups and bytes.
+  int copy_time(double* ms, int64_t* copies, int64_t* bytes);
   int sync();
 
   const PagedKVConfig& cfg() const { return cfg_; }
@@ -387,6 +390,8 @@ class PagedKV {
   std::atomic<int> mirror_waiting_{0};  // the job is waiting for a release
   // Returns true once mirror_release_[layer] holds `token` (or later), false to give up.
   bool wait_release(int layer, uint32_t token);
+  std::mutex copy_timing_mu_;
+  std::vector<PendingTiming> copy_timing_;  // mirror copy groups timed by the thread's job
   std::vector<std::pair<int64_t, int64_t>> mirror_spans_;  // (first host record, count) per row
   uint64_t mirror_step_bytes_ = 0;                         // bytes copied per layer this step
   // Deferred block mass (see finish_step_mass).

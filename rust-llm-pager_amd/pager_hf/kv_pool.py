@@ -313,5 +313,13 @@ class NativeKVPool:
                                                   ctypes.byref(nbytes)), "kernel_time")
         return ms.value, launches.value, nbytes.value
 
+    def copy_time(self) -> tuple[float, int, int]:
+        """(milliseconds, layer copy groups, bytes) of the mirror mode's DMA copies timed since the last call."""
+        ms, n, nbytes = ctypes.c_double(0), ctypes.c_int64(0), ctypes.c_int64(0)
+        with torch.cuda.device(self.device):
+            nat.check(self.lib.pgr_kv_copy_time(self.handle, ctypes.byref(ms), ctypes.byref(n), ctypes.byref(nbytes)),
+                      "copy_time")
+        return ms.value, n.value, nbytes.value
+
     def sync(self) -> None:
         self._call("sync", self.lib.pgr_kv_sync)

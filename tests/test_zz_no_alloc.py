@@ -17,7 +17,7 @@ import _pgr_native as nat
 
 pytestmark = pytest.mark.gpu
 
-CODES = {torch.float16: nat.DTYPE_F16, torch.bfloat16: nat.DTYPE_BF16}
+CODES = {torch.float16: nat.DTYPE_F16, torch.bfloat16: nat.DTYPE_BF16, torch.float32: nat.DTYPE_F32}
 
 
 def _inputs(b, hq, hkv, tc, d, dtype, seed, masked):
@@ -66,6 +66,9 @@ def _run(lib, noalloc, case, seed, masked):
 CASES = [
     ((8, 14, 2, 6000, 64, torch.float16), 1, True),
     ((2, 32, 8, 700, 128, torch.bfloat16), 2, False),
+    # fp32 q/k/v run the generic kernel, whose plan has more, smaller partial slots.
+    ((1, 16, 1, 32768, 128, torch.float32), 3, True),
+    ((4, 8, 2, 3000, 64, torch.float32), 4, False),
 ]
 
 
@@ -79,13 +82,17 @@ def test_noalloc_matches_workspace_entry_point_on_consecutive_calls():
             assert torch.equal(a, b), f"{name} differs for {case}"
 
 
-def test_noalloc_rejects_a_chunk_beyond_the_static_scratch():
+@pytest.mark.parametrize("case", [
+    (1200, 16, 1, 16, 128, torch.float16),  # 1,200 partial slots of 16 x 130 floats: ~10 MB
+    (1, 16, 1, 65536, 128, torch.float32),  # one row, but 1,024 slots of the generic kernel: ~8.5 MB
+])
+def test_noalloc_rejects_a_chunk_beyond_the_static_scratch(case):
     lib = nat.load()
-    b, hq, hkv, tc, d = 1200, 16, 1, 16, 128  # 1,200 partial slots of 16 x 130 floats: ~10 MB
-    q, k, v, m, l, acc, _, _ = _inputs(b, hq, hkv, tc, d, torch.float16, 3, False)
+    b, hq, hkv, tc, d, dtype = case
+    q, k, v, m, l, acc, _, _ = _inputs(b, hq, hkv, tc, d, dtype, 3, False)
     before = acc.clone()
     rc = lib.pgr_attn_step_noalloc(q.data_ptr(), k.data_ptr(), v.data_ptr(), None, None, m.data_ptr(), l.data_ptr(),
-                                   acc.data_ptr(), b, hq, hkv, tc, d, nat.DTYPE_F16, 1.0 / d**0.5, 0.0,
+                                   acc.data_ptr(), b, hq, hkv, tc, d, CODES[dtype], 1.0 / d**0.5, 0.0,
                                    torch.cuda.current_stream().cuda_stream)
     assert rc == nat.PGR_ERR_CAPACITY
     assert "static scratch" in nat.last_error()
