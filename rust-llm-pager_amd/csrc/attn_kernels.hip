@@ -296,6 +296,31 @@ __global__ __launch_bounds__(256) void dense_attn_kernel(DenseArgs a) {
   const uint16_t* kp = a.k + kv_base;
   const uint16_t* vp = a.v + kv_base;
 
+  const int t_begin = split * kWaves * a.wave_tokens + wave * a.wave_tokens;
+  const int t_end = min(t_begin + a.wave_tokens, a.tc);
+  const int tiles = t_begin < t_end ? (t_end - t_begin + 15) / 16 : 0;
+  const int tiles_per_block = kMass ? a.tokens_per_block / 16 : 1;
+
+  // Tile ti's K and V (rows past the chunk clamped to its last row, then masked) and which of
+  // the lane's four V rows are valid tokens.
+  auto fetch = [&](Tile<D>& t, bool (&ok)[4], int ti) {
+    const int t0 = t_begin + ti * 16;
+    load_k<D>(t, kp, min(t0 + n, a.tc - 1), g);
+    int rows[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int tok = t0 + 4 * g + i;
+      ok[i] = tok < t_end;
+      if (ok[i] && a.valid != nullptr) ok[i] = a.valid[(size_t)b * a.tc + tok] != 0;
+      rows[i] = min(tok, a.tc - 1);
+    }
+    if constexpr (kWithV) load_v<D>(t, vp, rows, n);
+  };
+
+  Tile<D> ta, tb;
+  bool oka[4], okb[4];
+  if (tiles > 0) fetch(ta, oka, 0);  // the first tile's loads go out before the query's
+
   u32x4 q[D / 32];
   load_q<D>(q, a.q + ((size_t)b * a.hq + qh) * D, real, g);
 
@@ -310,28 +335,11 @@ __global__ __launch_bounds__(256) void dense_attn_kernel(DenseArgs a) {
   f32x4 acc[D / 16];
 #pragma unroll
   for (int j = 0; j < D / 16; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  const int t_begin = split * kWaves * a.wave_tokens + wave * a.wave_tokens;
-  const int t_end = min(t_begin + a.wave_tokens, a.tc);
-  const int tiles = t_begin < t_end ? (t_end - t_begin + 15) / 16 : 0;
-  const int tiles_per_block = kMass ? a.tokens_per_block / 16 : 1;
   float blk = 0.f;
 
-  for (int ti = 0; ti < tiles; ++ti) {
+  auto process = [&](Tile<D>& t, const bool (&ok)[4], int ti) {
     const int t0 = t_begin + ti * 16;
-    Tile<D> t;
-    load_k<D>(t, kp, min(t0 + n, a.tc - 1), g);
-    int rows[4];
-    bool ok[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int tok = t0 + 4 * g + i;
-      ok[i] = tok < t_end;
-      if (ok[i] && a.valid != nullptr) ok[i] = a.valid[(size_t)b * a.tc + tok] != 0;
-      rows[i] = min(tok, a.tc - 1);
-    }
     if constexpr (kWithV) {
-      load_v<D>(t, vp, rows, n);
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         if (!ok[i]) zero_v_row<D>(t, i);
@@ -364,13 +372,31 @@ __global__ __launch_bounds__(256) void dense_attn_kernel(DenseArgs a) {
         if ((ti + 1) % tiles_per_block == 0 || ti + 1 == tiles) {
           const float bs = wave_sum_g(blk);
           if (g == 0 && real) {
-            const int j = (t0 - 0) / a.tokens_per_block;
+            const int j = t0 / a.tokens_per_block;
             a.block_mass[((size_t)b * a.hq + qh) * a.max_blocks + a.block_id_offset + j] = bs / l_fix;
           }
           blk = 0.f;
         }
       }
     }
+  };
+
+  // Two tiles per wave in flight: the next tile's loads are issued before the current tile is
+  // folded. Unconditional in the loop (a conditional fetch lets the compiler drain the load
+  // queue every iteration); the last one or two tiles are folded after it.
+  int ti = 0;
+  for (; ti + 2 < tiles; ti += 2) {
+    fetch(tb, okb, ti + 1);
+    process(ta, oka, ti);
+    fetch(ta, oka, ti + 2);
+    process(tb, okb, ti + 1);
+  }
+  if (ti + 1 < tiles) {
+    fetch(tb, okb, ti + 1);
+    process(ta, oka, ti);
+    process(tb, okb, ti + 1);
+  } else if (ti < tiles) {
+    process(ta, oka, ti);
   }
 
   const size_t slot = ((size_t)b * a.hkv + h) * a.n_split + split;
