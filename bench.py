@@ -122,6 +122,7 @@ def hbm_all_resident(layers, steps, warmup, target_wg=0, blocks_per_wg=32):
     dec.pool.sync()
     k_ms, k_launches, k_bytes = dec.pool.kernel_time()
     dec.pool.close()
+    ceiling = plain_read_ceiling(k_bytes // max(k_launches, 1), layers)
     c = CFG
     tok_bytes = 2 * c["hkv"] * c["d"] * 2
     layer_bytes = stats["resident_tokens"] * tok_bytes // steps  # K/V bytes one layer-step reads
@@ -140,9 +141,35 @@ def hbm_all_resident(layers, steps, warmup, target_wg=0, blocks_per_wg=32):
                    "achieved": round(kernel_gbs, 2), "frac": round(kernel_gbs / HBM_PEAK_GBS, 4)},
         "step": {"achieved": round(step_gbs, 2), "frac": round(step_gbs / HBM_PEAK_GBS, 4),
                  "note": "whole decode step per layer (planning, both kernels, host glue) over K/V bytes"},
+        "plain_read_ceiling": ceiling,
         "unit": "GB/s",
         "peak": HBM_PEAK_GBS,
     }
+
+
+def plain_read_ceiling(nbytes, buffers, reps=96):
+    """A plain streaming read of `nbytes` in one launch (768 workgroups x 256 threads, the decode
+    kernel's grid at batch 8), rotating over `buffers` buffers so that the bytes come from HBM,
+    each launch between fence-free events (pgr_bench_stream_read): what one launch reading the
+    kernel's bytes can reach on this device."""
+    import ctypes
+
+    import torch
+
+    import _pgr_native as nat
+
+    lib = nat.load()
+    nbytes = nbytes // 16 * 16
+    bufs = [torch.zeros(nbytes, dtype=torch.uint8, device="cuda") for _ in range(buffers)]
+    ptrs = (ctypes.c_void_p * buffers)(*[b.data_ptr() for b in bufs])
+    us = ctypes.c_double(0)
+    stream = torch.cuda.current_stream().cuda_stream
+    nat.check(lib.pgr_bench_stream_read(ptrs, buffers, nbytes, 768, 24, ctypes.byref(us), stream), "warmup")
+    nat.check(lib.pgr_bench_stream_read(ptrs, buffers, nbytes, 768, reps, ctypes.byref(us), stream), "stream read")
+    del bufs
+    gbs = nbytes / (us.value * 1e3)
+    return {"bytes": nbytes, "workgroups": 768, "avg_launch_us": round(us.value, 3), "achieved": round(gbs, 2),
+            "frac": round(gbs / HBM_PEAK_GBS, 4)}
 
 
 KERNEL_SOURCES = ("rust-llm-pager_amd/csrc/attn_kernels.hip", "rust-llm-pager_amd/csrc/pgr_common.h",
@@ -1056,6 +1083,10 @@ def main() -> int:
             "launches": kern["launches"],
             "avg_launch_us": kern["avg_launch_us"],
             "bytes_per_launch": kern["bytes_per_launch"],
+            # A plain streaming read of the same bytes in one launch, same timing: the part of
+            # the gap to peak that a kernel of this size can close.
+            "plain_read_ceiling": res["plain_read_ceiling"],
+            "frac_of_ceiling": round(kern["achieved"] / res["plain_read_ceiling"]["achieved"], 4),
         }
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(ctx, args.cpu_seconds)

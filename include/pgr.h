@@ -118,6 +118,14 @@ int pgr_attn_fold_fixed_step(const void* q, const void* k, const void* v, const 
 int pgr_attn_set_timing(int32_t on);
 int pgr_attn_kernel_time(double* ms, int64_t* launches, int64_t* bytes);
 
+/* No counterpart in the reference. For measurement: `reps` launches of a plain streaming read
+ * of `bytes` (a positive multiple of 16) by workgroups x 256 threads, nothing written, launch r
+ * reading srcs[r % n_src] (16-byte aligned device buffers); each launch between two fence-free
+ * events on `stream`. Synchronous; returns the mean microseconds per launch: the ceiling a
+ * kernel that reads the same bytes in one launch is measured against. */
+int pgr_bench_stream_read(const void* const* srcs, int32_t n_src, int64_t bytes, int32_t workgroups, int32_t reps,
+                          double* us_per_launch, void* stream);
+
 /* Fresh state for rows = B * Hq: m[r] = -inf, l[r] = 0, acc[r, :] = 0 (fp32, contiguous), in
  * one launch. Replaces streaming_attention_state_init, pager_hf/streaming_attention.py:444-449
  * (three fills there). */

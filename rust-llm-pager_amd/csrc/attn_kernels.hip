@@ -1154,7 +1154,7 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(const WorkItem* __restr
 // output and the final (m, l) for the mass pass are written. The kernel is latency-bound:
 // each thread issues a whole batch of partial loads before using any of them (a load past
 // the last partial re-reads it and is weighted 0).
-constexpr int kMergeBatch = 8;
+constexpr int kMergeBatch = 16;
 
 template <class Ty, int D>
 __global__ __launch_bounds__(256) void paged_merge_kernel(const SeqInfo* __restrict__ seqs, PagedArgs a) {

@@ -357,6 +357,38 @@ int pgr_attn_kernel_time(double* ms, int64_t* launches, int64_t* bytes) {
   }
 }
 
+int pgr_bench_stream_read(const void* const* srcs, int32_t n_src, int64_t bytes, int32_t workgroups, int32_t reps,
+                          double* us_per_launch, void* stream) {
+  try {
+    if (!srcs || n_src <= 0 || reps <= 0 || !us_per_launch || bytes <= 0 || bytes % 16 != 0 || workgroups <= 0)
+      return set_err(pgr::kErrInvalid, "need buffers, reps > 0 and bytes a positive multiple of 16");
+    for (int i = 0; i < n_src; ++i)
+      if (!srcs[i] || ((uintptr_t)srcs[i]) % 16 != 0) return set_err(pgr::kErrInvalid, "buffers must be 16-byte aligned");
+    std::vector<hipEvent_t> ev(2 * (size_t)reps, nullptr);
+    hipError_t e = hipSuccess;
+    for (size_t i = 0; i < ev.size() && e == hipSuccess; ++i) e = hipEventCreateWithFlags(&ev[i], hipEventDisableSystemFence);
+    for (int r = 0; r < reps && e == hipSuccess; ++r) {
+      e = hipEventRecord(ev[2 * r], as_stream(stream));
+      if (e == hipSuccess) e = pgr::launch_stream_read(srcs[r % n_src], bytes, workgroups, as_stream(stream));
+      if (e == hipSuccess) e = hipEventRecord(ev[2 * r + 1], as_stream(stream));
+    }
+    double total = 0.0;
+    for (int r = 0; r < reps && e == hipSuccess; ++r) {
+      float ms = 0.f;
+      e = hipEventSynchronize(ev[2 * r + 1]);
+      if (e == hipSuccess) e = hipEventElapsedTime(&ms, ev[2 * r], ev[2 * r + 1]);
+      total += ms;
+    }
+    for (hipEvent_t x : ev)
+      if (x) (void)hipEventDestroy(x);
+    if (e != hipSuccess) return hip_err(e, "stream read");
+    *us_per_launch = total * 1e3 / reps;
+    return pgr::kOk;
+  } catch (...) {
+    return exception_status();
+  }
+}
+
 int pgr_attn_state_init(float* m, float* l, float* acc, int64_t rows, int64_t head_dim, void* stream) {
   try {
     if (rows < 0 || head_dim <= 0) return set_err(pgr::kErrInvalid, "negative or zero dimension");

@@ -80,4 +80,31 @@ hipError_t launch_records_to_ref(const void* pool, const int32_t* slots, void* k
   return hipGetLastError();
 }
 
+// Measurement: a plain streaming read of `n_vec` 16-byte vectors, the workgroups striding over
+// them together (each wave instruction reads 1 KB of consecutive bytes). The reduction of what
+// was read is stored only if it equals an arbitrary constant, so the loads cannot be dropped
+// and nothing is written in practice.
+__device__ uint32_t g_read_sink[256];
+
+__global__ __launch_bounds__(256) void stream_read_kernel(const uint32_t* __restrict__ src, int64_t n_vec) {
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4* p = reinterpret_cast<const u32x4*>(src);
+  u32x4 acc = {0u, 0u, 0u, 0u};
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  for (; i + 3 * stride < n_vec; i += 4 * stride) {
+    const u32x4 a = p[i], b = p[i + stride], c = p[i + 2 * stride], d = p[i + 3 * stride];
+    acc ^= a ^ b ^ c ^ d;
+  }
+  for (; i < n_vec; i += stride) acc ^= p[i];
+  const uint32_t v = acc.x ^ acc.y ^ acc.z ^ acc.w;
+  if (v == 0x9e3779b9u) g_read_sink[blockIdx.x & 255] = v;
+}
+
+hipError_t launch_stream_read(const void* src, int64_t bytes, int workgroups, hipStream_t stream) {
+  if (bytes <= 0) return hipSuccess;
+  stream_read_kernel<<<workgroups, 256, 0, stream>>>(static_cast<const uint32_t*>(src), bytes / 16);
+  return hipGetLastError();
+}
+
 }  // namespace pgr

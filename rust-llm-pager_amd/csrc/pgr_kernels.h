@@ -133,5 +133,7 @@ hipError_t launch_ref_to_records(const void* key, const void* value, void* pool,
                                  int hkv, int tokens_per_block, int d, hipStream_t stream);
 hipError_t launch_records_to_ref(const void* pool, const int32_t* slots, void* key, void* value, int rows, int hkv,
                                  int tokens_per_block, int d, hipStream_t stream);
+// Measurement: a plain streaming read of `bytes` (a multiple of 16) with `workgroups` x 256 threads.
+hipError_t launch_stream_read(const void* src, int64_t bytes, int workgroups, hipStream_t stream);
 
 }  // namespace pgr
