@@ -414,11 +414,11 @@ def _layer_config(args, name, *, hq, hkv, d, dtype, batch, ctx, resident, window
     nb = ctx // T
     dec = PagedDecoder(num_layers=1, num_query_heads=hq, num_kv_heads=hkv, head_dim=d, tokens_per_block=T,
                        dtype=dtype, device="cuda", pool_blocks=batch * (resident + 8),
-                       host_blocks=batch * (nb + 8), staging_blocks=64, staging_buffers=2)
+                       host_blocks=batch * (nb + (2 * steps + warmup) // T + 16), staging_blocks=64, staging_buffers=2)
     g = torch.Generator(device="cuda").manual_seed(ctx)
     sids, cpu_groups = [], []
     for _ in range(batch):
-        sid = dec.add_session(capacity_tokens=ctx + steps + warmup + 64, vram_budget=resident * MIB16,
+        sid = dec.add_session(capacity_tokens=ctx + 2 * steps + warmup + 64, vram_budget=resident * MIB16,
                               ram_budget=1 << 42, recent_window=resident - 1, policy="recent_only")
         k = (torch.randn(1, hkv, ctx, d, device="cuda", generator=g) * 0.5).to(dtype)
         v = (torch.randn(1, hkv, ctx, d, device="cuda", generator=g) * 0.5).to(dtype)
@@ -453,6 +453,15 @@ def _layer_config(args, name, *, hq, hkv, d, dtype, batch, ctx, resident, window
     torch.cuda.synchronize()
     dec.pool.sync()
     dt = (time.perf_counter() - t0) / steps
+    # The host's own time per step: the same calls timed one by one, without synchronizing
+    # (begin_step includes its wait for the plan buffer the launch two steps back read).
+    host_s = 0.0
+    for i in range(warmup + steps, warmup + 2 * steps):
+        h0 = time.perf_counter()
+        one(i)
+        host_s += time.perf_counter() - h0
+    torch.cuda.synchronize()
+    dec.pool.sync()
     hbm_store = dec.pool.hbm_bytes()
     dec.pool.close()
     tok_bytes = 2 * hkv * d * 2
@@ -463,6 +472,7 @@ def _layer_config(args, name, *, hq, hkv, d, dtype, batch, ctx, resident, window
         "workload": name,
         "steps": steps,
         "ms_per_step": round(dt * 1e3, 4),
+        "host_ms_per_step": round(host_s / steps * 1e3, 4),
         "tokens_per_s": round(batch / dt, 1),
         "kv_GBs": round((host_b + hbm_b) / dt / 1e9, 2),
         "host_link": _rate(host_b, dt, LINK_PEAK_GBS),
