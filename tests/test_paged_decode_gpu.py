@@ -519,6 +519,42 @@ def test_mirror_store_destroyed_while_its_copies_are_queued():
     torch.cuda.synchronize()
 
 
+def test_mirror_ring_layers_out_of_order_and_left_out():
+    """Mirror mode over four layers and a ring of two buffers: a layer's copies go into its
+    buffer once the layer two below it has released it. Layers decoded out of order wait
+    their bounded wait for copies that cannot come yet and read the host in place; every
+    output still matches the oracle. A last step decodes two of the four layers only: the
+    store's copy thread gives up on the releases that never come, the store closes, and a new
+    store steps normally."""
+    g = torch.Generator().manual_seed(71)
+    ctx = [1500, 2600]
+    p = Pair(layers=4, hq=8, hkv=2, d=64, tpb=32, dtype=torch.float16, pool_blocks=2 * 16,
+             host_blocks=sum(c // 32 + 8 for c in ctx), staging_buffers=2, stream_mode="mirror")
+    for c in ctx:
+        p.add(ctx=c, capacity=c + 64, gen=g, vram_budget=6 * MIB16, ram_budget=1024 * MIB16, recent_window=3,
+              policy="recent_only")
+    for step in range(6):
+        _, _, err = p.step(g, order=[2, 0, 3, 1] if step % 2 == 0 else None)
+        assert err < TOL
+    assert p.dec.pool.hbm_bytes()["mirror"] > 0
+    S = len(ctx)
+    p.dec.begin_step(p.sids)
+    for layer in (2, 3):
+        q = (torch.randn(S, 8, 64, generator=g) * 0.5).half().cuda()
+        kv = (torch.randn(S, 2, 64, generator=g) * 0.5).half().cuda()
+        p.dec.decode_layer(layer, q, kv, kv)
+    p.dec.end_step(collect=False)
+    p.dec.pool.close()
+    torch.cuda.synchronize()
+    q = Pair(layers=2, hq=8, hkv=2, d=64, tpb=32, dtype=torch.float16, pool_blocks=16, host_blocks=160,
+             stream_mode="mirror")
+    q.add(ctx=1000, capacity=1100, gen=g, vram_budget=4 * MIB16, ram_budget=1024 * MIB16, recent_window=2,
+          policy="recent_only")
+    for _ in range(3):
+        _, _, err = q.step(g)
+        assert err < TOL
+
+
 @pytest.mark.parametrize("mode", ["direct", "staged", "mirror"])
 @pytest.mark.parametrize("d,tpb,window", [(16, 16, 24), (64, 32, 100), (256, 16, 40)])
 def test_per_layer_sliding_windows(d, tpb, window, mode):
