@@ -76,8 +76,11 @@ int pgr_attn_step(const void* q, const void* k, const void* v, const int32_t* va
  * smaller partial slots: there chunks with batch * num_kv_heads <= 496 always fit while
  * head_dim * n_rep <= 1024 (head_dim 64 at n_rep 16, 128 at n_rep 8); at head_dim 128 with
  * n_rep 16 a long chunk of even one row is rejected (1 x 16 x 65536 x 128 needs 8.5 MB).
- * Calls share their GPU's array: calls that overlap on one GPU (two streams, two threads)
- * race and must be serialized by the caller. */
+ * Calls share their GPU's array. Outside graph capture the library orders them: a call on
+ * another stream than the previous call's waits on the GPU (hipStreamWaitEvent) for the
+ * previous call to finish, so calls from several streams or threads run one after another
+ * in the order they were made. Calls recorded into graphs are not ordered by the library:
+ * replays that may overlap on one GPU race, and the caller must serialize them. */
 int pgr_attn_step_noalloc(const void* q, const void* k, const void* v, const int32_t* valid, const int32_t* active,
                           float* m, float* l, float* acc, int64_t batch, int64_t num_query_heads,
                           int64_t num_kv_heads, int64_t tokens, int64_t head_dim, int dtype, float scale,

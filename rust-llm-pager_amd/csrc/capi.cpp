@@ -18,7 +18,7 @@
 // Split-K partials of pgr_attn_step_noalloc: a file-scope device array, one copy per GPU,
 // held until the process ends. In host code `scratch` is a host-side stand-in, not a device
 // address: the device address is looked up once per device (hipGetSymbolAddress with that
-// device current, noalloc_scratch below) and only that address is used afterwards.
+// device current, noalloc_device below) and only that address is used afterwards.
 constexpr size_t kNoAllocScratchBytes = (size_t)8 << 20;
 static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 
@@ -162,24 +162,42 @@ int run_dense(int mode, const void* q, const void* k, const void* v, const int32
   return pgr::kOk;
 }
 
-// Device address of `scratch` on the current device, looked up on the first call there.
+// Per device, set up on the first call there: the device address of `scratch`, and the
+// order of calls that share it. Outside graph capture a call whose stream differs from the
+// previous call's makes its stream wait (on the GPU) for an event recorded after the
+// previous call's launches, so calls from several streams or threads run one after another
+// on the GPU, in the order they were made, instead of racing on the shared array.
 constexpr int kMaxDevices = 64;
-std::once_flag g_scratch_once[kMaxDevices];
-void* g_scratch_ptr[kMaxDevices];
-hipError_t g_scratch_err[kMaxDevices];
+struct NoAllocDevice {
+  std::once_flag once;
+  hipError_t err = hipSuccess;
+  const char* what = nullptr;
+  void* scratch = nullptr;
+  std::mutex mu;               // held over a call's launches and event record
+  hipEvent_t done = nullptr;   // recorded after the previous call's launches
+  hipStream_t last = nullptr;  // that call's stream
+  bool have_last = false;
+};
+NoAllocDevice g_noalloc[kMaxDevices];
 
-int noalloc_scratch(void** out) {
+int noalloc_device(NoAllocDevice** out) {
   int dev = 0;
   const hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return hip_err(e, "hipGetDevice");
   if (dev < 0 || dev >= kMaxDevices) return set_err(pgr::kErrUnsupported, "device index beyond the scratch table");
-  std::call_once(g_scratch_once[dev], [dev] {
+  NoAllocDevice& d = g_noalloc[dev];
+  std::call_once(d.once, [&d] {
     void* p = nullptr;
-    g_scratch_err[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-    g_scratch_ptr[dev] = p;
+    d.err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    d.what = "hipGetSymbolAddress(scratch)";
+    d.scratch = p;
+    if (d.err == hipSuccess) {
+      d.err = hipEventCreateWithFlags(&d.done, hipEventDisableTiming);
+      d.what = "hipEventCreateWithFlags";
+    }
   });
-  if (g_scratch_err[dev] != hipSuccess) return hip_err(g_scratch_err[dev], "hipGetSymbolAddress(scratch)");
-  *out = g_scratch_ptr[dev];
+  if (d.err != hipSuccess) return hip_err(d.err, d.what);
+  *out = &d;
   return pgr::kOk;
 }
 
@@ -270,11 +288,30 @@ int pgr_attn_step_noalloc(const void* q, const void* k, const void* v, const int
                                             " bytes of split-K partials, more than the " +
                                             std::to_string(kNoAllocScratchBytes) +
                                             "-byte static scratch; use pgr_attn_step with a workspace");
-    void* ws = nullptr;
-    rc = noalloc_scratch(&ws);
+    NoAllocDevice* dev = nullptr;
+    rc = noalloc_device(&dev);
     if (rc != pgr::kOk) return rc;
-    return run_dense(PGR_MODE_FOLD, q, k, v, valid, active, m, l, acc, nullptr, 0, 0, 16, batch, num_query_heads,
-                     num_kv_heads, tokens, head_dim, dtype, scale, softcap, ws, kNoAllocScratchBytes, stream);
+    const hipStream_t s = as_stream(stream);
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    hipError_t e = hipStreamIsCapturing(s, &cap);
+    if (e != hipSuccess) return hip_err(e, "hipStreamIsCapturing");
+    if (cap != hipStreamCaptureStatusNone)  // captured calls: the caller orders the replays
+      return run_dense(PGR_MODE_FOLD, q, k, v, valid, active, m, l, acc, nullptr, 0, 0, 16, batch, num_query_heads,
+                       num_kv_heads, tokens, head_dim, dtype, scale, softcap, dev->scratch, kNoAllocScratchBytes,
+                       stream);
+    std::lock_guard<std::mutex> lock(dev->mu);
+    if (dev->have_last && dev->last != s) {
+      e = hipStreamWaitEvent(s, dev->done, 0);
+      if (e != hipSuccess) return hip_err(e, "hipStreamWaitEvent (previous call on another stream)");
+    }
+    rc = run_dense(PGR_MODE_FOLD, q, k, v, valid, active, m, l, acc, nullptr, 0, 0, 16, batch, num_query_heads,
+                   num_kv_heads, tokens, head_dim, dtype, scale, softcap, dev->scratch, kNoAllocScratchBytes, stream);
+    if (rc != pgr::kOk) return rc;
+    e = hipEventRecord(dev->done, s);
+    if (e != hipSuccess) return hip_err(e, "hipEventRecord (call order)");
+    dev->last = s;
+    dev->have_last = true;
+    return pgr::kOk;
   } catch (...) {
     return exception_status();
   }

@@ -4,7 +4,8 @@ pgr_attn_step (partials in a caller workspace), both called through the C ABI.
 The two entry points run the same kernels on the same plan, so their (m, l, acc) must be
 identical bit for bit. Two calls in a row, the second on a smaller chunk, so the second
 runs over whatever the first left in the static array; then a chunk too large for the
-array is rejected before anything is launched.
+array is rejected before anything is launched; then calls on two streams that do not wait
+for each other, which the library orders on the GPU.
 """
 from __future__ import annotations
 
@@ -98,3 +99,33 @@ def test_noalloc_rejects_a_chunk_beyond_the_static_scratch(case):
     assert "static scratch" in nat.last_error()
     torch.cuda.synchronize()
     assert torch.equal(acc, before)
+
+
+def test_noalloc_calls_on_two_streams_do_not_race_on_the_static_scratch():
+    """A long chunk on one stream, then at once a short one on another stream that does not
+    wait for the first: both share the static array, so without the library's ordering the
+    short call's fold would overwrite partial slots before the long call's merge read them.
+    Each result must equal the workspace entry point's, bit for bit."""
+    lib = nat.load()
+    long_case = ((8, 14, 2, 32768, 64, torch.float16), 11, False)
+    short_case = ((8, 14, 2, 2048, 64, torch.float16), 12, True)
+    want = [_run(lib, False, c, s, mk) for c, s, mk in (long_case, short_case)]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for rep in range(3):
+        print(f"two-stream noalloc rep {rep}", flush=True)
+        states = []
+        for (case, seed, masked), st in zip((long_case, short_case), streams):
+            b, hq, hkv, tc, d, dtype = case
+            q, k, v, m, l, acc, valid, active = _inputs(b, hq, hkv, tc, d, dtype, seed, masked)
+            torch.cuda.synchronize()
+            states.append((q, k, v, m, l, acc, valid, active, case, st))
+        for q, k, v, m, l, acc, valid, active, case, st in states:
+            b, hq, hkv, tc, d, dtype = case
+            rc = lib.pgr_attn_step_noalloc(q.data_ptr(), k.data_ptr(), v.data_ptr(), _ptr(valid), _ptr(active),
+                                           m.data_ptr(), l.data_ptr(), acc.data_ptr(), b, hq, hkv, tc, d,
+                                           CODES[dtype], 1.0 / d**0.5, 0.0, st.cuda_stream)
+            assert rc == 0, nat.last_error()
+        torch.cuda.synchronize()
+        for (q, k, v, m, l, acc, valid, active, case, st), w in zip(states, want):
+            for name, a, b in zip(("m", "l", "acc"), (m.cpu(), l.cpu(), acc.cpu()), w):
+                assert torch.equal(a, b), f"{name} differs for {case} (rep {rep})"
