@@ -172,6 +172,34 @@ def plain_read_ceiling(nbytes, buffers, reps=96):
             "frac": round(gbs / HBM_PEAK_GBS, 4)}
 
 
+def host_read_ceiling(nbytes, workgroups=(16, 32, 64, 128, 256, 512), buffers=4, reps=48):
+    """A plain streaming read of `nbytes` of pinned host memory, read in place over the host
+    link by one launch (pgr_bench_stream_read, fence-free events), at each grid size in
+    `workgroups`, rotating over `buffers` buffers: the fastest read of a launch's host bytes."""
+    import ctypes
+
+    import torch
+
+    import _pgr_native as nat
+
+    lib = nat.load()
+    nbytes = nbytes // 16 * 16
+    bufs = [torch.empty(nbytes, dtype=torch.uint8, pin_memory=True).zero_() for _ in range(buffers)]
+    ptrs = (ctypes.c_void_p * buffers)(*[b.data_ptr() for b in bufs])
+    us = ctypes.c_double(0)
+    stream = torch.cuda.current_stream().cuda_stream
+    by_wg = {}
+    for wg in workgroups:
+        nat.check(lib.pgr_bench_stream_read(ptrs, buffers, nbytes, wg, 8, ctypes.byref(us), stream), "warmup")
+        nat.check(lib.pgr_bench_stream_read(ptrs, buffers, nbytes, wg, reps, ctypes.byref(us), stream), "host read")
+        by_wg[wg] = round(us.value, 3)
+    del bufs
+    best = min(by_wg, key=by_wg.get)
+    gbs = nbytes / (by_wg[best] * 1e3)
+    return {"bytes": nbytes, "best_workgroups": best, "avg_launch_us": by_wg[best], "achieved": round(gbs, 2),
+            "frac": round(gbs / LINK_PEAK_GBS, 4), "us_by_workgroups": by_wg}
+
+
 KERNEL_SOURCES = ("rust-llm-pager_amd/csrc/attn_kernels.hip", "rust-llm-pager_amd/csrc/pgr_common.h",
                   "rust-llm-pager_amd/build.py")
 
@@ -414,11 +442,11 @@ def _layer_config(args, name, *, hq, hkv, d, dtype, batch, ctx, resident, window
     nb = ctx // T
     dec = PagedDecoder(num_layers=1, num_query_heads=hq, num_kv_heads=hkv, head_dim=d, tokens_per_block=T,
                        dtype=dtype, device="cuda", pool_blocks=batch * (resident + 8),
-                       host_blocks=batch * (nb + (2 * steps + warmup) // T + 16), staging_blocks=64, staging_buffers=2)
+                       host_blocks=batch * (nb + (3 * steps + warmup) // T + 16), staging_blocks=64, staging_buffers=2)
     g = torch.Generator(device="cuda").manual_seed(ctx)
     sids, cpu_groups = [], []
     for _ in range(batch):
-        sid = dec.add_session(capacity_tokens=ctx + 2 * steps + warmup + 64, vram_budget=resident * MIB16,
+        sid = dec.add_session(capacity_tokens=ctx + 3 * steps + warmup + 64, vram_budget=resident * MIB16,
                               ram_budget=1 << 42, recent_window=resident - 1, policy="recent_only")
         k = (torch.randn(1, hkv, ctx, d, device="cuda", generator=g) * 0.5).to(dtype)
         v = (torch.randn(1, hkv, ctx, d, device="cuda", generator=g) * 0.5).to(dtype)
@@ -462,6 +490,15 @@ def _layer_config(args, name, *, hq, hkv, d, dtype, batch, ctx, resident, window
         host_s += time.perf_counter() - h0
     torch.cuda.synchronize()
     dec.pool.sync()
+    # The attention launch's own execution time, event-stamped per launch.
+    dec.pool.kernel_time()
+    dec.pool.set_timing(True)
+    for i in range(warmup + 2 * steps, warmup + 3 * steps):
+        one(i)
+    torch.cuda.synchronize()
+    dec.pool.sync()
+    k_ms, k_launches, k_bytes = dec.pool.kernel_time()
+    dec.pool.set_timing(False)
     hbm_store = dec.pool.hbm_bytes()
     dec.pool.close()
     tok_bytes = 2 * hkv * d * 2
@@ -478,6 +515,9 @@ def _layer_config(args, name, *, hq, hkv, d, dtype, batch, ctx, resident, window
         "host_link": _rate(host_b, dt, LINK_PEAK_GBS),
         "hbm": _rate(hbm_b, dt, HBM_PEAK_GBS),
         "hbm_kv_bytes": hbm_store,
+        "attention_launch": {"avg_us": round(k_ms * 1e3 / max(k_launches, 1), 3), "launches": k_launches,
+                             "kv_bytes": k_bytes // max(k_launches, 1)},
+        "host_read_ceiling": host_read_ceiling(int(host_b)) if host_b else None,
         "cpu_baseline": _cpu_record(cpu_bytes, cpu_s, batch, threads,
                                     f"dense fp32 attention and block mass in torch over the same in-scope K/V of "
                                     f"all {batch} sequences, repeated for ~{args.cpu_seconds / 3:.0f} s"),
