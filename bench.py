@@ -172,6 +172,27 @@ def plain_read_ceiling(nbytes, buffers, reps=96):
             "frac": round(gbs / HBM_PEAK_GBS, 4)}
 
 
+def h2d_copy_ceiling(nbytes, reps=16):
+    """hipMemcpyAsync host-to-device from pinned memory (torch's non-blocking copy), `reps`
+    copies of `nbytes` back to back between HIP events: what the copy engines reach over the
+    host link on this device."""
+    import torch
+
+    src = torch.empty(nbytes, dtype=torch.uint8, pin_memory=True).fill_(1)
+    dst = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    dst.copy_(src, non_blocking=True)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        dst.copy_(src, non_blocking=True)
+    e1.record()
+    e1.synchronize()
+    gbs = nbytes * reps / (e0.elapsed_time(e1) * 1e6)
+    del src, dst
+    return {"bytes": nbytes, "reps": reps, "achieved": round(gbs, 2), "frac": round(gbs / LINK_PEAK_GBS, 4)}
+
+
 def host_read_ceiling(nbytes, workgroups=(16, 32, 64, 128, 256, 512), buffers=4, reps=48):
     """A plain streaming read of `nbytes` of pinned host memory, read in place over the host
     link by one launch (pgr_bench_stream_read, fence-free events), at each grid size in
@@ -481,13 +502,15 @@ def _layer_config(args, name, *, hq, hkv, d, dtype, batch, ctx, resident, window
     torch.cuda.synchronize()
     dec.pool.sync()
     dt = (time.perf_counter() - t0) / steps
-    # The host's own time per step: the same calls timed one by one, without synchronizing
-    # (begin_step includes its wait for the plan buffer the launch two steps back read).
-    host_s = 0.0
+    # The host's time per step: the same calls timed one by one, without synchronizing;
+    # begin_step's wait for the GPU to finish reading the plan buffer it reuses (the host runs
+    # at most a step ahead) is reported apart, the rest is the host's own work.
+    host_s = wait_s = 0.0
     for i in range(warmup + steps, warmup + 2 * steps):
         h0 = time.perf_counter()
-        one(i)
+        st = one(i)
         host_s += time.perf_counter() - h0
+        wait_s += st["plan_wait_ns"] * 1e-9
     torch.cuda.synchronize()
     dec.pool.sync()
     # The attention launch's own execution time, event-stamped per launch.
@@ -510,6 +533,8 @@ def _layer_config(args, name, *, hq, hkv, d, dtype, batch, ctx, resident, window
         "steps": steps,
         "ms_per_step": round(dt * 1e3, 4),
         "host_ms_per_step": round(host_s / steps * 1e3, 4),
+        "host_plan_wait_ms_per_step": round(wait_s / steps * 1e3, 4),
+        "host_work_ms_per_step": round((host_s - wait_s) / steps * 1e3, 4),
         "tokens_per_s": round(batch / dt, 1),
         "kv_GBs": round((host_b + hbm_b) / dt / 1e9, 2),
         "host_link": _rate(host_b, dt, LINK_PEAK_GBS),
@@ -1052,6 +1077,14 @@ def main() -> int:
     k_ms, k_launches, k_bytes = dec.pool.kernel_time()
 
     tok_bytes = 2 * c["hkv"] * c["d"] * 2  # K + V per token per layer
+    # What the host link carries at best on this device (outside the timed region): copy
+    # engines (pinned hipMemcpyAsync H2D) and one kernel launch reading a step's host bytes in
+    # place over the link, as the attention launch does.
+    step_host_bytes = stats["host_tokens"] * tok_bytes // args.steps
+    link_ceilings = {
+        "h2d_copy": h2d_copy_ceiling(64 << 20),
+        "kernel_read": host_read_ceiling(step_host_bytes, workgroups=(64, 128, 256, 512, 768, 1024), reps=12),
+    }
     io_bytes = args.steps * c["batch"] * c["hq"] * c["d"] * 2 * 2  # q in + out
     hbm_bytes = stats["resident_tokens"] * tok_bytes + io_bytes
     host_bytes = stats["host_tokens"] * tok_bytes
@@ -1090,6 +1123,8 @@ def main() -> int:
             "bytes_per_step": host_bytes // args.steps,
             "copies_per_step": stats["copies"] / args.steps,
             "note": "host-resident K/V bytes per step over the step time; peak = PCIe Gen5 x16 nominal",
+            "ceilings": link_ceilings,
+            "frac_of_kernel_read": round(link_gbs / link_ceilings["kernel_read"]["achieved"], 4),
         },
         "hbm_resident": {"bytes_per_step": hbm_bytes // args.steps, "blocks_per_sequence": args.resident_blocks},
         "kernel": {

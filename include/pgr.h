@@ -36,7 +36,7 @@ extern "C" {
 
 /* ---- library ------------------------------------------------------------------------- */
 
-/* ABI version of this header (increments when an entry point is added or changed); 9. */
+/* ABI version of this header (increments when an entry point is added or changed); 10. */
 int pgr_abi_version(void);
 /* Message of the last failing call on this thread ("" if none). */
 const char* pgr_last_error(void);
@@ -226,9 +226,13 @@ typedef struct pgr_kv_stats_s {
 /* Per step: resident_tokens / host_tokens / host_blocks count what the attention launches
  * read from HBM and from the host tier (where the bytes are); gather_blocks counts the
  * entries of the step's gather lists (blocks the placement put on the host tier; they differ
- * only for prompt blocks that wait for their first placement, see pgr_kv_apply_tiers). */
+ * only for prompt blocks that wait for their first placement, see pgr_kv_apply_tiers).
+ * plan_wait_ns: how long pgr_kv_begin_step waited for the GPU to finish reading the pinned
+ * plan buffer it reuses (the host runs at most a step ahead of the GPU); the rest of the
+ * host's time in the step's calls is its own work. */
 typedef struct pgr_kv_step_stats_s {
   int64_t resident_tokens, host_tokens, host_blocks, copies, chunks, launches, work_items, gather_blocks;
+  int64_t plan_wait_ns;
 } pgr_kv_step_stats_t;
 
 /* Creates a store (allocates HBM pools, pinned host mirror, staging). NULL on failure.

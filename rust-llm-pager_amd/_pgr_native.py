@@ -36,7 +36,7 @@ STREAM_DIRECT = 0
 STREAM_STAGED = 1
 STREAM_MIRROR = 2
 
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 c_i32, c_i64, c_u8, c_u32, c_u64 = ctypes.c_int32, ctypes.c_int64, ctypes.c_uint8, ctypes.c_uint32, ctypes.c_uint64
 c_f32, c_f64, c_size, c_vp = ctypes.c_float, ctypes.c_double, ctypes.c_size_t, ctypes.c_void_p
@@ -98,6 +98,7 @@ class KVStepStats(ctypes.Structure):
         ("launches", c_i64),
         ("work_items", c_i64),
         ("gather_blocks", c_i64),
+        ("plan_wait_ns", c_i64),
     ]
 
 

@@ -236,7 +236,7 @@ int kv_rc(pgr::PagedKV* kv, int rc) {
 
 extern "C" {
 
-int pgr_abi_version(void) { return 9; }
+int pgr_abi_version(void) { return 10; }
 
 const char* pgr_last_error(void) { return g_last_error.c_str(); }
 
@@ -813,6 +813,7 @@ int pgr_kv_step_stats(void* kv, pgr_kv_step_stats_t* out) {
     out->launches = s.launches;
     out->work_items = s.work_items;
     out->gather_blocks = s.gather_blocks;
+    out->plan_wait_ns = s.plan_wait_ns;
     return pgr::kOk;
   } catch (...) {
     return exception_status();

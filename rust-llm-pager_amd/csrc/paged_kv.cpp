@@ -1322,12 +1322,15 @@ int PagedKV::begin_step(const int32_t* sids, int n, hipStream_t stream) {
   PlanBuf& pb = plan_bufs_[plan_buf_];
   if (pb.pending) {
     pb.pending = false;
+    const auto w0 = std::chrono::steady_clock::now();
     if (pb.by_flag) {
       const int rc = wait_plan_flag(pb, plan_buf_);
       if (rc != kOk) return rc;
     } else {
       PGR_HIP(hipEventSynchronize(pb.read));
     }
+    step_stats_.plan_wait_ns =
+        std::chrono::duration_cast<std::chrono::nanoseconds>(std::chrono::steady_clock::now() - w0).count();
   }
   if (plan_bytes > pb.bytes) {
     if (pb.host) PGR_HIP(hipHostFree(pb.host));

@@ -82,6 +82,7 @@ struct StepStats {
   int64_t launches = 0;         // attention kernel launches per layer
   int64_t work_items = 0;
   int64_t gather_blocks = 0;    // (block, row) entries of the gather lists (logical host residency)
+  int64_t plan_wait_ns = 0;     // begin_step's wait for the GPU to finish reading the plan buffer
 };
 
 // Device memory a store holds, in bytes.
