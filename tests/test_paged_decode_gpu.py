@@ -69,12 +69,17 @@ class Pair:
         self.ora.set_lo(sid, lo)
 
     def step(self, gen, *, compute=True, scale=0.5, sids=None, order=None, end_stream=None, graphs=None,
-             windows=None, settle=False):
+             windows=None, settle=False, rounding_allowance=False):
         """One decode step of `sids` (every session by default), checked against the oracle.
         With `graphs` (a dict) the layers run from a captured HIP graph, one per launch
         signature: captured when the signature is new, replayed otherwise. windows[layer]:
         that layer's own sliding window (None: none). settle: wait for the store's side-stream
-        work after begin_step (in the mirror mode every layer then reads its mirror)."""
+        work after begin_step (in the mirror mode every layer then reads its mirror).
+        rounding_allowance: the error is measured beyond two roundings of the model dtype that
+        the reference's own kernel makes as well: P rounded before P.V (streaming_attention.py:178;
+        at most u sum_i p_i |v_i| / l <= u max|v|) and the output rounded by the finalize
+        (at most u |ref|), with unit roundoff u = 2^-11 (fp16) or 2^-8 (bf16). With few tokens
+        in scope they exceed 2e-3 in bf16 (at |v| = 1 up to 3.9e-3 each)."""
         win = windows if windows is not None else [None] * self.layers
         sids = self.sids if sids is None else sids
         order = list(range(self.layers)) if order is None else order
@@ -134,8 +139,17 @@ class Pair:
                         print(f"placement margin: gap {gap:.3g} within 10x the score error {err:.3g} (session {sid})")
         err = None
         if compute:
-            err = max(np.abs(np32(o) - r).max() for o, r in zip(outs, ref["out"]))
-            assert err < TOL, f"max-abs error {err}"
+            u = {torch.float16: 2.0**-11, torch.bfloat16: 2.0**-8}[self.dtype] if rounding_allowance else 0.0
+            seqs = [(sid, r) for sid in sids for r in range(self.dec.sessions[sid].rows)]
+            err = 0.0
+            for layer, (o, r) in enumerate(zip(outs, ref["out"])):
+                excess = np.abs(np32(o) - r)
+                if u:
+                    vmax = np.array([np.abs(self.ora.sessions[sid].values[layer][row]).max() for sid, row in seqs],
+                                    np.float32)
+                    excess = excess - u * (np.abs(r) + vmax[:, None, None])
+                err = max(err, float(excess.max()))
+            assert err < TOL, f"max-abs error {err}" + (" beyond the dtype's roundings" if u else "")
         return res, ref, err
 
 
