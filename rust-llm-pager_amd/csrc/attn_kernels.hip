@@ -959,11 +959,29 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(const WorkItem* __restr
       static_cast<u32x4*>(a.aux_dst)[v] = static_cast<const u32x4*>(a.aux_src)[v];
   }
 
-  // This wave's entries are wave, wave+4, wave+8, ... (slot, block id). The one being
-  // fetched and the next one sit in SGPRs; the one after is read (a scalar load) when a
-  // block starts, a block ahead of its use. Entries past entry_count are never fetched (the
-  // slots exist in every work item).
-  BlockEntry ecur = wi->entries[wave], enxt = wi->entries[wave + kWaves];
+  // The work item's blocks hold count * tpb tiles, flat index x = entry * tpb + tile in
+  // block. With per-block mass (kMass) wave w folds whole blocks: entries w, w+4, w+8, ...
+  // (a block's mass is then one wave's). Otherwise it folds tiles x = w, w+4, w+8, ..., so
+  // that the four waves' tile counts differ by at most one and no wave holds the workgroup
+  // up by a whole block. The cursor (fe, ftb) names the next fetch's entry and tile in
+  // block; the entry being fetched and the next one sit in SGPRs, and the one after is read
+  // (a scalar load) as a fetch is issued, a fetch or a block ahead of its use. Entries past
+  // entry_count are never read by a fetch (the slots exist in every work item).
+  int fe = kMass ? 0 : wave / tpb, ftb = kMass ? 0 : wave - (wave / tpb) * tpb;
+  const int step_e = kWaves / tpb, step_tb = kWaves - step_e * tpb;  // x += kWaves (no kMass)
+  auto advance = [&](int& e, int& tb) {
+    tb += step_tb;
+    e += step_e;
+    if (tb >= tpb) {
+      tb -= tpb;
+      ++e;
+    }
+  };
+  auto entry_at = [&](int e) { return wi->entries[e < kMaxWorkEntries ? e : kMaxWorkEntries - 1]; };
+  int ne = fe, ntb = ftb;  // the fetch after the next one
+  if (!kMass) advance(ne, ntb);
+  BlockEntry ecur = kMass ? wi->entries[wave] : entry_at(fe);
+  BlockEntry enxt = kMass ? wi->entries[wave + kWaves] : entry_at(ne);
 
   // Mirror mode: host records come from the layer's HBM mirror, filled by DMA on the store's
   // copy stream, which sets the word after the layer's copies. One lane per workgroup polls
@@ -1008,12 +1026,12 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(const WorkItem* __restr
   for (int j = 0; j < D / 16; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int my_blocks = count > wave ? (count - wave + kWaves - 1) / kWaves : 0;
-  const int tiles = my_blocks * tpb;
+  const int tiles = kMass ? my_blocks * tpb : (count * tpb > wave ? (count * tpb - wave + kWaves - 1) / kWaves : 0);
 
-  // Next tile to fetch: flat index nf, entry fe, tile ftb within the block. Every fetch in
-  // the loop is unconditional, so the load counter stays in order; a fetch past the wave's
-  // last tile goes through an empty buffer resource and returns at once with zeros.
-  int nf = 0, fe = 0, ftb = 0;
+  // Next tile to fetch: the wave's nf-th. Every fetch in the loop is unconditional, so the
+  // load counter stays in order; a fetch past the wave's last tile goes through an empty
+  // buffer resource and returns at once with zeros.
+  int nf = 0;
   auto fetch = [&](PTile<D>& t, TileMeta& mt) {
     const int slot = ecur.slot, bid = ecur.block_id;
     const uint16_t* rb =
@@ -1031,11 +1049,19 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(const WorkItem* __restr
     mt.block_id = bid;
     mt.last = (ftb == tpb - 1) ? fe : -1;
     ++nf;
-    if (++ftb == tpb) {
-      ftb = 0;
-      ++fe;
+    if constexpr (kMass) {
+      if (++ftb == tpb) {
+        ftb = 0;
+        ++fe;
+        ecur = enxt;
+        if (fe + 1 < kWaveEntries) enxt = wi->entries[wave + (fe + 1) * kWaves];
+      }
+    } else {
+      fe = ne;
+      ftb = ntb;
       ecur = enxt;
-      if (fe + 1 < kWaveEntries) enxt = wi->entries[wave + (fe + 1) * kWaves];
+      advance(ne, ntb);
+      enxt = entry_at(ne);
     }
   };
 
