@@ -82,8 +82,19 @@ def build(steps_total, staging_blocks=2048, staging_buffers=3, blocks_per_wg=32,
     return dec, sids, ctx, q, kn, vn, out
 
 
-def run_steps(dec, sids, q, kn, vn, out, first, count, stats):
+# Spin-kernel cycles queued ahead of each step of a pass that stamps its launches with
+# events: the GPU then reaches a launch's start event after the host has queued the launch,
+# so the events hold the GPU's time only (without it, a host a little slower than the GPU
+# adds its submission time to some launches' intervals).
+TIMING_SPIN_CYCLES = 1_000_000
+
+
+def run_steps(dec, sids, q, kn, vn, out, first, count, stats, spin=0):
+    import torch
+
     for i in range(first, first + count):
+        if spin:
+            torch.cuda._sleep(spin)
         dec.begin_step(sids)
         st = dec.pool.step_stats()
         stats["resident_tokens"] += st["resident_tokens"]
@@ -117,7 +128,8 @@ def hbm_all_resident(layers, steps, warmup, target_wg=0, blocks_per_wg=32):
     dec.pool.kernel_time()
     dec.pool.set_timing(True)
     run_steps(dec, sids, q, kn, vn, out, warmup + steps, steps, {"resident_tokens": 0, "host_tokens": 0,
-                                                                  "copies": 0, "launches": 0})
+                                                                  "copies": 0, "launches": 0},
+              spin=TIMING_SPIN_CYCLES)
     torch.cuda.synchronize()
     dec.pool.sync()
     k_ms, k_launches, k_bytes = dec.pool.kernel_time()
@@ -454,7 +466,8 @@ def _cpu_record(kv_bytes, seconds, tokens, threads, sample):
 def _layer_config(args, name, *, hq, hkv, d, dtype, batch, ctx, resident, window, steps, warmup):
     """One decoder layer over `batch` sequences of `ctx` tokens, the `resident` most recent blocks
     in HBM (recent_only) and the rest on host, optionally a sliding window; `steps` decode steps,
-    each appending one token per sequence."""
+    each appending one token per sequence. The prompt holds ctx - warmup tokens, so that the
+    untimed warmup steps bring every sequence to ctx tokens when the timed steps start."""
     import torch
 
     from pager_hf import PagedDecoder
@@ -469,10 +482,11 @@ def _layer_config(args, name, *, hq, hkv, d, dtype, batch, ctx, resident, window
     for _ in range(batch):
         sid = dec.add_session(capacity_tokens=ctx + 3 * steps + warmup + 64, vram_budget=resident * MIB16,
                               ram_budget=1 << 42, recent_window=resident - 1, policy="recent_only")
-        k = (torch.randn(1, hkv, ctx, d, device="cuda", generator=g) * 0.5).to(dtype)
-        v = (torch.randn(1, hkv, ctx, d, device="cuda", generator=g) * 0.5).to(dtype)
-        dec.prefill(sid, [k], [v], ctx)
-        lo = ctx - (window or ctx)
+        pre = ctx - warmup
+        k = (torch.randn(1, hkv, pre, d, device="cuda", generator=g) * 0.5).to(dtype)
+        v = (torch.randn(1, hkv, pre, d, device="cuda", generator=g) * 0.5).to(dtype)
+        dec.prefill(sid, [k], [v], pre)
+        lo = max(pre - (window or pre), 0)
         cpu_groups.append((k[0, :, lo:].cpu(), v[0, :, lo:].cpu()))
         del k, v
         sids.append(sid)
@@ -483,7 +497,7 @@ def _layer_config(args, name, *, hq, hkv, d, dtype, batch, ctx, resident, window
     def one(i):
         if window:
             for sid in sids:
-                dec.set_lo(sid, [ctx + i - window + 1])
+                dec.set_lo(sid, [ctx - warmup + i - window + 1])
         dec.begin_step(sids)
         st = dec.pool.step_stats()
         dec.decode_layer(0, q, kn, kn)
@@ -517,6 +531,7 @@ def _layer_config(args, name, *, hq, hkv, d, dtype, batch, ctx, resident, window
     dec.pool.kernel_time()
     dec.pool.set_timing(True)
     for i in range(warmup + 2 * steps, warmup + 3 * steps):
+        torch.cuda._sleep(TIMING_SPIN_CYCLES)
         one(i)
     torch.cuda.synchronize()
     dec.pool.sync()
@@ -553,18 +568,20 @@ def config1(args):
     import torch
 
     return _layer_config(args, "one Qwen2.5-0.5B layer (14q/2kv, D 64, fp16), batch 1, 4096 tokens in 32-token "
-                               "blocks: the 8 most recent in HBM, 120 on host (recent_only); 128 steps",
+                               "blocks: the 8 most recent in HBM, 120 on host (recent_only); 128 timed steps from "
+                               "4096 tokens after 512 warmup steps",
                          hq=14, hkv=2, d=64, dtype=torch.float16, batch=1, ctx=4096, resident=8, window=None,
-                         steps=128, warmup=8)
+                         steps=128, warmup=512)
 
 
 def config4(args):
     import torch
 
     return _layer_config(args, "one Mistral-7B layer (32q/8kv, D 128, bf16), batch 4, 131072 tokens, window 4096: "
-                               "32 in-window blocks in HBM, 96 on host; 32 steps",
+                               "32 in-window blocks in HBM, 96 on host; 32 timed steps from 131072 tokens after 32 "
+                               "warmup steps",
                          hq=32, hkv=8, d=128, dtype=torch.bfloat16, batch=4, ctx=131072, resident=32, window=4096,
-                         steps=32, warmup=4)
+                         steps=32, warmup=32)
 
 
 def config3(args):
@@ -1091,7 +1108,7 @@ def main() -> int:
     dec.pool.kernel_time()
     dec.pool.set_timing(True)
     run_steps(dec, sids, q, kn, vn, out, args.warmup + args.steps, args.steps,
-              {"resident_tokens": 0, "host_tokens": 0, "copies": 0, "launches": 0})
+              {"resident_tokens": 0, "host_tokens": 0, "copies": 0, "launches": 0}, spin=TIMING_SPIN_CYCLES)
     torch.cuda.synchronize()
     dec.pool.sync()
     k_ms, k_launches, k_bytes = dec.pool.kernel_time()
