@@ -1182,8 +1182,13 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(const WorkItem* __restr
 // the last partial re-reads it and is weighted 0).
 constexpr int kMergeBatch = 16;
 
+// The leading arguments are preloaded into SGPRs (as in paged_attn_kernel): the partial loads
+// of the first batch depend on nothing else, and go out before the plan's SeqInfo arrives.
 template <class Ty, int D>
-__global__ __launch_bounds__(256) void paged_merge_kernel(const SeqInfo* __restrict__ seqs, PagedArgs a) {
+__global__ __launch_bounds__(256) void paged_merge_kernel(const SeqInfo* __restrict__ seqs, const float* pm0,
+                                                          const float* pl0, const float* pacc0,
+                                                          int partial_stride, int hq, int n_rep, int hkv,
+                                                          PagedArgs a) {
   constexpr int kLanes = D / 2;          // threads per partial group (two dims each)
   constexpr int G = 256 / kLanes;        // partial groups
   constexpr int kU = kMergeBatch;
@@ -1194,18 +1199,55 @@ __global__ __launch_bounds__(256) void paged_merge_kernel(const SeqInfo* __restr
   const int seq = blockIdx.x, qh = blockIdx.y;
   const int tid = threadIdx.x;
   const int c = tid % kLanes, grp = tid / kLanes;
-  const int hq = a.hq, h = qh / a.n_rep;
-  const SeqInfo* si = seqs + seq;  // preloaded leading argument, as in paged_attn_kernel
-  const int P = si->partial_count, base = si->partial_base;  // P >= 1: every sequence has a work item
-  const size_t kv_row = ((size_t)seq * a.hkv + h) * D;
-  // The attention launches before this merge have finished: tell the host that the step's
-  // plan buffer is free (a system-scope vector store into pinned host memory).
-  if (a.plan_flag != nullptr && seq == 0 && qh == 0 && tid == 0)
-    __hip_atomic_store(a.plan_flag, a.plan_token, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-  // Mirror mode: the layer's attention launch has finished reading its ring buffer; the host
-  // may queue the next copies into it once this word holds the step's token.
-  if (a.release_flag != nullptr && seq == 0 && qh == 0 && tid == 0)
-    __hip_atomic_store(a.release_flag, si->step_token, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  const SeqInfo* si = seqs + seq;
+  const size_t stride_a = (size_t)hq * D;
+  const float *pm, *pl, *pa;  // this (sequence, head)'s first slot
+  auto set_base = [&](int base) {
+    pm = pm0 + (size_t)base * hq + qh;
+    pl = pl0 + (size_t)base * hq + qh;
+    pa = pacc0 + ((size_t)base * hq + qh) * D + 2 * c;
+  };
+  // A batch: slots p0, p0 + G, ... (kU of them), clamped to limit - 1, every load issued
+  // before any is used. A slot at or past P (not written this step, or re-read) gets weight
+  // 0 in the fold: its m is -inf and its l and acc are zeroed, not multiplied, since an
+  // unwritten slot may hold anything.
+  auto load_batch = [&](int p0, int limit, float (&xm)[kU], float (&xl)[kU], float2 (&xa)[kU]) {
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int p = min(p0 + G * u, limit - 1);
+      xm[u] = pm[(size_t)p * hq];
+      xl[u] = pl[(size_t)p * hq];
+      xa[u] = *reinterpret_cast<const float2*>(pa + (size_t)p * stride_a);
+    }
+  };
+  float xm0[kU], xl0[kU];
+  float2 xa0[kU];
+  if (partial_stride > 0) {
+    // Sequence s owns slots s * partial_stride .. + partial_stride - 1: the first batch
+    // depends on the preloaded arguments only, and its loads go out before the plan's
+    // SeqInfo (P, the flags' token) and the current token's operands are read.
+    set_base(seq * partial_stride);
+    load_batch(grp, partial_stride, xm0, xl0, xa0);
+  } else {
+    // Packed slots (a step whose sequences' work-item counts differ too much for fixed
+    // ranges): the first slot and the count come from the sequence's SeqInfo.
+    set_base(si->partial_base);
+    load_batch(grp, si->partial_count, xm0, xl0, xa0);
+  }
+
+  const int P = si->partial_count;  // P >= 1: every sequence has a work item
+  const int h = qh / n_rep;
+  const size_t kv_row = ((size_t)seq * hkv + h) * D;
+  if (seq == 0 && qh == 0 && tid == 0) {
+    // The attention launches before this merge have finished: tell the host that the step's
+    // plan buffer is free (a system-scope vector store into pinned host memory).
+    if (a.plan_flag != nullptr)
+      __hip_atomic_store(a.plan_flag, a.plan_token, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    // Mirror mode: the layer's attention launch has finished reading its ring buffer; the
+    // host may queue the next copies into it once this word holds the step's token.
+    if (a.release_flag != nullptr)
+      __hip_atomic_store(a.release_flag, si->step_token, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  }
 
   // Group 0 also computes the current token's score (its loads overlap the partial loads).
   uint32_t qd = 0, kd = 0, vd = 0;
@@ -1215,26 +1257,17 @@ __global__ __launch_bounds__(256) void paged_merge_kernel(const SeqInfo* __restr
     vd = *reinterpret_cast<const uint32_t*>(a.v_new + kv_row + 2 * c);
   }
 
-  const float* pm = a.pm + (size_t)base * hq + qh;
-  const float* pl = a.pl + (size_t)base * hq + qh;
-  const float* pa = a.pacc + ((size_t)base * hq + qh) * D + 2 * c;
-  const size_t stride_a = (size_t)hq * D;
   float m = kNegInf, l = 0.f;
   float2 acc = float2{0.f, 0.f};
-  for (int p0 = grp; p0 < P; p0 += G * kU) {
-    float xm[kU], xl[kU];
-    float2 xa[kU];
-#pragma unroll
-    for (int u = 0; u < kU; ++u) {
-      const int p = min(p0 + G * u, P - 1);
-      xm[u] = pm[(size_t)p * hq];
-      xl[u] = pl[(size_t)p * hq];
-      xa[u] = *reinterpret_cast<const float2*>(pa + (size_t)p * stride_a);
-    }
+  auto fold_batch = [&](int p0, float (&xm)[kU], float (&xl)[kU], float2 (&xa)[kU]) {
     float bmax = kNegInf;
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
-      if (p0 + G * u >= P) xm[u] = kNegInf;  // re-read past the end: weight 0
+      if (p0 + G * u >= P) {
+        xm[u] = kNegInf;
+        xl[u] = 0.f;
+        xa[u] = float2{0.f, 0.f};
+      }
       bmax = fmaxf(bmax, xm[u]);
     }
     const float m_new = fmaxf(m, bmax);
@@ -1251,6 +1284,13 @@ __global__ __launch_bounds__(256) void paged_merge_kernel(const SeqInfo* __restr
       acc.y += xa[u].y * w;
     }
     m = m_new;
+  };
+  fold_batch(grp, xm0, xl0, xa0);
+  for (int p0 = grp + G * kU; p0 < P; p0 += G * kU) {  // P > G * kU slots: later batches clamp to P
+    float xm[kU], xl[kU];
+    float2 xa[kU];
+    load_batch(p0, P, xm, xl, xa);
+    fold_batch(p0, xm, xl, xa);
   }
   // q . k_new: group 0's two-dim products, summed over its lanes in each wave (every lane
   // takes part in the shuffles; group 0 is aligned to kRed lanes), then over its waves.
@@ -1562,22 +1602,22 @@ hipError_t launch_paged_d(const PagedArgs& a, int d, int n_work, bool mass, hipS
 }
 
 template <class Ty>
-void launch_merge_d(const PagedArgs& a, int d, dim3 grid, hipStream_t stream) {
+void launch_merge_d(const PagedArgs& a, int stride, int d, dim3 grid, hipStream_t stream) {
   switch (d) {
     case 16:
-      paged_merge_kernel<Ty, 16><<<grid, 256, 0, stream>>>(a.seqs, a);
+      paged_merge_kernel<Ty, 16><<<grid, 256, 0, stream>>>(a.seqs, a.pm, a.pl, a.pacc, stride, a.hq, a.n_rep, a.hkv, a);
       break;
     case 32:
-      paged_merge_kernel<Ty, 32><<<grid, 256, 0, stream>>>(a.seqs, a);
+      paged_merge_kernel<Ty, 32><<<grid, 256, 0, stream>>>(a.seqs, a.pm, a.pl, a.pacc, stride, a.hq, a.n_rep, a.hkv, a);
       break;
     case 64:
-      paged_merge_kernel<Ty, 64><<<grid, 256, 0, stream>>>(a.seqs, a);
+      paged_merge_kernel<Ty, 64><<<grid, 256, 0, stream>>>(a.seqs, a.pm, a.pl, a.pacc, stride, a.hq, a.n_rep, a.hkv, a);
       break;
     case 128:
-      paged_merge_kernel<Ty, 128><<<grid, 256, 0, stream>>>(a.seqs, a);
+      paged_merge_kernel<Ty, 128><<<grid, 256, 0, stream>>>(a.seqs, a.pm, a.pl, a.pacc, stride, a.hq, a.n_rep, a.hkv, a);
       break;
     default:
-      paged_merge_kernel<Ty, 256><<<grid, 256, 0, stream>>>(a.seqs, a);
+      paged_merge_kernel<Ty, 256><<<grid, 256, 0, stream>>>(a.seqs, a.pm, a.pl, a.pacc, stride, a.hq, a.n_rep, a.hkv, a);
   }
 }
 
@@ -1740,9 +1780,9 @@ hipError_t launch_paged_merge(int dtype, int d, const PagedLaunch& p, int n_seq,
   a.mass_stride = p.mass_stride;
   dim3 grid(n_seq, p.hq);
   if (dtype == kF16)
-    launch_merge_d<F16>(a, d, grid, stream);
+    launch_merge_d<F16>(a, p.partial_stride, d, grid, stream);
   else
-    launch_merge_d<BF16>(a, d, grid, stream);
+    launch_merge_d<BF16>(a, p.partial_stride, d, grid, stream);
   return hipGetLastError();
 }
 

@@ -1229,14 +1229,26 @@ int PagedKV::begin_step(const int32_t* sids, int n, hipStream_t stream) {
     }
     launch_work_end_[L] = (int)work_.size();
   }
+  // Partial slots: sequence q owns slots q * stride .. q * stride + stride - 1, stride = the
+  // most work items of any sequence, so that the merge finds a sequence's slots without
+  // reading the plan (it issues the loads of its first batch at once, and masks the slots
+  // past the sequence's count when that arrives). When that would take more than twice the
+  // packed slots (plus 1024), the slots are packed and the merge reads where they start.
+  int stride = 1, packed = 0;
+  for (size_t q = 0; q < seqs_.size(); ++q) {
+    stride = std::max(stride, seq_wg[q]);
+    packed += seq_wg[q];
+  }
+  const bool fixed = (int64_t)seqs_.size() * stride <= 2 * (int64_t)packed + 1024;
   int base = 0;
   for (size_t q = 0; q < seqs_.size(); ++q) {
-    seqs_[q].partial_base = base;
+    seqs_[q].partial_base = fixed ? (int32_t)q * stride : base;
     seqs_[q].partial_count = seq_wg[q];
     base += seq_wg[q];
   }
   for (WorkItem& w : work_) w.partial += seqs_[w.seq].partial_base;
-  n_partials_ = base;
+  n_partials_ = fixed ? (int)seqs_.size() * stride : packed;
+  partial_stride_ = fixed ? stride : 0;
   mass_stride_ = max_mass;
   step_stats_.copies = (int64_t)copies_.size();
   step_stats_.chunks = n_chunks_;
@@ -1547,6 +1559,7 @@ int PagedKV::decode_layer(int layer, const void* q, const void* k_new, const voi
   pl.hkv = cfg_.kv_heads;
   pl.tokens_per_block = T;
   pl.mass_stride = mass_stride_;
+  pl.partial_stride = partial_stride_;
   pl.scale = scale;
   pl.softcap = softcap;
   pl.window = window;
@@ -1718,7 +1731,7 @@ int PagedKV::step_signature(int64_t* out, int64_t cap) const {
       (int64_t)launch_work_begin_.size(), (int64_t)(uintptr_t)plan_bufs_[plan_buf_].dev, (int64_t)plan_on_device_,
       (int64_t)n_chunks_, (int64_t)prefetch_step_, (int64_t)(uintptr_t)d_stage_pairs_,
       (int64_t)(uintptr_t)d_chunk_begin_, (int64_t)mass_deferred_, (int64_t)(uintptr_t)mass_w_,
-      (int64_t)mass_layer_floats_, ring_records_};
+      (int64_t)mass_layer_floats_, ring_records_, (int64_t)partial_stride_};
   for (void* b : ring_) v.push_back((int64_t)(uintptr_t)b);
   for (size_t L = 0; L < launch_work_begin_.size(); ++L) {
     v.push_back(launch_work_begin_[L]);

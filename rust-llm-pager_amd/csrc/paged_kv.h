@@ -426,6 +426,7 @@ class PagedKV {
   std::vector<std::vector<int64_t>> step_host_ids_;
   int n_chunks_ = 0;
   int n_partials_ = 0;
+  int partial_stride_ = 0;  // partial slots per sequence (the most work items of any), or 0: packed
   int mass_stride_ = 0;
   std::vector<int64_t> stage_pairs_;      // staged mode: (host record, staging record) pairs
   std::vector<int64_t> chunk_pair_begin_;  // first pair of each chunk, and the end

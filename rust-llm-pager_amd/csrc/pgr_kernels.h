@@ -53,6 +53,10 @@ struct DenseLaunch {
 // token's K/V into the pool); launch_paged_merge then combines each sequence's partials
 // with the current token (k_new/v_new) into out and the final (mf, lf).
 struct PagedLaunch {
+  // Merge launch: sequence s's split-K partials are slots s * partial_stride ..
+  // s * partial_stride + partial_stride - 1 (the first SeqInfo::partial_count of them
+  // written), or, with partial_stride 0, SeqInfo::partial_count slots from partial_base.
+  int partial_stride = 0;
   const void* q;
   const void* k_new;
   const void* v_new;

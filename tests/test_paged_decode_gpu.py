@@ -612,3 +612,24 @@ def test_geometry_grid(hq, hkv, d, tpb, dtype, scale, softcap, policy, mode):
         want = np.array(ref["placement"][sid]["scores"])
         assert np.abs(got - want).max() < 2e-5
     assert p.dec.pool.step_stats()["host_blocks"] > 0
+
+
+@pytest.mark.parametrize("mode", ["direct", "staged"])
+def test_one_long_and_many_short_sessions(mode):
+    """One 24k-token session beside 30 sessions of a few dozen tokens: the long one gets
+    hundreds of work items and the short ones one each, so fixed per-sequence ranges of
+    split-K partial slots would take more than twice the slots the step writes, and the store
+    packs them instead (the merge then reads where each sequence's slots start). Then steps
+    of the long session with four of the short ones, where the ranges are fixed again. Every
+    step matches the oracle."""
+    g = torch.Generator().manual_seed(77)
+    p = Pair(layers=1, hq=8, hkv=2, d=64, tpb=32, dtype=torch.float16, pool_blocks=600, host_blocks=1200,
+             staging_blocks=1024, stream_mode=mode)
+    long_sid = p.add(ctx=24000, capacity=24100, gen=g, vram_budget=8 * MIB16, ram_budget=1024 * MIB16,
+                     recent_window=7, policy="recent_only")
+    short = [p.add(ctx=int(torch.randint(1, 80, (1,), generator=g)), capacity=200, gen=g, vram_budget=4 * MIB16,
+                   ram_budget=1024 * MIB16, recent_window=3, policy="sinks_heavy_hitter") for _ in range(30)]
+    for _ in range(3):
+        p.step(g)
+    for _ in range(3):
+        p.step(g, sids=[long_sid] + short[:4])
