@@ -16,13 +16,16 @@ host part against PCIe Gen5 x16.
 The HBM roofline is measured on the same batch with every block resident, over 24 layers
 (1.45 GB of K/V per step, beyond the 256 MB MALL): `roofline` is paged_attn_kernel's K/V
 bytes per launch over its HIP-event launch time there. `roofline_by_launch_size` repeats that
-measurement at batch 16, 32 and 64 and for a Mistral-7B layer (--no-launch-scale leaves it
+measurement at batch 16, 32 and 64, at batch 8 with every context 32768 tokens, and for a
+Mistral-7B layer, each row with its whole per-layer step as well (--no-launch-scale leaves it
 out). `operator_api` times the six-function operator API at the shapes of the reference's
 kernel probe (--no-operator leaves it out). Synthetic N(0,1)*0.5 data. Prints one JSON line.
 """
 from __future__ import annotations
 
 import argparse
+import contextlib
+import gc
 import json
 import os
 import sys
@@ -89,6 +92,21 @@ def build(steps_total, staging_blocks=2048, staging_buffers=3, blocks_per_wg=32,
 TIMING_SPIN_CYCLES = 1_000_000
 
 
+@contextlib.contextmanager
+def gc_paused():
+    """Python's cyclic garbage collector off over a wall-clock timed region, after one
+    collection, as `timeit` does: a full collection pass (milliseconds with torch loaded) would
+    otherwise land in some steps and not others."""
+    was = gc.isenabled()
+    gc.collect()
+    gc.disable()
+    try:
+        yield
+    finally:
+        if was:
+            gc.enable()
+
+
 def run_steps(dec, sids, q, kn, vn, out, first, count, stats, spin=0):
     import torch
 
@@ -115,15 +133,23 @@ def hbm_all_resident(layers, steps, warmup, target_wg=0, blocks_per_wg=32):
                                           target_wg=target_wg, blocks_per_wg=blocks_per_wg)
     stats = {"resident_tokens": 0, "host_tokens": 0, "copies": 0, "launches": 0}
     run_steps(dec, sids, q, kn, vn, out, 0, warmup, stats)
-    # Pass 1: step rate (no per-launch events).
+    # Pass 1: step rate (no per-launch events): the GPU's time over the steps, between two
+    # events on the stream, the first queued behind a spin kernel so that the host has queued
+    # the first step when the GPU reaches it, as in a decode loop; and the wall clock.
     stats = {"resident_tokens": 0, "host_tokens": 0, "copies": 0, "launches": 0}
     torch.cuda.synchronize()
     dec.pool.sync()
-    t0 = time.perf_counter()
-    run_steps(dec, sids, q, kn, vn, out, warmup, steps, stats)
-    torch.cuda.synchronize()
-    dec.pool.sync()
-    dt = time.perf_counter() - t0
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with gc_paused():
+        t0 = time.perf_counter()
+        torch.cuda._sleep(TIMING_SPIN_CYCLES)
+        e0.record()
+        run_steps(dec, sids, q, kn, vn, out, warmup, steps, stats)
+        e1.record()
+        torch.cuda.synchronize()
+        dec.pool.sync()
+        wall = time.perf_counter() - t0
+    dt = e0.elapsed_time(e1) / 1e3
     # Pass 2: the attention kernel's own execution time, event-stamped per launch.
     dec.pool.kernel_time()
     dec.pool.set_timing(True)
@@ -146,13 +172,15 @@ def hbm_all_resident(layers, steps, warmup, target_wg=0, blocks_per_wg=32):
         "steps": steps,
         "kv_bytes_per_layer_step": layer_bytes,
         "ms_per_step": round(dt / steps * 1e3, 4),
+        "wall_ms_per_step": round(wall / steps * 1e3, 4),
         "tokens_per_s": round(c["batch"] * steps / dt, 2),
         "kernel": {"name": "paged_attn_kernel", "launches": k_launches,
                    "avg_launch_us": round(k_ms * 1e3 / max(k_launches, 1), 3),
                    "bytes_per_launch": k_bytes // max(k_launches, 1),
                    "achieved": round(kernel_gbs, 2), "frac": round(kernel_gbs / HBM_PEAK_GBS, 4)},
         "step": {"achieved": round(step_gbs, 2), "frac": round(step_gbs / HBM_PEAK_GBS, 4),
-                 "note": "whole decode step per layer (planning, both kernels, host glue) over K/V bytes"},
+                 "note": "whole decode step per layer (planning, both kernels, host glue) over K/V bytes, "
+                         "GPU time between stream events around the steps (ms_per_step)"},
         "plain_read_ceiling": ceiling,
         "unit": "GB/s",
         "peak": HBM_PEAK_GBS,
@@ -324,12 +352,13 @@ def continuous(args):
     host_bytes[0] = hbm_bytes[0] = 0
     live = sum(r.context_tokens for r in sched._active)
     live_lens = [r.context_tokens for r in sched._active]
-    t0 = time.perf_counter()
-    for _ in range(args.cb_rounds):
-        sched._admit_new_requests()
-        sched._run_once()
-    torch.cuda.synchronize()
-    dt = time.perf_counter() - t0
+    with gc_paused():
+        t0 = time.perf_counter()
+        for _ in range(args.cb_rounds):
+            sched._admit_new_requests()
+            sched._run_once()
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
     tokens = sum(len(r.generated_tokens) for r in reqs) - tokens0
     hbm_store = eng.decoder.pool.hbm_bytes()
     sched.stop()
@@ -508,23 +537,25 @@ def _layer_config(args, name, *, hq, hkv, d, dtype, batch, ctx, resident, window
         one(i)
     torch.cuda.synchronize()
     dec.pool.sync()
-    t0 = time.perf_counter()
-    for i in range(warmup, warmup + steps):
-        st = one(i)
-        host += st["host_tokens"]
-        res_tok += st["resident_tokens"]
-    torch.cuda.synchronize()
-    dec.pool.sync()
-    dt = (time.perf_counter() - t0) / steps
+    with gc_paused():
+        t0 = time.perf_counter()
+        for i in range(warmup, warmup + steps):
+            st = one(i)
+            host += st["host_tokens"]
+            res_tok += st["resident_tokens"]
+        torch.cuda.synchronize()
+        dec.pool.sync()
+        dt = (time.perf_counter() - t0) / steps
     # The host's time per step: the same calls timed one by one, without synchronizing;
     # begin_step's wait for the GPU to finish reading the plan buffer it reuses (the host runs
     # at most a step ahead) is reported apart, the rest is the host's own work.
     host_s = wait_s = 0.0
-    for i in range(warmup + steps, warmup + 2 * steps):
-        h0 = time.perf_counter()
-        st = one(i)
-        host_s += time.perf_counter() - h0
-        wait_s += st["plan_wait_ns"] * 1e-9
+    with gc_paused():
+        for i in range(warmup + steps, warmup + 2 * steps):
+            h0 = time.perf_counter()
+            st = one(i)
+            host_s += time.perf_counter() - h0
+            wait_s += st["plan_wait_ns"] * 1e-9
     torch.cuda.synchronize()
     dec.pool.sync()
     # The attention launch's own execution time, event-stamped per launch.
@@ -623,10 +654,12 @@ def config3(args):
         first = pm.generate(ids, torch.ones_like(ids), 1)
         ids2 = torch.cat([ids, torch.tensor([first], device="cuda")], dim=1)
         torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        out = pm.generate(ids2, torch.ones_like(ids2), n_new)
-        torch.cuda.synchronize()
-        timed[(graphs, mode)] = ((time.perf_counter() - t0) / n_new, pm.last_run_stats, pm.decoder.pool.hbm_bytes())
+        with gc_paused():
+            t0 = time.perf_counter()
+            out = pm.generate(ids2, torch.ones_like(ids2), n_new)
+            torch.cuda.synchronize()
+            t_tok = (time.perf_counter() - t0) / n_new
+        timed[(graphs, mode)] = (t_tok, pm.last_run_stats, pm.decoder.pool.hbm_bytes())
         if mode == "mirror":
             # The DMA copies of each layer's host share, event-timed by the store on its copy
             # stream over 16 more tokens (apart from the timed run, which they would perturb).
@@ -736,11 +769,14 @@ def configs(args):
     return out
 
 
-def hbm_scale_rows(batches=(8, 16, 32, 64), mistral=True):
+def hbm_scale_rows(batches=(8, 16, 32, 64), mistral=True, full_context=True):
     """The all-resident attention kernel as the bytes per launch grow: Qwen2.5-0.5B geometry
-    (14q/2kv, D 64, fp16) at the given batches with contexts U[1024, 32768], and a Mistral-7B
-    layer (32q/8kv, D 128, bf16) at batch 4 x 32768 tokens. Every block resident, several
-    layers so the K/V read per step exceeds the MALL; event-timed launches."""
+    (14q/2kv, D 64, fp16) at the given batches with contexts U[1024, 32768], the same layer at
+    batch 8 with every context 32768 tokens (with the plain-read ceiling of its bytes), and a
+    Mistral-7B layer (32q/8kv, D 128, bf16) at batch 4 x 32768 tokens. Every block resident,
+    several layers so the K/V read per step exceeds the MALL. Per row: the attention launches
+    between fence-free events (each step queued behind a spin kernel), and the whole per-layer
+    step (both kernels, planning, host glue) between two events around 16 steps."""
     import torch
 
     from pager_hf import PagedDecoder
@@ -748,7 +784,7 @@ def hbm_scale_rows(batches=(8, 16, 32, 64), mistral=True):
     T = 32
     out = []
 
-    def measure(name, hq, hkv, d, dtype, ctxs, layers, steps=8, warmup=2):
+    def measure(name, hq, hkv, d, dtype, ctxs, layers, steps=16, warmup=2, ceiling=False):
         nb = [c // T + 2 for c in ctxs]
         dec = PagedDecoder(num_layers=layers, num_query_heads=hq, num_kv_heads=hkv, head_dim=d, tokens_per_block=T,
                            dtype=dtype, device="cuda", pool_blocks=sum(nb) + 16 * len(ctxs),
@@ -767,32 +803,60 @@ def hbm_scale_rows(batches=(8, 16, 32, 64), mistral=True):
         q = (torch.randn(S, hq, d, device="cuda", generator=g) * 0.5).to(dtype)
         kn = (torch.randn(S, hkv, d, device="cuda", generator=g) * 0.5).to(dtype)
 
-        def run(n):
+        def run(n, spin=0):
             for _ in range(n):
+                if spin:
+                    torch.cuda._sleep(spin)
                 dec.begin_step(sids)
                 for layer in range(layers):
                     dec.decode_layer(layer, q, kn, kn)
                 dec.end_step(collect=False)
 
         run(warmup)
+        # Whole steps (planning, both kernels per layer, host glue), no per-launch events: the
+        # GPU's time from the first step's start to the last step's end, between two events on
+        # the stream, the first queued behind a spin kernel so that the host has queued the
+        # first step when the GPU reaches it (as in a decode loop, where the host plans a step
+        # while the GPU runs the one before).
         torch.cuda.synchronize()
         dec.pool.sync()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with gc_paused():
+            torch.cuda._sleep(4 * TIMING_SPIN_CYCLES)  # ~2 ms: longer than planning a batch-64 step
+            e0.record()
+            run(steps)
+            e1.record()
+            torch.cuda.synchronize()
+            dec.pool.sync()
+        layer_us = e0.elapsed_time(e1) * 1e3 / (steps * layers)
+        # The attention launches alone, event-stamped.
         dec.pool.kernel_time()
         dec.pool.set_timing(True)
-        run(steps)
+        run(steps, spin=TIMING_SPIN_CYCLES)
         torch.cuda.synchronize()
         dec.pool.sync()
         ms, n, by = dec.pool.kernel_time()
         dec.pool.close()
         us = ms * 1e3 / n
-        out.append({"workload": name, "bytes_per_launch": by // n, "avg_launch_us": round(us, 2),
-                    "achieved": round(by / n / us / 1e3, 1), "frac": round(by / n / us / 1e3 / HBM_PEAK_GBS, 4)})
+        row = {"workload": name, "bytes_per_launch": by // n, "avg_launch_us": round(us, 2),
+               "achieved": round(by / n / us / 1e3, 1), "frac": round(by / n / us / 1e3 / HBM_PEAK_GBS, 4),
+               "layer_step_us": round(layer_us, 2),
+               "layer_step_frac": round(by / n / layer_us / 1e3 / HBM_PEAK_GBS, 4)}
+        if ceiling:
+            c = plain_read_ceiling(by // n, layers)
+            row["plain_read_ceiling"] = c
+            row["frac_of_ceiling"] = round(by / n / us / 1e3 / c["achieved"], 4)
+        out.append(row)
 
+    # Qwen2.5-0.5B's 24 layers per step: the K/V read per step is past the MALL, and the host's
+    # planning and placement per step (O(blocks)) run beside the GPU's layers, as in the model.
     for batch in batches:
         ctxs = draw_contexts(CFG["seed"], batch, CFG["ctx_lo"], CFG["ctx_hi"])
-        layers = max(2, int(1.6e9 // (sum(ctxs) * 512)))  # > 1.5 GB per step: past the MALL
-        measure(f"0.5B layer, batch {batch}, contexts U[1024,32768], {layers} layers", 14, 2, 64, torch.float16,
-                ctxs, layers)
+        measure(f"0.5B layer, batch {batch}, contexts U[1024,32768], 24 layers", 14, 2, 64, torch.float16,
+                ctxs, 24)
+    if full_context:
+        measure("0.5B layer, batch 8, every context 32768, 24 layers", 14, 2, 64, torch.float16,
+                [32768] * 8, 24, ceiling=True)
     if mistral:
         measure("Mistral-7B layer (32q/8kv, D 128, bf16), batch 4 x 32768, 4 layers", 32, 8, 128, torch.bfloat16,
                 [32768] * 4, 4)
@@ -800,7 +864,7 @@ def hbm_scale_rows(batches=(8, 16, 32, 64), mistral=True):
 
 
 def hbm_scale(args):
-    """--workload hbm-scale: hbm_scale_rows() at batch 8 to 64 and the Mistral-7B layer."""
+    """--workload hbm-scale: hbm_scale_rows() at batch 8 to 64, batch 8 x 32768 and the Mistral-7B layer."""
     out = hbm_scale_rows()
     return {
         "metric": "all-resident paged attention HBM GB/s against bytes per launch",
@@ -1099,11 +1163,12 @@ def main() -> int:
     stats = {"resident_tokens": 0, "host_tokens": 0, "copies": 0, "launches": 0}
     torch.cuda.synchronize()
     dec.pool.sync()
-    t0 = time.perf_counter()
-    run_steps(dec, sids, q, kn, vn, out, args.warmup, args.steps, stats)
-    torch.cuda.synchronize()
-    dec.pool.sync()
-    dt = time.perf_counter() - t0
+    with gc_paused():
+        t0 = time.perf_counter()
+        run_steps(dec, sids, q, kn, vn, out, args.warmup, args.steps, stats)
+        torch.cuda.synchronize()
+        dec.pool.sync()
+        dt = time.perf_counter() - t0
     # Pass 2: the attention kernel's own execution time, event-stamped per launch.
     dec.pool.kernel_time()
     dec.pool.set_timing(True)
@@ -1219,7 +1284,8 @@ def main() -> int:
     if not args.no_launch_scale:
         # The same kernel, every block resident, as a launch carries more bytes: batch 8 is the
         # roofline above; a launch of several rounds of workgroups amortizes each workgroup's
-        # fixed start, query wait and partial store.
+        # fixed start, query wait and partial store. Batch 8 with every context at 32768 tokens
+        # carries 134 MB per launch.
         line["roofline_by_launch_size"] = {
             "kernel": "paged_attn_kernel", "bound": "hbm", "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "rows": hbm_scale_rows(batches=(16, 32, 64), mistral=True),
