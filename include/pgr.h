@@ -128,6 +128,10 @@ int pgr_attn_kernel_time(double* ms, int64_t* launches, int64_t* bytes);
  * kernel that reads the same bytes in one launch is measured against. */
 int pgr_bench_stream_read(const void* const* srcs, int32_t n_src, int64_t bytes, int32_t workgroups, int32_t reps,
                           double* us_per_launch, void* stream);
+/* The same `reps` launches back to back between one pair of fence-free events: the ceiling
+ * for pgr_kv_bench_attention's back-to-back launches. */
+int pgr_bench_stream_read_back_to_back(const void* const* srcs, int32_t n_src, int64_t bytes, int32_t workgroups,
+                                       int32_t reps, double* us_per_launch, void* stream);
 
 /* Fresh state for rows = B * Hq: m[r] = -inf, l[r] = 0, acc[r, :] = 0 (fp32, contiguous), in
  * one launch. Replaces streaming_attention_state_init, pager_hf/streaming_attention.py:444-449
@@ -372,6 +376,18 @@ int pgr_kv_block_bytes(void* kv, int32_t sid, int64_t* bytes);
  * milliseconds, the number of layer copy groups and their bytes, then forgets them. */
 int pgr_kv_set_timing(void* kv, int32_t on);
 int pgr_kv_kernel_time(void* kv, double* ms, int64_t* launches, int64_t* bytes);
+/* No counterpart in the reference. For measurement (direct mode): with a step open whose first
+ * layer has been decoded, launches the step's attention kernel (without per-block mass) for
+ * every layer, `reps` times, back to back between two fence-free events on `stream`, and
+ * returns the mean microseconds per launch and the K/V bytes each launch reads. Per-launch
+ * events (pgr_kv_set_timing) add the time between each start marker and its dispatch. The
+ * launches rewrite the step's split-K partials and each layer's current token: q, k_new and
+ * v_new hold num_layers device pointers, each layer's inputs of the step, as given to
+ * pgr_kv_decode_layer, with its scale and softcap. The merges are not repeated, so the step's
+ * outputs stay as decode_layer wrote them. Synchronous; not under graph capture. */
+int pgr_kv_bench_attention(void* kv, const void* const* q, const void* const* k_new, const void* const* v_new,
+                           float scale, float softcap, int32_t reps, double* us_per_launch, int64_t* bytes_per_launch,
+                           void* stream);
 int pgr_kv_copy_time(void* kv, double* ms, int64_t* copies, int64_t* bytes);
 /* Waits for all work of the store (both streams). */
 int pgr_kv_sync(void* kv);

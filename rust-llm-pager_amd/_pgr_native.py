@@ -133,6 +133,7 @@ SIGNATURES: dict[str, tuple] = {
          c_vp, c_size, c_vp],
     ),
     "pgr_bench_stream_read": (ctypes.c_int, [P(c_vp), c_i32, c_i64, c_i32, c_i32, P(c_f64), c_vp]),
+    "pgr_bench_stream_read_back_to_back": (ctypes.c_int, [P(c_vp), c_i32, c_i64, c_i32, c_i32, P(c_f64), c_vp]),
     "pgr_attn_set_timing": (ctypes.c_int, [c_i32]),
     "pgr_attn_kernel_time": (ctypes.c_int, [P(c_f64), P(c_i64), P(c_i64)]),
     "pgr_attn_state_init": (ctypes.c_int, [c_vp, c_vp, c_vp, c_i64, c_i64, c_vp]),
@@ -184,6 +185,8 @@ SIGNATURES: dict[str, tuple] = {
     "pgr_kv_block_bytes": (ctypes.c_int, [c_vp, c_i32, P(c_i64)]),
     "pgr_kv_set_timing": (ctypes.c_int, [c_vp, c_i32]),
     "pgr_kv_kernel_time": (ctypes.c_int, [c_vp, P(c_f64), P(c_i64), P(c_i64)]),
+    "pgr_kv_bench_attention": (ctypes.c_int, [c_vp, P(c_vp), P(c_vp), P(c_vp), c_f32, c_f32, c_i32, P(c_f64), P(c_i64),
+                                               c_vp]),
     "pgr_kv_copy_time": (ctypes.c_int, [c_vp, P(c_f64), P(c_i64), P(c_i64)]),
     "pgr_kv_sync": (ctypes.c_int, [c_vp]),
 }

@@ -898,6 +898,47 @@ int pgr_kv_kernel_time(void* kv, double* ms, int64_t* launches, int64_t* bytes) 
   }
 }
 
+int pgr_kv_bench_attention(void* kv, const void* const* q, const void* const* k_new, const void* const* v_new,
+                           float scale, float softcap, int32_t reps, double* us_per_launch, int64_t* bytes_per_launch,
+                           void* stream) {
+  try {
+    if (!kv || !q || !k_new || !v_new || !us_per_launch || !bytes_per_launch)
+      return set_err(pgr::kErrInvalid, "null pointer");
+    if (!(scale > 0.f) || !std::isfinite(scale)) return set_err(pgr::kErrInvalid, "scale must be positive and finite");
+    return kv_rc(kv_of(kv), kv_of(kv)->bench_attention(q, k_new, v_new, scale, softcap > 0.f ? softcap : 0.f, reps,
+                                                       as_stream(stream), us_per_launch, bytes_per_launch));
+  } catch (...) {
+    return exception_status();
+  }
+}
+
+int pgr_bench_stream_read_back_to_back(const void* const* srcs, int32_t n_src, int64_t bytes, int32_t workgroups,
+                                       int32_t reps, double* us_per_launch, void* stream) {
+  try {
+    if (!srcs || n_src <= 0 || reps <= 0 || !us_per_launch || bytes <= 0 || bytes % 16 != 0 || workgroups <= 0)
+      return set_err(pgr::kErrInvalid, "need buffers, reps > 0 and bytes a positive multiple of 16");
+    for (int i = 0; i < n_src; ++i)
+      if (!srcs[i] || ((uintptr_t)srcs[i]) % 16 != 0) return set_err(pgr::kErrInvalid, "buffers must be 16-byte aligned");
+    hipEvent_t ev[2] = {nullptr, nullptr};
+    hipError_t e = hipSuccess;
+    for (int i = 0; i < 2 && e == hipSuccess; ++i) e = hipEventCreateWithFlags(&ev[i], hipEventDisableSystemFence);
+    if (e == hipSuccess) e = hipEventRecord(ev[0], as_stream(stream));
+    for (int r = 0; r < reps && e == hipSuccess; ++r)
+      e = pgr::launch_stream_read(srcs[r % n_src], bytes, workgroups, as_stream(stream));
+    if (e == hipSuccess) e = hipEventRecord(ev[1], as_stream(stream));
+    float ms = 0.f;
+    if (e == hipSuccess) e = hipEventSynchronize(ev[1]);
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, ev[0], ev[1]);
+    for (hipEvent_t x : ev)
+      if (x) (void)hipEventDestroy(x);
+    if (e != hipSuccess) return hip_err(e, "stream read");
+    *us_per_launch = (double)ms * 1e3 / reps;
+    return pgr::kOk;
+  } catch (...) {
+    return exception_status();
+  }
+}
+
 int pgr_kv_copy_time(void* kv, double* ms, int64_t* copies, int64_t* bytes) {
   try {
     if (!kv || !ms || !copies || !bytes) return set_err(pgr::kErrInvalid, "null pointer");

@@ -1519,6 +1519,83 @@ bool PagedKV::wait_release(int layer, uint32_t token) {
   return ok;
 }
 
+void PagedKV::base_launch(PagedLaunch& pl, int layer, const void* q, const void* k_new, const void* v_new, void* out,
+                          bool mass, float scale, float softcap, int window) const {
+  pl.q = q;
+  pl.k_new = k_new;
+  pl.v_new = v_new;
+  pl.pool = pool_[layer];
+  pl.stage = cfg_.stream_mode == 1 ? stage_ : host_dev_[layer];
+  if (cfg_.stream_mode == 2) {
+    pl.mirror = ring_[layer % ring_.size()];
+    pl.mirror_flag = mirror_flags_ + layer;
+    pl.release_flag = mirror_release_dev_ + layer;
+  }
+  pl.seqs = d_seqs_;
+  pl.pm = d_pm_;
+  pl.pl = d_pl_;
+  pl.pacc = d_pacc_;
+  pl.mass_m = mass ? d_mass_m_ : nullptr;
+  pl.mass_s = mass ? d_mass_s_ : nullptr;
+  pl.out = out;
+  pl.mf = d_mf_;
+  pl.lf = d_lf_;
+  pl.hq = cfg_.query_heads;
+  pl.hkv = cfg_.kv_heads;
+  pl.tokens_per_block = cfg_.tokens_per_block;
+  pl.mass_stride = mass_stride_;
+  pl.partial_stride = partial_stride_;
+  pl.scale = scale;
+  pl.softcap = softcap;
+  pl.window = window;
+}
+
+// Measurement only. The attention launches of decode_layer for every layer, again, with the
+// plan already on the device (so every launch reads its work items from the workspace, as
+// the step's launches after its first do), reps times back to back between two fence-free
+// events: per-launch events add the time between each start marker and its dispatch, about
+// 1.6 us on a 13 us launch. The launches rewrite the step's partials and, in each layer, its
+// current token (the caller passes each layer's q, k_new and v_new of the step); the merges,
+// and so the step's outputs, are not repeated.
+int PagedKV::bench_attention(const void* const* q, const void* const* k_new, const void* const* v_new, float scale,
+                             float softcap, int reps, hipStream_t stream, double* us_per_launch,
+                             int64_t* bytes_per_launch) {
+  if (!in_step_ || !plan_on_device_)
+    return fail(kErrState, "bench_attention needs an open step whose first layer was decoded");
+  if (cfg_.stream_mode != 0) return fail(kErrUnsupported, "bench_attention runs in the direct stream mode only");
+  if (reps <= 0 || !q || !k_new || !v_new || !us_per_launch || !bytes_per_launch)
+    return fail(kErrInvalid, "bench_attention: reps > 0 and q, k_new, v_new and outputs required");
+  for (int layer = 0; layer < cfg_.num_layers; ++layer)
+    if (!q[layer] || !k_new[layer] || !v_new[layer]) return fail(kErrInvalid, "bench_attention: a null layer input");
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  PGR_HIP(hipStreamIsCapturing(stream, &cap));
+  if (cap != hipStreamCaptureStatusNone) return fail(kErrState, "bench_attention under stream capture");
+  int64_t ent = 0;
+  for (const WorkItem& w : work_) ent += w.entry_count;
+  hipEvent_t ev[2] = {nullptr, nullptr};
+  for (hipEvent_t& e : ev) PGR_HIP(hipEventCreateWithFlags(&e, hipEventDisableSystemFence));
+  hipError_t e = hipEventRecord(ev[0], stream);
+  int launches = 0;
+  for (int r = 0; r < reps && e == hipSuccess; ++r)
+    for (int layer = 0; layer < cfg_.num_layers && e == hipSuccess; ++layer) {
+      PagedLaunch pl{};
+      base_launch(pl, layer, q[layer], k_new[layer], v_new[layer], nullptr, false, scale, softcap, 0);
+      pl.work = d_work_;
+      pl.n_work = (int)work_.size();
+      e = launch_paged(cfg_.dtype, cfg_.head_dim, pl, stream);
+      ++launches;
+    }
+  if (e == hipSuccess) e = hipEventRecord(ev[1], stream);
+  float ms = 0.f;
+  if (e == hipSuccess) e = hipEventSynchronize(ev[1]);
+  if (e == hipSuccess) e = hipEventElapsedTime(&ms, ev[0], ev[1]);
+  for (hipEvent_t x : ev) (void)hipEventDestroy(x);
+  if (e != hipSuccess) return hip_fail(e, "bench_attention");
+  *us_per_launch = (double)ms * 1e3 / launches;
+  *bytes_per_launch = ent * (int64_t)cfg_.tokens_per_block * 2 * cfg_.head_dim * 2 * cfg_.kv_heads;
+  return kOk;
+}
+
 int PagedKV::decode_layer(int layer, const void* q, const void* k_new, const void* v_new, void* out,
                           float* mass_accum, int64_t accum_stride, float scale, float softcap, int window,
                           hipStream_t stream) {
@@ -1536,33 +1613,7 @@ int PagedKV::decode_layer(int layer, const void* q, const void* k_new, const voi
   const int T = cfg_.tokens_per_block;
   const size_t rec = rec_bytes();
   PagedLaunch pl{};
-  pl.q = q;
-  pl.k_new = k_new;
-  pl.v_new = v_new;
-  pl.pool = pool_[layer];
-  pl.stage = cfg_.stream_mode == 1 ? stage_ : host_dev_[layer];
-  if (cfg_.stream_mode == 2) {
-    pl.mirror = ring_[layer % ring_.size()];
-    pl.mirror_flag = mirror_flags_ + layer;
-    pl.release_flag = mirror_release_dev_ + layer;
-  }
-  pl.seqs = d_seqs_;
-  pl.pm = d_pm_;
-  pl.pl = d_pl_;
-  pl.pacc = d_pacc_;
-  pl.mass_m = mass_accum ? d_mass_m_ : nullptr;
-  pl.mass_s = mass_accum ? d_mass_s_ : nullptr;
-  pl.out = out;
-  pl.mf = d_mf_;
-  pl.lf = d_lf_;
-  pl.hq = hq;
-  pl.hkv = cfg_.kv_heads;
-  pl.tokens_per_block = T;
-  pl.mass_stride = mass_stride_;
-  pl.partial_stride = partial_stride_;
-  pl.scale = scale;
-  pl.softcap = softcap;
-  pl.window = window;
+  base_launch(pl, layer, q, k_new, v_new, out, mass_accum != nullptr, scale, softcap, window);
   const int n_launch = (int)launch_work_begin_.size();
   const int nbuf = cfg_.staging_buffers;
   // Side stream: wait until the previous reader of buffer `buf` finished, then stream the

@@ -43,6 +43,8 @@
 
 namespace pgr {
 
+struct PagedLaunch;
+
 class PlacementPager;
 
 struct PagedKVConfig {
@@ -208,6 +210,11 @@ class PagedKV {
   // Optional timing of the attention launches (HIP events on the compute stream).
   void set_timing(bool on) { timing_ = on; }
   int kernel_time(double* ms, int64_t* launches, int64_t* bytes);
+  // Measurement only: the open step's attention launches (no per-block mass) for every layer,
+  // reps times back to back between two fence-free events (direct mode, after the step's
+  // first decode_layer). See pgr_kv_bench_attention.
+  int bench_attention(const void* const* q, const void* const* k_new, const void* const* v_new, float scale,
+                      float softcap, int reps, hipStream_t stream, double* us_per_launch, int64_t* bytes_per_launch);
   // Mirror mode with timing on: the DMA copies of each layer's share, event-timed on the copy
   // stream. Waits for them; returns the summed milliseconds, the layer copy groups and bytes.
   int copy_time(double* ms, int64_t* copies, int64_t* bytes);
@@ -338,6 +345,10 @@ class PagedKV {
   hipEvent_t moves_done_ = nullptr;
   std::vector<hipStream_t> moves_waited_;
   int order_after_moves(hipStream_t stream);
+  // The launch arguments decode_layer and bench_attention share for `layer` (plan pointers and
+  // work items are set per launch).
+  void base_launch(PagedLaunch& pl, int layer, const void* q, const void* k_new, const void* v_new, void* out,
+                   bool mass, float scale, float softcap, int window) const;
   // The step's decode launches run on the stream decode_layer was given. Placement
   // (end_step_place, apply_tiers) on another stream reads the mass those launches write and
   // evicts records they append to, so it first waits for them: an event recorded on

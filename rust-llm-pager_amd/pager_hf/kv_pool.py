@@ -313,6 +313,25 @@ class NativeKVPool:
                                                   ctypes.byref(nbytes)), "kernel_time")
         return ms.value, launches.value, nbytes.value
 
+    def bench_attention(self, q, k_new, v_new, reps: int = 1, scale=None, softcap=None) -> tuple[float, int]:
+        """Measurement only: the open step's attention launches for every layer, `reps` times,
+        back to back between two events (pgr_kv_bench_attention). q, k_new and v_new are lists
+        with each layer's inputs of the step (the launches write each layer's current token
+        again). Returns (microseconds per launch, K/V bytes per launch)."""
+        if not (len(q) == len(k_new) == len(v_new) == self.num_layers):
+            raise ValueError(f"bench_attention needs {self.num_layers} q, k_new and v_new tensors (one per layer)")
+        if scale is None:
+            scale = 1.0 / (self.head_dim**0.5)
+
+        def ptrs(ts):
+            return (ctypes.c_void_p * len(ts))(*[t.data_ptr() for t in ts])
+
+        us, nbytes = ctypes.c_double(0), ctypes.c_int64(0)
+        self._call("bench_attention", self.lib.pgr_kv_bench_attention, ptrs(q), ptrs(k_new), ptrs(v_new),
+                   float(scale), float(softcap or 0.0), int(reps), ctypes.byref(us), ctypes.byref(nbytes),
+                   self._stream())
+        return us.value, nbytes.value
+
     def copy_time(self) -> tuple[float, int, int]:
         """(milliseconds, layer copy groups, bytes) of the mirror mode's DMA copies timed since the last call."""
         ms, n, nbytes = ctypes.c_double(0), ctypes.c_int64(0), ctypes.c_int64(0)

@@ -1,6 +1,8 @@
-"""Launch timing of the paged attention kernel (pgr_kv_set_timing / pgr_kv_kernel_time), which
-bench.py's roofline figure is built on: counts, bytes and durations over passes that reuse the
-store's timing events, and no effect on the decode results."""
+"""Launch timing of the paged attention kernel, which bench.py's roofline figures are built on:
+per-launch events (pgr_kv_set_timing / pgr_kv_kernel_time), counts, bytes and durations over
+passes that reuse the store's timing events; back-to-back launches of an open step
+(pgr_kv_bench_attention), bytes equal to the per-launch figure; neither changes the decode
+results of the step or of the steps after it."""
 import numpy as np
 import pytest
 import torch
@@ -53,4 +55,50 @@ def test_kernel_time_counts_and_bytes_over_reused_events():
             assert ms > 0.0 and ms / launches < 5.0, ms  # milliseconds per launch: microseconds here
     finally:
         dec.pool.set_timing(False)
+        dec.pool.close()
+
+
+@pytest.mark.gpu
+def test_back_to_back_attention_launches_keep_the_decode_intact():
+    layers, hq, hkv, d, T = 3, 14, 2, 64, 32
+    g = torch.Generator().manual_seed(12)
+    dec = PagedDecoder(num_layers=layers, num_query_heads=hq, num_kv_heads=hkv, head_dim=d, tokens_per_block=T,
+                       dtype=torch.float16, device="cuda:0", pool_blocks=64, host_blocks=64, staging_blocks=64)
+    ora = PagedDecodeOracle(num_layers=layers, num_query_heads=hq, num_kv_heads=hkv, head_dim=d, tokens_per_block=T)
+    kw = dict(vram_budget=4 * MIB16, ram_budget=64 * MIB16, recent_window=3, policy="recent_only")
+    n = 310  # the open block fills during the steps: appends land in a new block too
+    sid = dec.add_session(capacity_tokens=n + 64, **kw)
+    ora.add_session(sid, **kw)
+    ks = [(torch.randn(1, hkv, n, d, generator=g) * 0.5).half() for _ in range(layers)]
+    vs = [(torch.randn(1, hkv, n, d, generator=g) * 0.5).half() for _ in range(layers)]
+    dec.prefill(sid, [k.cuda() for k in ks], [v.cuda() for v in vs], n)
+    ora.prefill(sid, [k.float().numpy() for k in ks], [v.float().numpy() for v in vs], n)
+    try:
+        for step in range(14):
+            q = [(torch.randn(1, hq, d, generator=g) * 0.5).half() for _ in range(layers)]
+            kn = [(torch.randn(1, hkv, d, generator=g) * 0.5).half() for _ in range(layers)]
+            vn = [(torch.randn(1, hkv, d, generator=g) * 0.5).half() for _ in range(layers)]
+            qd, knd, vnd = [x.cuda() for x in q], [x.cuda() for x in kn], [x.cuda() for x in vn]
+            dec.begin_step([sid])
+            if step == 0:
+                with pytest.raises(RuntimeError):  # the plan is not on the device before a layer runs
+                    dec.pool.bench_attention(qd, knd, vnd)
+            dec.pool.kernel_time()
+            dec.pool.set_timing(True)
+            outs = [dec.decode_layer(l, qd[l], knd[l], vnd[l]) for l in range(layers)]
+            dec.pool.set_timing(False)
+            us, nbytes = dec.pool.bench_attention(qd, knd, vnd, reps=2)
+            torch.cuda.synchronize()
+            _, launches, per_bytes = dec.pool.kernel_time()
+            assert nbytes == per_bytes // launches and nbytes > 0
+            assert 0.0 < us < 5000.0
+            outs = [o.float().cpu().numpy() for o in outs]
+            dec.end_step()
+            ref = ora.step([sid], [x.float().numpy() for x in q], [x.float().numpy() for x in kn],
+                           [x.float().numpy() for x in vn])
+            for l in range(layers):
+                assert float(np.abs(outs[l] - ref["out"][l]).max()) < 2e-3, (step, l)
+        with pytest.raises(ValueError):
+            dec.pool.bench_attention(qd[:1], knd[:1], vnd[:1])
+    finally:
         dec.pool.close()
