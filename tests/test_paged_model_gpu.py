@@ -15,14 +15,14 @@ pytestmark = pytest.mark.gpu
 MIB16 = 16 * 1024 * 1024
 
 
-def _model(cfg_kwargs, seed, init_std=None):
+def _model(cfg_kwargs, seed, init_std=None, dtype=torch.float16):
     from transformers import LlamaConfig, LlamaForCausalLM
 
     cfg = LlamaConfig(**cfg_kwargs)
     if init_std is not None:
         cfg.initializer_range = init_std
     torch.manual_seed(seed)
-    m = LlamaForCausalLM(cfg).to(dtype=torch.float16, device="cuda").eval()
+    m = LlamaForCausalLM(cfg).to(dtype=dtype, device="cuda").eval()
     return m
 
 
@@ -49,9 +49,9 @@ def _baseline(model, input_ids, attention_mask, max_new_tokens):
     return tokens, logits, gaps
 
 
-def _teacher_forced(pm, input_ids, attention_mask, tokens, logits, gaps):
+def _teacher_forced(pm, input_ids, attention_mask, tokens, logits, gaps, tie=TIE):
     """Feed the baseline's own tokens through the paged path; returns the largest logit
-    difference. Where the baseline is decisive (gap > TIE) the argmax must agree."""
+    difference. Where the baseline is decisive (gap > tie) the argmax must agree."""
     pm._start_session(input_ids, attention_mask, len(tokens[0]))
     nxt, cur = input_ids[:, -1:], attention_mask
     worst = 0.0
@@ -61,7 +61,7 @@ def _teacher_forced(pm, input_ids, attention_mask, tokens, logits, gaps):
             worst = max(worst, (got.float() - logits[i]).abs().max().item())
             mine = torch.argmax(got, dim=-1).tolist()
             for r in range(len(tokens)):
-                if gaps[i][r] > TIE:
+                if gaps[i][r] > tie:
                     assert mine[r] == tokens[r][i], f"row {r} step {i}: decisive step (gap {gaps[i][r]:.3g}) differs"
             nxt = torch.tensor([[t[i]] for t in tokens], device=input_ids.device)
             cur = torch.cat([cur, torch.ones_like(cur[:, :1])], dim=1)
@@ -69,12 +69,12 @@ def _teacher_forced(pm, input_ids, attention_mask, tokens, logits, gaps):
     return worst
 
 
-def _check_free_running(got_rows, tokens, gaps):
+def _check_free_running(got_rows, tokens, gaps, tie=TIE):
     """Identical tokens up to the first step; a first difference only at a baseline near-tie."""
     for r, (got, want) in enumerate(zip(got_rows, tokens)):
         first = next((i for i, (a, b) in enumerate(zip(got, want)) if a != b), None)
         if first is not None:
-            assert gaps[first][r] < TIE, f"row {r}: first difference at step {first}, baseline gap {gaps[first][r]:.3g}"
+            assert gaps[first][r] < tie, f"row {r}: first difference at step {first}, baseline gap {gaps[first][r]:.3g}"
 
 
 SMALL = dict(hidden_size=512, intermediate_size=1024, num_hidden_layers=4, num_attention_heads=8,
@@ -100,6 +100,30 @@ def test_small_llama_greedy_matches_unpaged(policy, mode):
     assert st.final_num_blocks == (600 + 48 - 1) // 16
     assert st.total_cpu_to_gpu_mb > 0  # host blocks were read over the link
     assert 0.0 <= st.min_attention_in_gpu <= st.max_attention_in_gpu <= 1.0 + 1e-5
+
+
+@pytest.mark.parametrize("policy,mode", [("sinks_heavy_hitter", "direct"), ("recent_only", "staged")])
+def test_small_llama_bf16_greedy_matches_unpaged(policy, mode):
+    """The same small Llama in bfloat16 (configuration 5's dtype). The paged path rounds P to
+    bf16 before P.V, as the reference's kernel does, and HF's attention rounds its own way, so
+    logits agree to bf16's resolution rather than fp16's: a near-tie is a gap below 8 bf16
+    ulps at the logits' magnitude (8 x 2^-8 x 4 = 0.125), and the teacher-forced logits stay
+    within twice that."""
+    from pager_hf import PagedModel
+
+    model = _model(SMALL, seed=11, init_std=0.05, dtype=torch.bfloat16)
+    g = torch.Generator().manual_seed(5)
+    ids = torch.randint(0, SMALL["vocab_size"], (1, 600), generator=g).cuda()
+    mask = torch.ones_like(ids)
+    want, logits, gaps = _baseline(model, ids, mask, 48)
+    pm = PagedModel(model, vram_budget=6 * MIB16, ram_budget=1 << 40, recent_window=4, rebalance_interval=4,
+                    policy=policy, tokens_per_block=16, stream_mode=mode)
+    worst = _teacher_forced(pm, ids, mask, want, logits, gaps, tie=0.125)
+    print(f"bf16 teacher-forced worst logit difference {worst:.4f}", flush=True)
+    assert worst < 0.25
+    got = pm.generate(ids, mask, 48)
+    _check_free_running([got], want, gaps, tie=0.125)
+    assert pm.last_run_stats.total_cpu_to_gpu_mb > 0
 
 
 def test_batch_of_two_with_left_padding():
