@@ -102,7 +102,8 @@ def test_small_llama_greedy_matches_unpaged(policy, mode):
     assert 0.0 <= st.min_attention_in_gpu <= st.max_attention_in_gpu <= 1.0 + 1e-5
 
 
-@pytest.mark.parametrize("policy,mode", [("sinks_heavy_hitter", "direct"), ("recent_only", "staged")])
+@pytest.mark.parametrize("policy,mode", [("sinks_heavy_hitter", "direct"), ("recent_only", "staged"),
+                                         ("heavy_hitter", "mirror")])
 def test_small_llama_bf16_greedy_matches_unpaged(policy, mode):
     """The same small Llama in bfloat16 (configuration 5's dtype). The paged path rounds P to
     bf16 before P.V, as the reference's kernel does, and HF's attention rounds its own way, so
