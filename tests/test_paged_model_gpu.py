@@ -127,7 +127,8 @@ def test_small_llama_bf16_greedy_matches_unpaged(policy, mode):
     assert pm.last_run_stats.total_cpu_to_gpu_mb > 0
 
 
-def test_batch_of_two_with_left_padding():
+@pytest.mark.parametrize("mode", ["direct", "staged", "mirror"])
+def test_batch_of_two_with_left_padding(mode):
     from pager_hf import PagedModel
 
     model = _model(SMALL, seed=12, init_std=0.05)
@@ -138,13 +139,14 @@ def test_batch_of_two_with_left_padding():
     mask[1, :57] = 0
     want, logits, gaps = _baseline(model, ids, mask, 32)
     pm = PagedModel(model, vram_budget=5 * MIB16, ram_budget=1 << 40, recent_window=3, policy="sinks_heavy_hitter",
-                    tokens_per_block=16)
+                    tokens_per_block=16, stream_mode=mode)
     assert _teacher_forced(pm, ids, mask, want, logits, gaps) < LOGIT_TOL
     got = pm.generate(ids, mask, 32)
     _check_free_running(got, want, gaps)
 
 
-def test_session_continues_across_generate_calls():
+@pytest.mark.parametrize("mode", ["direct", "mirror"])
+def test_session_continues_across_generate_calls(mode):
     from pager_hf import PagedModel
 
     model = _model(SMALL, seed=13, init_std=0.05)
@@ -153,7 +155,7 @@ def test_session_continues_across_generate_calls():
     mask = torch.ones_like(ids)
     want, logits, gaps = _baseline(model, ids, mask, 40)
     pm = PagedModel(model, vram_budget=4 * MIB16, ram_budget=1 << 40, recent_window=2, policy="sinks_heavy_hitter",
-                    tokens_per_block=16, max_context_tokens=512)
+                    tokens_per_block=16, max_context_tokens=512, stream_mode=mode)
     one_shot = pm.generate(ids, mask, 40)
     pm.reset()
     first = pm.generate(ids, mask, 25)
