@@ -162,7 +162,7 @@ def hbm_all_resident(layers, steps, warmup, target_wg=0, blocks_per_wg=32):
     dec.pool.sync()
     k_ms, k_launches, k_bytes = dec.pool.kernel_time()
     dec.pool.set_timing(False)
-    # Pass 3: the same launches back to back, one pair of events around each step's 24
+    # Pass 3: the same launches back to back, one pair of events around each step's launches
     # (pgr_kv_bench_attention, after the step's own layers; every launch reads its work items
     # from the device copy of the plan, as the step's launches after its first do).
     b2b_us = b2b_bytes = 0.0
@@ -205,8 +205,8 @@ def hbm_all_resident(layers, steps, warmup, target_wg=0, blocks_per_wg=32):
                                 "avg_launch_us": round(b2b_us, 3), "bytes_per_launch": b2b_bytes,
                                 "achieved": round(b2b_bytes / b2b_us / 1e3, 2),
                                 "frac": round(b2b_bytes / b2b_us / 1e3 / HBM_PEAK_GBS, 4),
-                                "timing": "each step's attention launches again, the 24 back to back between one "
-                                          "pair of fence-free events (plan on the device)"},
+                                "timing": f"each step's attention launches again, the {layers} back to back between "
+                                          "one pair of fence-free events (plan on the device)"},
         "step": {"achieved": round(step_gbs, 2), "frac": round(step_gbs / HBM_PEAK_GBS, 4),
                  "note": "whole decode step per layer (planning, both kernels, host glue) over K/V bytes, "
                          "GPU time between stream events around the steps (ms_per_step)"},
