@@ -1022,20 +1022,39 @@ def operator_api(dtype_name="float16"):
         nat.check(lib.pgr_attn_set_timing(0), "pgr_attn_set_timing")
         fold_us = fold_ms.value * 1e3 / max(fold_n.value, 1)
         fold_gbs = fold_bytes.value / max(fold_n.value, 1) / (fold_us * 1e3)
-        del chunks
+        # The same fold launches back to back over the chunk copies, without the merges, at
+        # least 20 of them between one pair of events (pgr_attn_bench_step), queued behind a
+        # spin kernel so that the host has queued them when the GPU reaches the first.
+        m, l, acc = streaming_attention_state_init(1, hq, d, q.device)
+        ws_bytes = lib.pgr_attn_workspace_bytes(1, hq, hkv, tokens, d, nat.MODE_FOLD, 16)
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
+        karr = (ctypes.c_void_p * n_copy)(*[kc.data_ptr() for kc, _ in chunks])
+        varr = (ctypes.c_void_p * n_copy)(*[vc.data_ptr() for _, vc in chunks])
+        b2b_us, b2b_bytes = ctypes.c_double(0), ctypes.c_int64(0)
+        code = {torch.float16: nat.DTYPE_F16, torch.bfloat16: nat.DTYPE_BF16}[q.dtype]
+        torch.cuda._sleep(TIMING_SPIN_CYCLES)
+        nat.check(lib.pgr_attn_bench_step(q.data_ptr(), karr, varr, n_copy, m.data_ptr(), l.data_ptr(), acc.data_ptr(),
+                                          1, hq, hkv, tokens, d, code, 1.0 / d**0.5, ws.data_ptr(), ws_bytes,
+                                          max(3, -(-20 // n_copy)), ctypes.byref(b2b_us), ctypes.byref(b2b_bytes),
+                                          torch.cuda.current_stream().cuda_stream), "pgr_attn_bench_step")
+        b2b_gbs = b2b_bytes.value / (b2b_us.value * 1e3)
+        del chunks, ws
         kv = 2 * hkv * tokens * d * k.element_size()
         rows.append({"tokens": tokens, "ms_per_call": round(ms, 4), "torch_eager_ms": round(ms_eager, 4),
                      "ms_per_call_graph": round(ms_graph, 4), "kv_GBs_graph": round(kv / ms_graph / 1e6, 1),
                      "hbm_frac_graph": round(kv / ms_graph / 1e6 / HBM_PEAK_GBS, 4),
                      "fold_us": round(fold_us, 3), "fold_GBs": round(fold_gbs, 1),
-                     "fold_frac": round(fold_gbs / HBM_PEAK_GBS, 4)})
+                     "fold_frac": round(fold_gbs / HBM_PEAK_GBS, 4),
+                     "fold_us_back_to_back": round(b2b_us.value, 3), "fold_GBs_back_to_back": round(b2b_gbs, 1),
+                     "fold_frac_back_to_back": round(b2b_gbs / HBM_PEAK_GBS, 4)})
     return {
         "workload": "operator API, Qwen2.5-7B shape (28q/4kv, D 128), batch 1, one contiguous chunk per call; "
                     "state_init + step + finalize per call, 20 calls between two events (ms_per_call: eager calls, "
                     "as the reference's probe times them; ms_per_call_graph: replays of the call captured in a HIP "
                     "graph; fold_us / fold_frac: the attention kernel alone, events around each launch, its K+V "
                     "bytes over 8 TB/s, timed calls rotating over chunk copies beyond the MALL and queued behind a "
-                    "spin kernel so that the events hold GPU time only)",
+                    "spin kernel so that the events hold GPU time only; fold_*_back_to_back: the same launches over "
+                    "the same copies back to back between one pair of events)",
         "dtype": dtype_name, "rows": rows,
     }
 

@@ -1688,6 +1688,7 @@ hipError_t launch_dense(int dtype, int mode, int d, const DenseLaunch& p, hipStr
                       : launch_dense_ty<BF16>(a, mode, p.batch, d, stream);
   if (e != hipSuccess) return e;
   if (p.ev_stop != nullptr && (e = hipEventRecord(p.ev_stop, stream)) != hipSuccess) return e;
+  if (p.attention_only) return hipSuccess;
   return launch_dense_merge(a, mode, p.batch, d, p.m, p.l, p.acc, stream);
 }
 

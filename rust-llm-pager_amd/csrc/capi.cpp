@@ -100,24 +100,11 @@ hipError_t timing_event(hipEvent_t* ev) {
   return hipEventCreateWithFlags(ev, hipEventDisableSystemFence);
 }
 
-int run_dense(int mode, const void* q, const void* k, const void* v, const int32_t* valid, const int32_t* active,
-              float* m, float* l, float* acc, float* block_mass, int64_t max_blocks, int64_t block_id_offset,
-              int64_t tpb, int64_t batch, int64_t hq, int64_t hkv, int64_t tokens, int64_t d, int dtype, float scale,
-              float softcap, void* ws, size_t ws_bytes, void* stream) {
-  int rc = check_dense(batch, hq, hkv, tokens, d, dtype, scale);
-  if (rc != pgr::kOk) return rc;
-  if (mode == PGR_MODE_ACCUMULATE) {
-    if (tpb <= 0 || tpb % 16 != 0) return set_err(pgr::kErrUnsupported, "tokens_per_block must be a multiple of 16");
-    const int64_t nb = (tokens + tpb - 1) / tpb;
-    if (block_id_offset < 0 || block_id_offset + nb > max_blocks)
-      return set_err(pgr::kErrInvalid, "block_mass is too small for block_id_offset + this chunk's blocks");
-    if (block_mass == nullptr) return set_err(pgr::kErrInvalid, "block_mass is null");
-  }
-  if (tokens == 0 || batch == 0) return pgr::kOk;  // nothing to fold: the state is unchanged
-  if (!q || !k || !m || !l || (mode != PGR_MODE_STATS && (!v || !acc)))
-    return set_err(pgr::kErrInvalid, "null tensor pointer");
-  const DensePlan p = plan_dense(batch, hq, hkv, tokens, d, mode, tpb, dtype);
-  if (ws == nullptr || ws_bytes < p.bytes) return set_err(pgr::kErrCapacity, "workspace too small");
+// The launch arguments of one operator call over its plan and workspace.
+pgr::DenseLaunch dense_launch(const DensePlan& p, const void* q, const void* k, const void* v, const int32_t* valid,
+                              const int32_t* active, float* m, float* l, float* acc, float* block_mass,
+                              int64_t max_blocks, int64_t block_id_offset, int64_t tpb, int64_t batch, int64_t hq,
+                              int64_t hkv, int64_t tokens, float scale, float softcap, void* ws) {
   char* w = static_cast<char*>(ws);
   pgr::DenseLaunch L{};
   L.q = q;
@@ -143,6 +130,29 @@ int run_dense(int mode, const void* q, const void* k, const void* v, const int32
   L.block_id_offset = (int)block_id_offset;
   L.scale = scale;
   L.softcap = softcap > 0.f ? softcap : 0.f;
+  return L;
+}
+
+int run_dense(int mode, const void* q, const void* k, const void* v, const int32_t* valid, const int32_t* active,
+              float* m, float* l, float* acc, float* block_mass, int64_t max_blocks, int64_t block_id_offset,
+              int64_t tpb, int64_t batch, int64_t hq, int64_t hkv, int64_t tokens, int64_t d, int dtype, float scale,
+              float softcap, void* ws, size_t ws_bytes, void* stream) {
+  int rc = check_dense(batch, hq, hkv, tokens, d, dtype, scale);
+  if (rc != pgr::kOk) return rc;
+  if (mode == PGR_MODE_ACCUMULATE) {
+    if (tpb <= 0 || tpb % 16 != 0) return set_err(pgr::kErrUnsupported, "tokens_per_block must be a multiple of 16");
+    const int64_t nb = (tokens + tpb - 1) / tpb;
+    if (block_id_offset < 0 || block_id_offset + nb > max_blocks)
+      return set_err(pgr::kErrInvalid, "block_mass is too small for block_id_offset + this chunk's blocks");
+    if (block_mass == nullptr) return set_err(pgr::kErrInvalid, "block_mass is null");
+  }
+  if (tokens == 0 || batch == 0) return pgr::kOk;  // nothing to fold: the state is unchanged
+  if (!q || !k || !m || !l || (mode != PGR_MODE_STATS && (!v || !acc)))
+    return set_err(pgr::kErrInvalid, "null tensor pointer");
+  const DensePlan p = plan_dense(batch, hq, hkv, tokens, d, mode, tpb, dtype);
+  if (ws == nullptr || ws_bytes < p.bytes) return set_err(pgr::kErrCapacity, "workspace too small");
+  pgr::DenseLaunch L = dense_launch(p, q, k, v, valid, active, m, l, acc, block_mass, max_blocks, block_id_offset, tpb,
+                                    batch, hq, hkv, tokens, scale, softcap, ws);
   std::unique_lock<std::mutex> lk(g_timing_mu);
   const bool timed = g_timing_on;
   if (timed) {
@@ -265,6 +275,47 @@ int pgr_attn_step(const void* q, const void* k, const void* v, const int32_t* va
   try {
     return run_dense(PGR_MODE_FOLD, q, k, v, valid, active, m, l, acc, nullptr, 0, 0, 16, batch, num_query_heads,
                      num_kv_heads, tokens, head_dim, dtype, scale, softcap, workspace, workspace_bytes, stream);
+  } catch (...) {
+    return exception_status();
+  }
+}
+
+int pgr_attn_bench_step(const void* q, const void* const* k, const void* const* v, int32_t n_chunks, float* m, float* l,
+                        float* acc, int64_t batch, int64_t num_query_heads, int64_t num_kv_heads, int64_t tokens,
+                        int64_t head_dim, int dtype, float scale, void* workspace, size_t workspace_bytes,
+                        int32_t reps, double* us_per_launch, int64_t* bytes_per_launch, void* stream) {
+  try {
+    int rc = check_dense(batch, num_query_heads, num_kv_heads, tokens, head_dim, dtype, scale);
+    if (rc != pgr::kOk) return rc;
+    if (!q || !k || !v || !m || !l || !acc || n_chunks <= 0 || reps <= 0 || !us_per_launch || !bytes_per_launch ||
+        tokens <= 0 || batch <= 0)
+      return set_err(pgr::kErrInvalid, "pgr_attn_bench_step: inputs, chunks > 0, reps > 0 and outputs required");
+    for (int c = 0; c < n_chunks; ++c)
+      if (!k[c] || !v[c]) return set_err(pgr::kErrInvalid, "pgr_attn_bench_step: a null chunk");
+    const DensePlan p = plan_dense(batch, num_query_heads, num_kv_heads, tokens, head_dim, PGR_MODE_FOLD, 16, dtype);
+    if (workspace == nullptr || workspace_bytes < p.bytes) return set_err(pgr::kErrCapacity, "workspace too small");
+    hipEvent_t ev[2] = {nullptr, nullptr};
+    hipError_t e = hipSuccess;
+    for (int i = 0; i < 2 && e == hipSuccess; ++i) e = hipEventCreateWithFlags(&ev[i], hipEventDisableSystemFence);
+    if (e == hipSuccess) e = hipEventRecord(ev[0], as_stream(stream));
+    for (int r = 0; r < reps && e == hipSuccess; ++r)
+      for (int c = 0; c < n_chunks && e == hipSuccess; ++c) {
+        pgr::DenseLaunch L = dense_launch(p, q, k[c], v[c], nullptr, nullptr, m, l, acc, nullptr, 0, 0, 16, batch,
+                                          num_query_heads, num_kv_heads, tokens, scale, 0.f, workspace);
+        L.attention_only = true;
+        e = pgr::launch_dense(dtype, PGR_MODE_FOLD, (int)head_dim, L, as_stream(stream));
+      }
+    if (e == hipSuccess) e = hipEventRecord(ev[1], as_stream(stream));
+    float ms = 0.f;
+    if (e == hipSuccess) e = hipEventSynchronize(ev[1]);
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, ev[0], ev[1]);
+    for (hipEvent_t x : ev)
+      if (x) (void)hipEventDestroy(x);
+    if (e != hipSuccess) return hip_err(e, "pgr_attn_bench_step");
+    *us_per_launch = (double)ms * 1e3 / ((double)reps * n_chunks);
+    const int64_t elem = dtype == pgr::kF32 ? 4 : 2;
+    *bytes_per_launch = batch * num_kv_heads * tokens * head_dim * elem * 2;
+    return pgr::kOk;
   } catch (...) {
     return exception_status();
   }

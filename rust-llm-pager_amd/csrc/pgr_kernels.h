@@ -46,6 +46,8 @@ struct DenseLaunch {
   // merge): the fold kernel's own duration for measurement.
   hipEvent_t ev_start = nullptr;
   hipEvent_t ev_stop = nullptr;
+  // Measurement only: launch the attention kernel and not the merge (m, l, acc untouched).
+  bool attention_only = false;
 };
 
 // The paged decode kernels of one layer. launch_paged folds work items [work, work + n_work)
