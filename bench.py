@@ -1025,7 +1025,6 @@ def operator_api(dtype_name="float16"):
         # The same fold launches back to back over the chunk copies, without the merges, at
         # least 20 of them between one pair of events (pgr_attn_bench_step), queued behind a
         # spin kernel so that the host has queued them when the GPU reaches the first.
-        m, l, acc = streaming_attention_state_init(1, hq, d, q.device)
         ws_bytes = lib.pgr_attn_workspace_bytes(1, hq, hkv, tokens, d, nat.MODE_FOLD, 16)
         ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
         karr = (ctypes.c_void_p * n_copy)(*[kc.data_ptr() for kc, _ in chunks])
@@ -1033,8 +1032,8 @@ def operator_api(dtype_name="float16"):
         b2b_us, b2b_bytes = ctypes.c_double(0), ctypes.c_int64(0)
         code = {torch.float16: nat.DTYPE_F16, torch.bfloat16: nat.DTYPE_BF16}[q.dtype]
         torch.cuda._sleep(TIMING_SPIN_CYCLES)
-        nat.check(lib.pgr_attn_bench_step(q.data_ptr(), karr, varr, n_copy, m.data_ptr(), l.data_ptr(), acc.data_ptr(),
-                                          1, hq, hkv, tokens, d, code, 1.0 / d**0.5, ws.data_ptr(), ws_bytes,
+        nat.check(lib.pgr_attn_bench_step(q.data_ptr(), karr, varr, n_copy, 1, hq, hkv, tokens, d, code, 1.0 / d**0.5,
+                                          ws.data_ptr(), ws_bytes,
                                           max(3, -(-20 // n_copy)), ctypes.byref(b2b_us), ctypes.byref(b2b_bytes),
                                           torch.cuda.current_stream().cuda_stream), "pgr_attn_bench_step")
         b2b_gbs = b2b_bytes.value / (b2b_us.value * 1e3)

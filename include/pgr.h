@@ -122,14 +122,15 @@ int pgr_attn_set_timing(int32_t on);
 int pgr_attn_kernel_time(double* ms, int64_t* launches, int64_t* bytes);
 /* No counterpart in the reference. For measurement: the attention (fold) launch of
  * pgr_attn_step, without its merge, over each of n_chunks chunks (k[c], v[c], all of one
- * shape, no masks), `reps` rounds, back to back between one pair of fence-free events on
- * `stream`; returns the mean microseconds per launch and the K/V bytes each launch reads.
- * m, l and acc are not modified (they size the launch like pgr_attn_step's); the workspace
- * is pgr_attn_step's. Synchronous; not under graph capture. */
-int pgr_attn_bench_step(const void* q, const void* const* k, const void* const* v, int32_t n_chunks, float* m, float* l,
-                        float* acc, int64_t batch, int64_t num_query_heads, int64_t num_kv_heads, int64_t tokens,
-                        int64_t head_dim, int dtype, float scale, void* workspace, size_t workspace_bytes,
-                        int32_t reps, double* us_per_launch, int64_t* bytes_per_launch, void* stream);
+ * shape, no masks, no running state: the merge is what reads and updates it), `reps` rounds,
+ * back to back between one pair of fence-free events on `stream`; returns the mean
+ * microseconds per launch and the K/V bytes each launch reads. The workspace is
+ * pgr_attn_step's (pgr_attn_workspace_bytes, fold mode). Synchronous; not under graph
+ * capture. */
+int pgr_attn_bench_step(const void* q, const void* const* k, const void* const* v, int32_t n_chunks, int64_t batch,
+                        int64_t num_query_heads, int64_t num_kv_heads, int64_t tokens, int64_t head_dim, int dtype,
+                        float scale, void* workspace, size_t workspace_bytes, int32_t reps, double* us_per_launch,
+                        int64_t* bytes_per_launch, void* stream);
 
 /* No counterpart in the reference. For measurement: `reps` launches of a plain streaming read
  * of `bytes` (a positive multiple of 16) by workgroups x 256 threads, nothing written, launch r

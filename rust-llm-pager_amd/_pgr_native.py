@@ -134,8 +134,8 @@ SIGNATURES: dict[str, tuple] = {
     ),
     "pgr_bench_stream_read": (ctypes.c_int, [P(c_vp), c_i32, c_i64, c_i32, c_i32, P(c_f64), c_vp]),
     "pgr_bench_stream_read_back_to_back": (ctypes.c_int, [P(c_vp), c_i32, c_i64, c_i32, c_i32, P(c_f64), c_vp]),
-    "pgr_attn_bench_step": (ctypes.c_int, [c_vp, P(c_vp), P(c_vp), c_i32, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_i64,
-                                            c_i64, ctypes.c_int, c_f32, c_vp, c_size, c_i32, P(c_f64), P(c_i64), c_vp]),
+    "pgr_attn_bench_step": (ctypes.c_int, [c_vp, P(c_vp), P(c_vp), c_i32, c_i64, c_i64, c_i64, c_i64, c_i64,
+                                            ctypes.c_int, c_f32, c_vp, c_size, c_i32, P(c_f64), P(c_i64), c_vp]),
     "pgr_attn_set_timing": (ctypes.c_int, [c_i32]),
     "pgr_attn_kernel_time": (ctypes.c_int, [P(c_f64), P(c_i64), P(c_i64)]),
     "pgr_attn_state_init": (ctypes.c_int, [c_vp, c_vp, c_vp, c_i64, c_i64, c_vp]),

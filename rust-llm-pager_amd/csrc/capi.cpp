@@ -280,15 +280,15 @@ int pgr_attn_step(const void* q, const void* k, const void* v, const int32_t* va
   }
 }
 
-int pgr_attn_bench_step(const void* q, const void* const* k, const void* const* v, int32_t n_chunks, float* m, float* l,
-                        float* acc, int64_t batch, int64_t num_query_heads, int64_t num_kv_heads, int64_t tokens,
-                        int64_t head_dim, int dtype, float scale, void* workspace, size_t workspace_bytes,
-                        int32_t reps, double* us_per_launch, int64_t* bytes_per_launch, void* stream) {
+int pgr_attn_bench_step(const void* q, const void* const* k, const void* const* v, int32_t n_chunks, int64_t batch,
+                        int64_t num_query_heads, int64_t num_kv_heads, int64_t tokens, int64_t head_dim, int dtype,
+                        float scale, void* workspace, size_t workspace_bytes, int32_t reps, double* us_per_launch,
+                        int64_t* bytes_per_launch, void* stream) {
   try {
     int rc = check_dense(batch, num_query_heads, num_kv_heads, tokens, head_dim, dtype, scale);
     if (rc != pgr::kOk) return rc;
-    if (!q || !k || !v || !m || !l || !acc || n_chunks <= 0 || reps <= 0 || !us_per_launch || !bytes_per_launch ||
-        tokens <= 0 || batch <= 0)
+    if (!q || !k || !v || n_chunks <= 0 || reps <= 0 || !us_per_launch || !bytes_per_launch || tokens <= 0 ||
+        batch <= 0)
       return set_err(pgr::kErrInvalid, "pgr_attn_bench_step: inputs, chunks > 0, reps > 0 and outputs required");
     for (int c = 0; c < n_chunks; ++c)
       if (!k[c] || !v[c]) return set_err(pgr::kErrInvalid, "pgr_attn_bench_step: a null chunk");
@@ -300,8 +300,9 @@ int pgr_attn_bench_step(const void* q, const void* const* k, const void* const* 
     if (e == hipSuccess) e = hipEventRecord(ev[0], as_stream(stream));
     for (int r = 0; r < reps && e == hipSuccess; ++r)
       for (int c = 0; c < n_chunks && e == hipSuccess; ++c) {
-        pgr::DenseLaunch L = dense_launch(p, q, k[c], v[c], nullptr, nullptr, m, l, acc, nullptr, 0, 0, 16, batch,
-                                          num_query_heads, num_kv_heads, tokens, scale, 0.f, workspace);
+        // The fold launch reads no running state (only the merge does), so none is passed.
+        pgr::DenseLaunch L = dense_launch(p, q, k[c], v[c], nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 0, 0,
+                                          16, batch, num_query_heads, num_kv_heads, tokens, scale, 0.f, workspace);
         L.attention_only = true;
         e = pgr::launch_dense(dtype, PGR_MODE_FOLD, (int)head_dim, L, as_stream(stream));
       }
